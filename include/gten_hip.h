@@ -1,0 +1,202 @@
+/*
+ * gten_hip.h -- C-ABI of the MI355X (gfx950) decode path of nanochatllms.cpp.
+ *
+ * The reference has no FFI layer: its operator API is the C++ free functions
+ * of gten::ops (src/gten/ops.h:10-40) over gten::Tensor (src/gten/tensor.h),
+ * driven by the model classes' logits() (src/gten/abc.h:12-28).  Each entry
+ * point below names the reference interface it replaces.  All compute calls
+ * are asynchronous on `stream` (a hipStream_t; NULL = the library's stream)
+ * and return NC_OK or a negative status; nc_last_error() describes the last
+ * failure.  Device pointers are plain HBM addresses; no torch types.
+ *
+ * Layouts (also in nanochatllms.cpp_amd/csrc/nc_layout.h):
+ *   activation row, dtype Q8 : [nb*32 int8 codes][nb fp16 deltas][pad to 16 B]
+ *   activation row, dtype F16: [cols fp16][pad], F32: [cols fp32][pad]
+ *   weights Q4/Q8: codes + separate fp16 delta array, lane-permuted per block;
+ *   weights F16: 64-column groups interleaved over 8-row groups.
+ * nc_act_from_reference / nc_weight_from_reference convert from the
+ * reference's byte layouts (34-byte Q8 blocks, 18-byte Q4 blocks).
+ */
+#ifndef GTEN_HIP_H
+#define GTEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NC_OK 0
+#define NC_ERR_ARG (-1)
+#define NC_ERR_HIP (-2)
+#define NC_ERR_NOMEM (-3)
+#define NC_ERR_STATE (-4)
+
+/* Dtypes, numbered as gten::Dtype (src/gten/gten_types.h:20-26). */
+#define NC_I32 0
+#define NC_F16 1
+#define NC_F32 2
+#define NC_Q8 3
+#define NC_Q4 4
+
+/* A device tensor: `rows` x `cols` values.  Activations: `data` holds rows of
+ * `pitch` bytes (deltas inside each Q8 row, `deltas` unused).  Weights: `data`
+ * holds the codes (or fp16 values), `deltas` the fp16 block deltas. */
+typedef struct nc_tensor {
+    void* data;
+    void* deltas;
+    int dtype;
+    int rows;
+    int cols;
+    int pitch;
+} nc_tensor;
+
+/* ---- runtime ---------------------------------------------------------------- */
+int nc_init(int device);
+const char* nc_last_error(void);
+int nc_malloc(void** ptr, size_t bytes);
+int nc_free(void* ptr);
+int nc_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int nc_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int nc_memset_d(void* dst, int value, size_t bytes);
+int nc_synchronize(void);
+
+/* ---- layouts (host-side, no GPU needed) -------------------------------------- */
+/* Bytes of one activation row (Tensor::bstride(0) of the reference,
+ * src/gten/tensor.h:96-116, in the device layout). */
+int nc_act_pitch(int dtype, int cols);
+/* Reference activation rows (Q8: 34-byte blocks; F16/F32 plain) <-> device
+ * rows, both on the host. */
+int nc_act_from_reference(const void* ref, void* dev_layout, int dtype, int rows, int cols);
+int nc_act_to_reference(const void* dev_layout, void* ref, int dtype, int rows, int cols);
+/* Sizes of a weight in the device layout. */
+int nc_weight_bytes(int dtype, int rows, int cols, size_t* code_bytes, size_t* delta_bytes);
+/* Reference weight payload (as read_into_weight stores it, src/gten/utils.cpp:
+ * 29-48: Q8/Q4 blocks or fp16 rows) -> device layout, on the host. */
+int nc_weight_from_reference(const void* ref, int dtype, int rows, int cols, void* codes, void* deltas);
+
+/* ---- weights on the device ---------------------------------------------------- */
+/* Deterministic N(0, stddev) fp32 values: Irwin-Hall sum of 12 24-bit
+ * uniforms from a counter-based splitmix64 hash of (seed, tensor_id, index). */
+int nc_gen_normal(uint64_t seed, uint32_t tensor_id, float stddev, int64_t n, float* out, void* stream);
+/* q8_quantize / q4_quantize of the converters (src/tinyllama/
+ * tinyllama_to_gten.py:24-91) from device fp32 [rows, cols] into `out`
+ * (data/deltas preallocated with nc_weight_bytes).  F16 converts with RNE. */
+int nc_weight_quantize(const float* w, nc_tensor* out, void* stream);
+
+/* ---- ops: gten::ops (src/gten/ops.h:10-40) on device tensors ----------------- */
+/* Each processes rows [start, n_ctx) like the reference's start_pos. */
+/* token_embed (ops.h:37): out[r] = table[tokens[r]], Q4 rows requantized to Q8. */
+int nc_token_embed(const nc_tensor* table, const int32_t* tokens, nc_tensor* out, int start, int n_ctx,
+                   void* stream);
+/* matmul_2d (ops.h:18): out[r, c] = dot(x[r], w[c]) with the reference's
+ * lane/block summation order; out dtype F32 gives the raw dot products,
+ * an activation dtype stores them requantized. */
+int nc_matmul_2d(const nc_tensor* x, const nc_tensor* w, nc_tensor* out, int start, int n_ctx, void* stream);
+/* rms_norm (ops.h:26): d_norm = cols for the 2-D op, the head size for the
+ * per-head (3-D) op; w is fp16 [d_norm]. */
+int nc_rms_norm(const nc_tensor* x, const uint16_t* w, nc_tensor* out, int d_norm, int start, int n_ctx,
+                void* stream);
+/* layer_norm (ops.h:16). */
+int nc_layer_norm(const nc_tensor* x, const uint16_t* w, const uint16_t* b, nc_tensor* out, int start, int n_ctx,
+                  void* stream);
+/* rotary_emb (ops.h:28).  `table` is nc_rope_table's (cos, sin) pairs. */
+int nc_rotary_emb(const nc_tensor* x, nc_tensor* out, int d_head, float rope_pct, const float* table, int start,
+                  int n_ctx, void* stream);
+/* Host: (cos, sin) of m * powf(10000, -(2j/d_r)) for m < max_ctx, j < d_r/2,
+ * evaluated with the host libm exactly as src/gten/ops.cpp:801-812. */
+int nc_rope_table(int max_ctx, int d_head, float rope_pct, float* out);
+int nc_silu(const nc_tensor* x, nc_tensor* out, int start, int n_ctx, void* stream);          /* ops.h:32 */
+int nc_multiply(const nc_tensor* a, const nc_tensor* b, nc_tensor* out, int start, int n_ctx,
+                void* stream);                                                                /* ops.h:20 */
+int nc_add(const nc_tensor* a, const nc_tensor* b, nc_tensor* out, int start, int n_ctx, void* stream); /* ops.h:12 */
+int nc_scale(nc_tensor* x, float s, int start, int n_ctx, void* stream);                        /* ops.h:30 */
+int nc_bias_add(nc_tensor* x, const uint16_t* b, int start, int n_ctx, void* stream);           /* ops.h:14 */
+/* qkv_attn (ops.h:24): causal GQA attention of rows [start, n_ctx). */
+int nc_qkv_attn(const nc_tensor* q, const nc_tensor* k, const nc_tensor* v, nc_tensor* out, int n_heads,
+                int n_kv_heads, int d_head, int start, int n_ctx, void* stream);
+/* The device's std::exp(float) as softmax and SiLU use it (src/gten/
+ * ops.cpp:752,1072): y[i] = expf(x[i]). */
+int nc_expf(const float* x, float* y, int64_t n, void* stream);
+/* The same function evaluated on the host CPU (no GPU needed). */
+float nc_expf_host(float x);
+/* Greedy pick of greedy_sample (src/gten/sampler.cpp:33-41): first index of
+ * the maximum. */
+int nc_argmax(const float* x, int n, int32_t* out, void* stream);
+
+/* ---- models: gten::Model::logits (src/gten/abc.h:25) and greedy_sample ------ */
+#define NC_ARCH_LLAMA 0   /* src/tinyllama */
+#define NC_ARCH_ZEPHYR 1  /* src/zephyr */
+#define NC_ARCH_MINICPM 2 /* src/minicpm */
+#define NC_ARCH_OPENELM 3 /* src/openelm */
+#define NC_MAX_LAYERS 64
+
+typedef struct nc_model_config {
+    int arch;
+    int wdtype; /* NC_F16, NC_Q8 or NC_Q4 (ModuleDtype mFloat16 / mQint8 / mQint4) */
+    int n_vocab;
+    int n_embd;
+    int n_layers;
+    int d_head;
+    int max_ctx; /* inference context: prompt + generated tokens */
+    int eos;
+    float rope_pct;
+    int n_heads[NC_MAX_LAYERS];
+    int n_kv_heads[NC_MAX_LAYERS];
+    int n_ffn[NC_MAX_LAYERS];
+} nc_model_config;
+
+/* Weight slots (layer >= 0) and global tensors (layer = -1). */
+#define NC_W_Q 0
+#define NC_W_K 1
+#define NC_W_V 2
+#define NC_W_O 3
+#define NC_W_GATE 4
+#define NC_W_UP 5
+#define NC_W_DOWN 6
+#define NC_W_ATTN_NORM 7
+#define NC_W_ATTN_NORM_B 8
+#define NC_W_MLP_NORM 9
+#define NC_W_MLP_NORM_B 10
+#define NC_W_Q_BIAS 11
+#define NC_W_K_BIAS 12
+#define NC_W_V_BIAS 13
+#define NC_W_Q_NORM 14
+#define NC_W_K_NORM 15
+#define NC_TID_EMB 0xFFFF0
+#define NC_TID_NORM 0xFFFF1
+#define NC_TID_NORM_B 0xFFFF2
+#define NC_TID_LM 0xFFFF3
+
+/* Model constructor (TinyLLama(n_ctx, dtype) and siblings): allocates every
+ * weight and every [max_ctx, d] activation buffer in HBM. */
+int nc_model_create(const nc_model_config* cfg, void** model);
+int nc_model_free(void* model);
+/* Synthetic weights generated and quantized on the device (same values as
+ * the CPU generator for the same seed). */
+int nc_model_init_synthetic(void* model, uint64_t seed);
+/* One weight from its reference payload bytes (read_into_weight,
+ * src/gten/utils.cpp:29-48). */
+int nc_model_set_weight(void* model, int layer, int slot, const void* ref_bytes, size_t n_bytes);
+/* The stored weight back in the reference's payload bytes. */
+int nc_model_get_weight(void* model, int layer, int slot, void* ref_bytes, size_t n_bytes);
+/* Model::logits(tokens, start_pos): processes rows [start_pos, n_tokens) and
+ * copies the last row's fp32 logits to `logits` (host, n_vocab floats). */
+int nc_model_logits(void* model, const int32_t* tokens, int n_tokens, int start_pos, float* logits);
+/* Residual stream after `layer` at `row`, in the reference's byte layout. */
+int nc_model_layer_out(void* model, int layer, int row, void* ref_bytes);
+/* greedy_sample (src/gten/sampler.cpp:11-60) without the tokenizer: prefill
+ * the prompt, then up to n_gen greedy steps with device-side argmax; stops
+ * at eos.  *n_out = tokens produced. */
+int nc_model_generate(void* model, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out, int* n_out);
+/* Split form for timing: nc_model_prefill runs the start_pos = 0 call and
+ * leaves the greedy token on the device; nc_model_decode runs n_steps more
+ * calls (no host round trip between steps) and appends the tokens. */
+int nc_model_prefill(void* model, const int32_t* prompt, int n_prompt);
+int nc_model_decode(void* model, int n_steps, int32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,247 @@
+"""MI355X (gfx950) decode path of nanochatllms.cpp behind a C-ABI.
+
+The product is ``_build/libgten_hip.so`` (HIP kernels + C entry points declared
+in ``include/gten_hip.h``).  This module is the Python host mirror used by the
+tests and the benchmark: ctypes bindings, device tensors, and the model
+workloads.  It never falls back to a CPU path: if the library is missing or
+the GPU is unavailable, calls raise.
+
+The directory name contains a dot, so import it with :func:`load_package`
+from a file path, e.g. ``importlib`` with ``spec_from_file_location``.
+"""
+import ctypes as C
+import os
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "_build", "libgten_hip.so")
+
+I32, F16, F32, Q8, Q4 = 0, 1, 2, 3, 4
+LLAMA, ZEPHYR, MINICPM, OPENELM = 0, 1, 2, 3
+MAX_LAYERS = 64
+W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN = range(7)
+W_ATTN_NORM, W_ATTN_NORM_B, W_MLP_NORM, W_MLP_NORM_B = 7, 8, 9, 10
+W_Q_BIAS, W_K_BIAS, W_V_BIAS, W_Q_NORM, W_K_NORM = 11, 12, 13, 14, 15
+TID_EMB, TID_NORM, TID_NORM_B, TID_LM = 0xFFFF0, 0xFFFF1, 0xFFFF2, 0xFFFF3
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class Tensor(C.Structure):
+    """nc_tensor: a device tensor descriptor (no ownership)."""
+    _fields_ = [("data", C.c_void_p), ("deltas", C.c_void_p), ("dtype", C.c_int), ("rows", C.c_int),
+                ("cols", C.c_int), ("pitch", C.c_int)]
+
+
+class ModelConfig(C.Structure):
+    """nc_model_config (field layout shared with the oracle's or_config)."""
+    _fields_ = [("arch", C.c_int), ("wdtype", C.c_int), ("n_vocab", C.c_int), ("n_embd", C.c_int),
+                ("n_layers", C.c_int), ("d_head", C.c_int), ("max_ctx", C.c_int), ("eos", C.c_int),
+                ("rope_pct", C.c_float), ("n_heads", C.c_int * MAX_LAYERS),
+                ("n_kv_heads", C.c_int * MAX_LAYERS), ("n_ffn", C.c_int * MAX_LAYERS)]
+
+
+def make_config(arch, wdtype, n_vocab, n_embd, n_layers, n_heads, n_kv_heads, n_ffn, max_ctx, eos=-1,
+                rope_pct=1.0, d_head=64, cls=ModelConfig):
+    c = cls()
+    c.arch, c.wdtype, c.n_vocab, c.n_embd, c.n_layers = arch, wdtype, n_vocab, n_embd, n_layers
+    c.d_head, c.max_ctx, c.eos, c.rope_pct = d_head, max_ctx, eos, rope_pct
+    as_list = lambda v: list(v) if isinstance(v, (list, tuple)) else [v] * n_layers
+    for i, (h, kv, f) in enumerate(zip(as_list(n_heads), as_list(n_kv_heads), as_list(n_ffn))):
+        c.n_heads[i], c.n_kv_heads[i], c.n_ffn[i] = h, kv, f
+    return c
+
+
+# The five workloads: model shapes of the reference's configs
+# (tinyllama/tinyllama.h:12-24 with vocab 32000, zephyr/zephyr.h:10-23,
+# minicpm/minicpm.h:9-24, an OpenELM-1.1B-like ramp on openelm/openelm.h:13-24),
+# synthetic N(0, 0.02) weights, random prompts of `prompt` tokens and `gen`
+# greedy tokens; max_ctx = prompt + gen.
+_ELM_F = [1024, 1280, 1536, 1792, 2048, 2304, 2560, 2816, 3072, 3328, 3584, 3840, 4096, 4608, 4608, 5120,
+          5376, 5632, 5888, 6144, 6400, 6656, 6912, 7168, 7424, 7680, 7936, 8192]
+WORKLOADS = {
+    "tinyllama-q8": dict(arch=LLAMA, wdtype=Q8, n_vocab=32000, n_embd=2048, n_layers=22, n_heads=32, n_kv_heads=4,
+                         n_ffn=5632, eos=32002, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0001),
+    "tinyllama-q4": dict(arch=LLAMA, wdtype=Q4, n_vocab=32000, n_embd=2048, n_layers=22, n_heads=32, n_kv_heads=4,
+                         n_ffn=5632, eos=32002, rope_pct=1.0, prompt=64, gen=256, seed=0x5EED0001),
+    "zephyr-f16": dict(arch=ZEPHYR, wdtype=F16, n_vocab=100352, n_embd=2048, n_layers=24, n_heads=32,
+                       n_kv_heads=32, n_ffn=5632, eos=100257, rope_pct=0.25, prompt=128, gen=128, seed=0x5EED0003),
+    "minicpm-q4": dict(arch=MINICPM, wdtype=Q4, n_vocab=122753, n_embd=2304, n_layers=40, n_heads=36,
+                       n_kv_heads=36, n_ffn=5760, eos=2, rope_pct=1.0, prompt=512, gen=128, seed=0x5EED0004),
+    "openelm-q8": dict(arch=OPENELM, wdtype=Q8, n_vocab=32000, n_embd=2048, n_layers=28,
+                       n_heads=[16] * 12 + [20] * 16, n_kv_heads=[4] * 12 + [5] * 16, n_ffn=_ELM_F,
+                       eos=32002, rope_pct=1.0, prompt=64, gen=256, seed=0x5EED0005),
+}
+PROMPT_SEED_OFFSET = 0x1000
+
+
+def workload_config(name, cls=ModelConfig, max_ctx=None):
+    w = WORKLOADS[name]
+    return make_config(w["arch"], w["wdtype"], w["n_vocab"], w["n_embd"], w["n_layers"], w["n_heads"],
+                       w["n_kv_heads"], w["n_ffn"], max_ctx or (w["prompt"] + w["gen"]), eos=w["eos"],
+                       rope_pct=w["rope_pct"], cls=cls)
+
+
+def act_row_bytes_ref(dtype, cols):
+    """Bytes of one activation row in the reference's layout."""
+    if dtype == Q8:
+        return (cols + 31) // 32 * 34
+    return cols * (2 if dtype == F16 else 4)
+
+
+def weight_bytes_ref(dtype, rows, cols):
+    if dtype == Q8:
+        return rows * (cols // 32) * 34
+    if dtype == Q4:
+        return rows * (cols // 32) * 18
+    return rows * cols * 2
+
+
+_lib = None
+
+
+def lib():
+    """The loaded product library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+    L = C.CDLL(LIB_PATH)
+    VP, I, F, SZ, U64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_uint64
+    TP = C.POINTER(Tensor)
+    sig = {
+        "nc_init": (I, [I]), "nc_last_error": (C.c_char_p, []), "nc_malloc": (I, [C.POINTER(VP), SZ]),
+        "nc_free": (I, [VP]), "nc_memcpy_h2d": (I, [VP, VP, SZ]), "nc_memcpy_d2h": (I, [VP, VP, SZ]),
+        "nc_memset_d": (I, [VP, I, SZ]), "nc_synchronize": (I, []),
+        "nc_act_pitch": (I, [I, I]), "nc_act_from_reference": (I, [VP, VP, I, I, I]),
+        "nc_act_to_reference": (I, [VP, VP, I, I, I]),
+        "nc_weight_bytes": (I, [I, I, I, C.POINTER(SZ), C.POINTER(SZ)]),
+        "nc_weight_from_reference": (I, [VP, I, I, I, VP, VP]),
+        "nc_gen_normal": (I, [U64, C.c_uint32, F, C.c_int64, VP, VP]),
+        "nc_weight_quantize": (I, [VP, TP, VP]),
+        "nc_token_embed": (I, [TP, VP, TP, I, I, VP]), "nc_matmul_2d": (I, [TP, TP, TP, I, I, VP]),
+        "nc_rms_norm": (I, [TP, VP, TP, I, I, I, VP]), "nc_layer_norm": (I, [TP, VP, VP, TP, I, I, VP]),
+        "nc_rotary_emb": (I, [TP, TP, I, F, VP, I, I, VP]), "nc_rope_table": (I, [I, I, F, VP]),
+        "nc_silu": (I, [TP, TP, I, I, VP]), "nc_multiply": (I, [TP, TP, TP, I, I, VP]),
+        "nc_add": (I, [TP, TP, TP, I, I, VP]), "nc_scale": (I, [TP, F, I, I, VP]),
+        "nc_bias_add": (I, [TP, VP, I, I, VP]), "nc_qkv_attn": (I, [TP, TP, TP, TP, I, I, I, I, I, VP]),
+        "nc_argmax": (I, [VP, I, VP, VP]), "nc_expf": (I, [VP, VP, C.c_int64, VP]),
+        "nc_expf_host": (F, [F]),
+        "nc_model_create": (I, [C.POINTER(ModelConfig), C.POINTER(VP)]), "nc_model_free": (I, [VP]),
+        "nc_model_init_synthetic": (I, [VP, U64]), "nc_model_set_weight": (I, [VP, I, I, VP, SZ]),
+        "nc_model_get_weight": (I, [VP, I, I, VP, SZ]), "nc_model_logits": (I, [VP, VP, I, I, VP]),
+        "nc_model_layer_out": (I, [VP, I, I, VP]), "nc_model_generate": (I, [VP, VP, I, I, VP, C.POINTER(I)]),
+        "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype, f.argtypes = res, args
+    _lib = L
+    return L
+
+
+def check(status, what=""):
+    if status != 0:
+        msg = lib().nc_last_error().decode(errors="replace")
+        raise HipError(f"{what}: status {status}: {msg}")
+
+
+def init(device=0):
+    check(lib().nc_init(device), "nc_init")
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class DeviceBuffer:
+    """An HBM allocation owned by Python (freed on close/GC)."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(lib().nc_malloc(C.byref(p), max(self.nbytes, 16)), "nc_malloc")
+        self.ptr = p.value
+
+    def upload(self, arr, offset=0):
+        check(lib().nc_memcpy_h2d(C.c_void_p(self.ptr + offset), _ptr(arr), arr.nbytes), "h2d")
+
+    def download(self, arr, offset=0):
+        check(lib().nc_memcpy_d2h(_ptr(arr), C.c_void_p(self.ptr + offset), arr.nbytes), "d2h")
+        return arr
+
+    def close(self):
+        if self.ptr:
+            lib().nc_free(C.c_void_p(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Model:
+    """gten::Model on the device (nc_model_*)."""
+
+    def __init__(self, cfg):
+        self.cfg = cfg
+        h = C.c_void_p()
+        check(lib().nc_model_create(C.byref(cfg), C.byref(h)), "nc_model_create")
+        self.h = h
+
+    def init_synthetic(self, seed):
+        check(lib().nc_model_init_synthetic(self.h, seed), "init_synthetic")
+
+    def set_weight(self, layer, slot, ref_bytes):
+        check(lib().nc_model_set_weight(self.h, layer, slot, _ptr(ref_bytes), ref_bytes.nbytes), "set_weight")
+
+    def get_weight(self, layer, slot, nbytes):
+        import numpy as np
+        out = np.zeros(nbytes, np.uint8)
+        check(lib().nc_model_get_weight(self.h, layer, slot, _ptr(out), nbytes), "get_weight")
+        return out
+
+    def logits(self, tokens, start_pos):
+        import numpy as np
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(self.cfg.n_vocab, np.float32)
+        check(lib().nc_model_logits(self.h, _ptr(toks), len(toks), start_pos, _ptr(out)), "logits")
+        return out
+
+    def layer_out(self, layer, row):
+        import numpy as np
+        adt = F16 if self.cfg.wdtype == F16 else Q8
+        out = np.zeros(act_row_bytes_ref(adt, self.cfg.n_embd), np.uint8)
+        check(lib().nc_model_layer_out(self.h, layer, row, _ptr(out)), "layer_out")
+        return out
+
+    def generate(self, prompt, n_gen):
+        import numpy as np
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, np.int32)
+        n = C.c_int()
+        check(lib().nc_model_generate(self.h, _ptr(p), len(p), n_gen, _ptr(out), C.byref(n)), "generate")
+        return out[: n.value]
+
+    def prefill(self, prompt):
+        import numpy as np
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        check(lib().nc_model_prefill(self.h, _ptr(p), len(p)), "prefill")
+
+    def decode(self, n_steps):
+        check(lib().nc_model_decode(self.h, n_steps, None), "decode")
+
+    def close(self):
+        if self.h:
+            lib().nc_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

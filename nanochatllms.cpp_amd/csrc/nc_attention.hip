@@ -1,0 +1,208 @@
+// nc_attention.hip -- causal GQA attention over the HBM-resident KV cache.
+//
+// Replaces qkv_attn -> qk_masked_softmax -> transpose_v -> qkv_matmul
+// (gten/ops.cpp:1017-1220).  One workgroup per (query head, query row):
+//   s_c  = dot(q_h, k_{c,g}) * (1/sqrtf(d_head)) for c <= row, -inf after,
+//          with the reference's dot product of the activation dtype (Q8:
+//          four integer lane sums per block, fp32 terms folded in block order;
+//          F16: eight fp32 lanes summed left to right);
+//   p    = softmax over the whole n_ctx row: max, expf(s - max), sequential
+//          sum, divide; the probability row is requantized in the activation
+//          dtype (Q8 blocks of 32 positions, last one partial) and read back;
+//   o_j  = 8-lane fp32 dot of p with V column j over n_ctx positions (lane =
+//          position mod 8, lanes summed left to right, then the n_ctx mod 8
+//          tail in order); the 64 outputs are requantized as the attention
+//          output row.
+// The K and V caches are the K/V Linear outputs (rows = positions) in the
+// activation dtype, as the reference keeps them (gten/modules.cpp:78-87).
+#include "nc_act.h"
+#include "nc_kernels.h"
+
+namespace nc {
+
+__device__ __forceinline__ uint32_t pick_pair2(uint32_t lo, uint32_t hi, int odd)
+{
+    return odd ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
+}
+
+// Lane-permuted dwords of one 32-code block (see nc_matvec.hip).
+__device__ __forceinline__ void lane_dwords(const uint8_t* codes, uint32_t xa[4], uint32_t xb[4])
+{
+    const uint4* p = reinterpret_cast<const uint4*>(codes);
+    const uint4 a = p[0], b = p[1];
+    const uint32_t X[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        xa[k] = pick_pair2(X[k >> 1], X[2 + (k >> 1)], k & 1);
+        xb[k] = pick_pair2(X[4 + (k >> 1)], X[6 + (k >> 1)], k & 1);
+    }
+}
+
+template <int ADT>
+__global__ __launch_bounds__(256) void k_attn(const uint8_t* __restrict__ q, int q_pitch,
+                                              const uint8_t* __restrict__ kc, int k_pitch,
+                                              const uint8_t* __restrict__ vc, int v_pitch,
+                                              uint8_t* __restrict__ out, int out_pitch, int hq, int hkv, int start,
+                                              int n_ctx, float scale)
+{
+    extern __shared__ __align__(16) float sm[];
+    const int npad = (n_ctx + 3) & ~3;
+    float* S = sm;            // scores / probabilities, n_ctx
+    float* red = S + npad;    // 256
+    float* acc = red + 256;   // [8][64]
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x;
+    const int qr = blockIdx.y;       // row within q / out (pointers start at row `start`)
+    const int row = start + qr;      // absolute position of the query
+    const int g = h / (hq / hkv);
+    const int qcols = hq * 64, kvcols = hkv * 64;
+    const int qd = act_delta_offset(qcols), kvd = act_delta_offset(kvcols);
+    const uint8_t* qrow = q + (size_t)qr * q_pitch;
+
+    // ---- scores
+    if (ADT == Q8) {
+        uint32_t qa[2][4], qb[2][4];
+        float dq[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            lane_dwords(qrow + h * 64 + b * 32, qa[b], qb[b]);
+            dq[b] = h2f(reinterpret_cast<const uint16_t*>(qrow + qd)[h * 2 + b]);
+        }
+        for (int c = tid; c < n_ctx; c += 256) {
+            float s = -INFINITY;
+            if (c <= row) {
+                const uint8_t* krow = kc + (size_t)c * k_pitch;
+                float a4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    uint32_t ka[4], kb[4];
+                    lane_dwords(krow + g * 64 + b * 32, ka, kb);
+                    const float dd = dq[b] * h2f(reinterpret_cast<const uint16_t*>(krow + kvd)[g * 2 + b]);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        int L = __builtin_amdgcn_sdot4((int)qa[b][k], (int)ka[k], 0, false);
+                        L = __builtin_amdgcn_sdot4((int)qb[b][k], (int)kb[k], L, false);
+                        a4[k] = a4[k] + (float)L * dd;
+                    }
+                }
+                s = ((a4[0] + a4[1]) + (a4[2] + a4[3])) * scale;
+            }
+            S[c] = s;
+        }
+    } else {
+        float qv[64];
+        const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + h * 64;
+#pragma unroll
+        for (int e = 0; e < 64; e++) qv[e] = h2f(qh[e]);
+        for (int c = tid; c < n_ctx; c += 256) {
+            float s = -INFINITY;
+            if (c <= row) {
+                const uint16_t* kh = reinterpret_cast<const uint16_t*>(kc + (size_t)c * k_pitch) + g * 64;
+                float a8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                for (int m = 0; m < 8; m++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) a8[j] = qv[8 * m + j] * h2f(kh[8 * m + j]) + a8[j];
+                s = a8[0] + a8[1] + a8[2] + a8[3] + a8[4] + a8[5] + a8[6] + a8[7];
+                s = s * scale;
+            }
+            S[c] = s;
+        }
+    }
+    __syncthreads();
+
+    // ---- softmax
+    float mx = -INFINITY;
+    for (int c = tid; c < n_ctx; c += 256) mx = fmaxf(mx, S[c]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+        __syncthreads();
+    }
+    mx = red[0];
+    for (int c = tid; c < n_ctx; c += 256) S[c] = expf_ref(S[c] - mx);
+    __syncthreads();
+    const float sum = seq_sum(S, n_ctx);
+    __syncthreads();
+    // every thread walks its positions in 32-lane blocks; lanes past n_ctx
+    // still take part in the block reduction with valid = false
+    for (int c0 = 0; c0 < n_ctx; c0 += 256) {
+        const int c = c0 + tid;
+        const bool valid = c < n_ctx;
+        const float p = valid ? S[c] / sum : 0.0f;
+        const float pr = act_roundtrip<ADT>(p, valid);
+        if (valid) S[c] = pr;
+    }
+    __syncthreads();
+
+    // ---- P @ V: thread = (column j, lanes l0, l0 + 1)
+    {
+        const int j = tid & 63;
+        const int l0 = (tid >> 6) * 2;
+        const int n8 = (n_ctx / 8) * 8;
+#pragma unroll
+        for (int li = 0; li < 2; li++) {
+            const int l = l0 + li;
+            float a = 0.0f;
+            for (int c = l; c < n8; c += 8) {
+                const uint8_t* vrow = vc + (size_t)c * v_pitch;
+                a = S[c] * act_load<ADT>(vrow, g * 64 + j, kvd) + a;
+            }
+            acc[l * 64 + j] = a;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int j = tid;
+        float s = acc[j];
+#pragma unroll
+        for (int l = 1; l < 8; l++) s = s + acc[l * 64 + j];
+        for (int c = (n_ctx / 8) * 8; c < n_ctx; c++)
+            s = s + S[c] * act_load<ADT>(vc + (size_t)c * v_pitch, g * 64 + j, kvd);
+        act_store<ADT>(out + (size_t)qr * out_pitch, h * 64 + j, qd, s, true);
+    }
+}
+
+int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k_pitch, const uint8_t* vc, int v_pitch,
+                uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st)
+{
+    const int rows = n_ctx - start;
+    if (rows <= 0) return NC_OK;
+    if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "qkv_attn: %d query heads over %d kv heads", hq, hkv);
+    const float scale = 1.0f / sqrtf(64.0f);
+    const size_t lds = ((size_t)((n_ctx + 3) & ~3) + 256 + 512) * 4;
+    if (lds > 64 * 1024) return fail(NC_ERR_ARG, "qkv_attn: context %d too long", n_ctx);
+    const dim3 grid(hq, rows);
+    if (adt == NC_Q8)
+        hipLaunchKernelGGL((k_attn<Q8>), grid, dim3(256), lds, st, q, q_pitch, kc, k_pitch, vc, v_pitch, out, out_pitch,
+                           hq, hkv, start, n_ctx, scale);
+    else if (adt == NC_F16)
+        hipLaunchKernelGGL((k_attn<F16>), grid, dim3(256), lds, st, q, q_pitch, kc, k_pitch, vc, v_pitch, out, out_pitch,
+                           hq, hkv, start, n_ctx, scale);
+    else
+        return fail(NC_ERR_ARG, "qkv_attn: activation dtype %d", adt);
+    return launch_status("k_attn");
+}
+
+}  // namespace nc
+
+using namespace nc;
+
+extern "C" int nc_qkv_attn(const nc_tensor* q, const nc_tensor* k, const nc_tensor* v, nc_tensor* out, int n_heads,
+                           int n_kv_heads, int d_head, int start, int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(q && k && v && out && q->data && k->data && v->data && out->data, "qkv_attn: null tensor");
+    NC_CHECK_ARG(d_head == 64, "qkv_attn: head size %d (the kernels are built for 64)", d_head);
+    NC_CHECK_ARG(q->dtype == k->dtype && k->dtype == v->dtype && v->dtype == out->dtype,
+                 "qkv_attn: dtypes differ");  // the reference's assert, gten/ops.cpp:1216
+    NC_CHECK_ARG(q->cols == n_heads * 64 && k->cols == n_kv_heads * 64 && v->cols == k->cols && out->cols == q->cols,
+                 "qkv_attn: widths do not match the head counts");
+    NC_CHECK_ARG(start >= 0 && start <= n_ctx && n_ctx <= k->rows && n_ctx <= v->rows && n_ctx <= q->rows &&
+                     n_ctx <= out->rows,
+                 "qkv_attn: rows [%d, %d)", start, n_ctx);
+    return attn_launch(q->dtype, (const uint8_t*)q->data + (size_t)start * q->pitch, q->pitch,
+                       (const uint8_t*)k->data, k->pitch, (const uint8_t*)v->data, v->pitch,
+                       (uint8_t*)out->data + (size_t)start * out->pitch, out->pitch, n_heads, n_kv_heads, start, n_ctx,
+                       stream_of(stream));
+}

@@ -1,0 +1,126 @@
+// nc_device.h -- device-side numerics shared by the gfx950 kernels.
+//
+// Every helper reproduces one rounding step of the reference CPU path
+// exactly; the kernels are compiled with -ffp-contract=off and IEEE fp32
+// division / sqrt so that no step is fused or approximated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nc_layout.h"
+
+namespace nc {
+
+constexpr int kWave = 64;
+
+// fp16 -> fp32, exact (gten/gten_types.h:129-133).
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// fp32 -> fp16, round to nearest even (gten/gten_types.h:136-139; F16C
+// _mm256_cvtps_ph(x, 0) in gten/ops.cpp:97-107).
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// std::exp(float) as the reference calls it (gten/ops.cpp:752,1072): the
+// reference runs glibc's expf, which on x86-64 hosts with FMA is the
+// table-driven algorithm of ARM's optimized-routines (math/expf.c,
+// math/exp2f_data.c; MIT / Apache-2.0) compiled with fused multiply-adds.
+// Restated here step by step so the device result equals the host's bit for
+// bit:  x*N/ln2 = k + r (N = 32, round-to-nearest via the 1.5*2^52 shift),
+// 2^(k/N) from a 32-entry table, 2^(r/N) by a cubic, all in double, one
+// rounding to fp32 at the end.  kExp2Tab[i] = bits(2^(i/32)) - (i << 47).
+constexpr uint64_t kExp2Tab[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+NC_HD float expf_ref(float x)
+{
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {                            // |x| >= 88 or NaN
+        if (ux == 0xff800000u) return 0.0f;            // -inf
+        if (abstop >= 0x7f8u) return x + x;            // +inf, NaN
+        if (x > 0x1.62e42ep6f) return __builtin_inff(); // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;           // underflow
+    }
+    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32;
+    constexpr double kShift = 0x1.8p+52;
+    constexpr double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+    constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+    constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    const uint64_t t = kExp2Tab[ki & 31u] + (ki << 47);
+    const double s = __builtin_bit_cast(double, t);
+    const double z = __builtin_fma(kC0, r, kC1);
+    const double r2 = r * r;
+    double y = __builtin_fma(kC2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// Reduction of a value across the 32 lanes of a half-wave (xor butterfly).
+__device__ __forceinline__ float half_wave_max(float v)
+{
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
+    return v;
+}
+
+// q8_quantize_block (gten/quants.cpp:16-30) for one 32-value block held one
+// value per lane of a 32-lane group: absmax (order-free), delta =
+// absmax/127 (IEEE division), fp16 delta stored, scale = 1/delta from the
+// fp32 delta, q = (int8)roundf(x * scale).  `valid` lanes beyond a partial
+// block's end contribute nothing.  Returns the int8 code; *d16 gets the
+// stored delta.
+__device__ __forceinline__ int8_t q8_quant_lane(float x, bool valid, uint16_t* d16)
+{
+    const float a = valid ? fabsf(x) : 0.0f;
+    const float amax = half_wave_max(a);
+    const float delta = amax / 127.0f;
+    *d16 = f2h(delta);
+    const float scale = delta != 0.0f ? 1.0f / delta : 0.0f;
+    return (int8_t)roundf(x * scale);
+}
+
+// Q8 round trip of one value of a lane-resident block: what
+// write_row_from_float followed by read_row_to_float leaves.
+__device__ __forceinline__ float q8_roundtrip_lane(float x, bool valid)
+{
+    uint16_t d16;
+    const int8_t q = q8_quant_lane(x, valid, &d16);
+    return (float)q * h2f(d16);
+}
+
+__device__ __forceinline__ float f16_roundtrip(float x) { return h2f(f2h(x)); }
+
+// Sequential fp32 sum of buf[0..n) in index order, every calling lane
+// reading the same addresses (an LDS broadcast), so every lane ends with the
+// sum.  This is the scalar accumulation loop of the reference's norms and
+// softmax (gten/ops.cpp:673-683,833-835,1069-1075).
+__device__ __forceinline__ float seq_sum(const float* buf, int n)
+{
+    float s = 0.0f;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(buf + i);
+        s = s + v.x;
+        s = s + v.y;
+        s = s + v.z;
+        s = s + v.w;
+    }
+    for (; i < n; i++) s = s + buf[i];
+    return s;
+}
+
+}  // namespace nc

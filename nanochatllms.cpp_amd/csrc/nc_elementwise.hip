@@ -1,0 +1,584 @@
+// nc_elementwise.hip -- norms, RoPE, SiLU/multiply/add/scale/bias, token
+// embedding, requantization and argmax for gfx950.
+//
+// Each kernel restates one gten op (gten/ops.cpp) including the write of its
+// output in the activation dtype (write_row_from_float, gten/ops.cpp:87-123):
+// Q8 rows are requantized per 32-value block (absmax / 127, fp16 delta,
+// roundf) on the 32 lanes that hold the block.  The fused variants used by
+// the decode step take the fp32 output of a matvec and first apply the
+// requantization the reference's Linear::forward performs on it
+// (gten/modules.cpp:89-104), so their results equal the unfused op chain.
+#include <cmath>
+#include <vector>
+
+#include "nc_act.h"
+#include "nc_kernels.h"
+
+namespace nc {
+
+constexpr int kNormMaxPerThread = 16;
+constexpr int kNormMaxCols = 4096;
+
+// ---------------------------------------------------------------- requant --
+
+// write_row_from_float of fp32 rows (matmul output) into activation rows.
+template <int ADT>
+__global__ __launch_bounds__(256) void k_write_rows(const float* __restrict__ in, int in_pitch, uint8_t* __restrict__ out,
+                                                   int out_pitch, int cols)
+{
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int r = blockIdx.y;
+    const bool valid = e < cols;
+    const float v = valid ? in[(size_t)r * in_pitch + e] : 0.0f;
+    act_store<ADT>(out + (size_t)r * out_pitch, e, act_delta_offset(cols), v, valid);
+}
+
+// ------------------------------------------------------------------ norms --
+
+enum NormKind { kRms = 0, kLayerNorm = 1 };
+
+// One workgroup per normalized segment (a row, or one head of a row).
+// Input: the activation row a, or (ADD) the residual sum a + b where b is a
+// matvec's fp32 output requantized as the Linear output (optionally scaled
+// and requantized again, MiniCPM's ops::scale).  The sum is stored to h_out
+// in the activation dtype and normalized from that stored value.
+//   RMS: rms_norm_vec_f32 (gten/ops.cpp:830-846): sequential sum of squares,
+//        rms = sqrtf(ss / n), y = x / (rms + 1e-6f) * w.
+//   LN : vec_layer_norm_f32 (gten/ops.cpp:669-698): sequential mean and
+//        variance, y = ((x - mean) / (sqrtf(var) + 1e-5f)) * w + b.
+// post_scale != 1 applies ops::scale to the stored result (MiniCPM).
+template <int ADT, int KIND, bool ADD>
+__global__ __launch_bounds__(256) void k_norm(const uint8_t* __restrict__ a, int a_pitch,
+                                              const float* __restrict__ braw, int b_pitch, float bscale,
+                                              uint8_t* __restrict__ h_out, int h_pitch,
+                                              const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
+                                              uint8_t* __restrict__ out, int out_pitch, int n, int row_cols,
+                                              float post_scale)
+{
+    __shared__ __align__(16) float buf[kNormMaxCols];
+    const int tid = threadIdx.x;
+    const int bs = blockDim.x;
+    const int per = n / bs;
+    const int r = blockIdx.y;
+    const int seg0 = blockIdx.x * n;  // first column of this segment in the row
+    const int dofs = act_delta_offset(row_cols);
+    const uint8_t* arow = a + (size_t)r * a_pitch;
+    uint8_t* orow = out + (size_t)r * out_pitch;
+
+    float xv[kNormMaxPerThread];
+#pragma unroll
+    for (int m = 0; m < kNormMaxPerThread; m++) {
+        if (m >= per) continue;
+        const int e = seg0 + tid + m * bs;
+        float x = act_load<ADT>(arow, e, dofs);
+        if (ADD) {
+            float b = act_roundtrip<ADT>(braw[(size_t)r * b_pitch + e], true);
+            if (bscale != 1.0f) b = act_roundtrip<ADT>(b * bscale, true);
+            const float s = x + b;
+            x = act_roundtrip<ADT>(s, true);
+            act_store<ADT>(h_out + (size_t)r * h_pitch, e, dofs, s, true);
+        }
+        xv[m] = x;
+        buf[tid + m * bs] = KIND == kRms ? x * x : x;
+    }
+    __syncthreads();
+    const float s1 = seq_sum(buf, n);
+    float mean = 0.0f, denom;
+    if (KIND == kRms) {
+        const float rms = sqrtf(s1 / (float)n);
+        denom = rms + 1e-6f;
+    } else {
+        mean = s1 / (float)n;
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < kNormMaxPerThread; m++) {
+            if (m >= per) continue;
+            buf[tid + m * bs] = (xv[m] - mean) * (xv[m] - mean);
+        }
+        __syncthreads();
+        const float ssq = seq_sum(buf, n);
+        denom = sqrtf(ssq / (float)n) + 1e-05f;
+    }
+#pragma unroll
+    for (int m = 0; m < kNormMaxPerThread; m++) {
+        if (m >= per) continue;
+        const int i = tid + m * bs;  // index within the segment (weight index)
+        float y;
+        if (KIND == kRms) y = xv[m] / denom * h2f(w[i]);
+        else y = ((xv[m] - mean) / denom) * h2f(w[i]) + h2f(bias[i]);
+        if (post_scale != 1.0f) y = act_roundtrip<ADT>(y, true) * post_scale;
+        act_store<ADT>(orow, seg0 + i, dofs, y, true);
+    }
+}
+
+// ------------------------------------------------------------------- rope --
+
+// (x_j, x_{j+d/2}) -> (x_j cos - x_{j+d/2} sin, x_j sin + x_{j+d/2} cos) on
+// the first d_r dims of a 64-wide head held one value per lane.
+__device__ __forceinline__ float rope_lane(float x, int lane, int d_half, const float2* cs)
+{
+    const int d_r = 2 * d_half;
+    const int partner = lane < d_half ? lane + d_half : (lane < d_r ? lane - d_half : lane);
+    const float xp = __shfl(x, partner);
+    if (lane < d_half) {
+        const float2 t = cs[lane];
+        return x * t.x - xp * t.y;
+    }
+    if (lane < d_r) {
+        const float2 t = cs[lane - d_half];
+        return xp * t.y + x * t.x;
+    }
+    return x;
+}
+
+// rotary_emb (gten/ops.cpp:775-821) on stored activation rows: one
+// wavefront per 64-wide head; row r has position start + blockIdx.y.
+template <int ADT>
+__global__ __launch_bounds__(64) void k_rope(const uint8_t* __restrict__ in, int in_pitch, uint8_t* __restrict__ out,
+                                             int out_pitch, int cols, const float2* __restrict__ table, int d_half,
+                                             int start)
+{
+    const int lane = threadIdx.x;
+    const int r = blockIdx.y;
+    const int e = blockIdx.x * 64 + lane;
+    const int dofs = act_delta_offset(cols);
+    const float x = act_load<ADT>(in + (size_t)r * in_pitch, e, dofs);
+    const float y = rope_lane(x, lane, d_half, table + (size_t)(start + r) * d_half);
+    act_store<ADT>(out + (size_t)r * out_pitch, e, dofs, y, true);
+}
+
+// Decode-step epilogue of the fused q|k|v matvec: per 64-wide head segment
+// of the fp32 output [q heads | k heads | v heads]:
+//   Linear output requantized (+ fp16 bias, requantized: bias_add_inplace),
+//   q/k: optional per-head RMSNorm (OpenELM's QK norm, requantized), RoPE at
+//   the row's position (requantized); q -> q_out, k -> K cache row,
+//   v -> V cache row.
+template <int ADT, bool BIAS, bool QKNORM>
+__global__ __launch_bounds__(64) void k_qkv_post(const float* __restrict__ raw, int raw_pitch, int hq, int hkv,
+                                                 const uint16_t* __restrict__ bq, const uint16_t* __restrict__ bk,
+                                                 const uint16_t* __restrict__ bv, const uint16_t* __restrict__ qn_w,
+                                                 const uint16_t* __restrict__ kn_w, const float2* __restrict__ table,
+                                                 int d_half, int start, uint8_t* __restrict__ q_out, int q_pitch,
+                                                 uint8_t* __restrict__ k_cache, int k_pitch,
+                                                 uint8_t* __restrict__ v_cache, int v_pitch)
+{
+    __shared__ __align__(16) float buf[64];
+    const int lane = threadIdx.x;
+    const int seg = blockIdx.x;
+    const int r = blockIdx.y;
+    const int pos = start + r;
+    const int kind = seg < hq ? 0 : (seg < hq + hkv ? 1 : 2);
+    const int h = kind == 0 ? seg : (kind == 1 ? seg - hq : seg - hq - hkv);
+    float x = act_roundtrip<ADT>(raw[(size_t)r * raw_pitch + seg * 64 + lane], true);
+    if (BIAS) {
+        const uint16_t* b = kind == 0 ? bq : (kind == 1 ? bk : bv);
+        x = act_roundtrip<ADT>(x + h2f(b[h * 64 + lane]), true);
+    }
+    if (kind < 2) {
+        if (QKNORM) {
+            buf[lane] = x * x;
+            __syncthreads();
+            const float rms = sqrtf(seq_sum(buf, 64) / 64.0f);
+            x = act_roundtrip<ADT>(x / (rms + 1e-6f) * h2f((kind == 0 ? qn_w : kn_w)[lane]), true);
+        }
+        x = rope_lane(x, lane, d_half, table + (size_t)pos * d_half);
+    }
+    uint8_t* dst;
+    int cols;
+    if (kind == 0) { dst = q_out + (size_t)r * q_pitch; cols = hq * 64; }
+    else if (kind == 1) { dst = k_cache + (size_t)pos * k_pitch; cols = hkv * 64; }
+    else { dst = v_cache + (size_t)pos * v_pitch; cols = hkv * 64; }
+    act_store<ADT>(dst, h * 64 + lane, act_delta_offset(cols), x, true);
+}
+
+// ------------------------------------------------------------ elementwise --
+
+enum EwOp { kSilu = 0, kMul = 1, kAdd = 2, kScale = 3, kBias = 4 };
+
+// silu_impl / mul_impl / add_impl / scale / bias_add_inplace
+// (gten/ops.cpp:733-757, 918-1014, 146-164, 639-666) on activation rows.
+template <int ADT, int OP>
+__global__ __launch_bounds__(256) void k_ew(const uint8_t* __restrict__ a, int a_pitch, const uint8_t* __restrict__ b,
+                                            int b_pitch, const uint16_t* __restrict__ bias, float s,
+                                            uint8_t* __restrict__ out, int out_pitch, int cols)
+{
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int r = blockIdx.y;
+    const bool valid = e < cols;
+    const int dofs = act_delta_offset(cols);
+    const int ec = valid ? e : 0;
+    const float x = act_load<ADT>(a + (size_t)r * a_pitch, ec, dofs);
+    float y;
+    if (OP == kSilu) y = x / (1.0f + expf_ref(-x));
+    else if (OP == kMul) y = x * act_load<ADT>(b + (size_t)r * b_pitch, ec, dofs);
+    else if (OP == kAdd) y = x + act_load<ADT>(b + (size_t)r * b_pitch, ec, dofs);
+    else if (OP == kScale) y = x * s;
+    else y = x + h2f(bias[ec]);
+    act_store<ADT>(out + (size_t)r * out_pitch, e, dofs, y, valid);
+}
+
+// Decode-step SwiGLU from the fused gate|up matvec output [gate | up]:
+// gate and up requantized as Linear outputs, SiLU in place (requantized),
+// multiply in place (requantized) -- ffn_forward, tinyllama/tinyllama.cpp:88-97.
+template <int ADT>
+__global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ raw, int raw_pitch, int f,
+                                                  uint8_t* __restrict__ out, int out_pitch)
+{
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int r = blockIdx.y;
+    const bool valid = e < f;
+    const int ec = valid ? e : 0;
+    const float* rr = raw + (size_t)r * raw_pitch;
+    const float g = act_roundtrip<ADT>(rr[ec], valid);
+    const float gs = act_roundtrip<ADT>(g / (1.0f + expf_ref(-g)), valid);
+    const float u = act_roundtrip<ADT>(rr[f + ec], valid);
+    act_store<ADT>(out + (size_t)r * out_pitch, e, act_delta_offset(f), gs * u, valid);
+}
+
+// -------------------------------------------------------------- embedding --
+
+// token_embed / copy_row (gten/ops.cpp:526-576): Q8 and F16 rows copied,
+// Q4 rows dequantized and requantized to Q8.  post_scale != 1 applies
+// ops::scale afterwards (MiniCPM's embedding scale).
+template <int WDT, int ADT>
+__global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ codes, const uint16_t* __restrict__ deltas,
+                                               int vocab, const int32_t* __restrict__ tokens, uint8_t* __restrict__ out,
+                                               int out_pitch, int d, float post_scale)
+{
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int r = blockIdx.y;
+    const bool valid = e < d;
+    const int ec = valid ? e : 0;
+    int tok = tokens[r];
+    tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+    uint8_t* orow = out + (size_t)r * out_pitch;
+    const int dofs = act_delta_offset(d);
+    const int nb = d / 32;
+    float v;
+    if (WDT == Q4 || WDT == Q8) {
+        const size_t blk = (size_t)tok * nb + (ec >> 5);
+        const float dw = h2f(deltas[blk]);
+        if (WDT == Q8) {
+            const int q = q8_weight_code(codes + blk * 8, ec & 31);
+            if (post_scale == 1.0f) {
+                if (valid) {
+                    reinterpret_cast<int8_t*>(orow)[e] = (int8_t)q;
+                    if ((e & 31) == 0) reinterpret_cast<uint16_t*>(orow + dofs)[e >> 5] = deltas[blk];
+                }
+                return;
+            }
+            v = (float)q * dw;
+        } else {
+            v = (float)(q4_weight_code(codes + blk * 4, ec & 31) - 7) * dw;
+        }
+    } else {
+        const int npad = (vocab + 7) & ~7;
+        v = h2f(reinterpret_cast<const uint16_t*>(codes)[f16_weight_index(tok, ec, npad)]);
+    }
+    if (post_scale != 1.0f) v = act_roundtrip<ADT>(v, valid) * post_scale;
+    act_store<ADT>(orow, e, dofs, v, valid);
+}
+
+// ----------------------------------------------------------------- argmax --
+
+// First index of the maximum (strict '>' scan of gten/sampler.cpp:33-41).
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, int32_t* __restrict__ out)
+{
+    __shared__ float sv[1024];
+    __shared__ int si[1024];
+    const int tid = threadIdx.x;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < n; i += 1024) {
+        const float v = x[i];
+        if (v > best) { best = v; bi = i; }
+    }
+    sv[tid] = best;
+    si[tid] = bi;
+    __syncthreads();
+    for (int s = 512; s > 0; s >>= 1) {
+        if (tid < s) {
+            const float v = sv[tid + s];
+            const int i = si[tid + s];
+            if (v > sv[tid] || (v == sv[tid] && i < si[tid])) { sv[tid] = v; si[tid] = i; }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) out[0] = si[0] == 0x7fffffff ? 0 : si[0];
+}
+
+// ============================================================ launchers ==
+
+#define NC_ADT_DISPATCH(adt, KERNEL_CALL)                              \
+    do {                                                               \
+        if ((adt) == NC_Q8) { constexpr int ADT = Q8; KERNEL_CALL; }    \
+        else if ((adt) == NC_F16) { constexpr int ADT = F16; KERNEL_CALL; } \
+        else { constexpr int ADT = F32; KERNEL_CALL; }                 \
+    } while (0)
+
+int write_rows(const float* in, int in_pitch, uint8_t* out, int out_pitch, int dtype, int cols, int rows,
+               hipStream_t st)
+{
+    if (rows <= 0) return NC_OK;
+    const dim3 grid((cols + 255) / 256, rows);
+    NC_ADT_DISPATCH(dtype, hipLaunchKernelGGL((k_write_rows<ADT>), grid, dim3(256), 0, st, in, in_pitch, out,
+                                              out_pitch, cols));
+    return launch_status("k_write_rows");
+}
+
+static int norm_block(int n) { return n >= 256 ? 256 : n; }
+
+int norm_launch(int kind, int adt, bool add, const uint8_t* a, int a_pitch, const float* braw, int b_pitch,
+                float bscale, uint8_t* h_out, int h_pitch, const uint16_t* w, const uint16_t* bias, uint8_t* out,
+                int out_pitch, int d_norm, int row_cols, int rows, float post_scale, hipStream_t st)
+{
+    if (rows <= 0) return NC_OK;
+    const int bs = norm_block(d_norm);
+    if (d_norm % 32 || row_cols % d_norm || d_norm % bs || d_norm / bs > kNormMaxPerThread || d_norm > kNormMaxCols)
+        return fail(NC_ERR_ARG, "norm: unsupported size %d (row %d)", d_norm, row_cols);
+    if (adt != NC_Q8 && adt != NC_F16) return fail(NC_ERR_ARG, "norm: activation dtype %d", adt);
+    const dim3 grid(row_cols / d_norm, rows);
+#define NORM_CALL(K, A)                                                                                           \
+    hipLaunchKernelGGL((k_norm<ADT, K, A>), grid, dim3(bs), 0, st, a, a_pitch, braw, b_pitch, bscale, h_out, h_pitch, \
+                       w, bias, out, out_pitch, d_norm, row_cols, post_scale)
+    if (adt == NC_Q8) {
+        constexpr int ADT = Q8;
+        if (kind == kRms) { if (add) NORM_CALL(kRms, true); else NORM_CALL(kRms, false); }
+        else { if (add) NORM_CALL(kLayerNorm, true); else NORM_CALL(kLayerNorm, false); }
+    } else {
+        constexpr int ADT = F16;
+        if (kind == kRms) { if (add) NORM_CALL(kRms, true); else NORM_CALL(kRms, false); }
+        else { if (add) NORM_CALL(kLayerNorm, true); else NORM_CALL(kLayerNorm, false); }
+    }
+#undef NORM_CALL
+    return launch_status("k_norm");
+}
+
+int qkv_post_launch(int adt, const float* raw, int raw_pitch, int hq, int hkv, const uint16_t* bq, const uint16_t* bk,
+                    const uint16_t* bv, const uint16_t* qn_w, const uint16_t* kn_w, const float* table, int d_half,
+                    int start, int rows, uint8_t* q_out, int q_pitch, uint8_t* k_cache, int k_pitch,
+                    uint8_t* v_cache, int v_pitch, hipStream_t st)
+{
+    if (rows <= 0) return NC_OK;
+    const dim3 grid(hq + 2 * hkv, rows);
+    const bool bias = bq != nullptr, qkn = qn_w != nullptr;
+#define QKV_CALL(B, N)                                                                                              \
+    hipLaunchKernelGGL((k_qkv_post<ADT, B, N>), grid, dim3(64), 0, st, raw, raw_pitch, hq, hkv, bq, bk, bv, qn_w, kn_w, \
+                       (const float2*)table, d_half, start, q_out, q_pitch, k_cache, k_pitch, v_cache, v_pitch)
+    if (adt == NC_Q8) {
+        constexpr int ADT = Q8;
+        if (bias) { if (qkn) QKV_CALL(true, true); else QKV_CALL(true, false); }
+        else { if (qkn) QKV_CALL(false, true); else QKV_CALL(false, false); }
+    } else if (adt == NC_F16) {
+        constexpr int ADT = F16;
+        if (bias) { if (qkn) QKV_CALL(true, true); else QKV_CALL(true, false); }
+        else { if (qkn) QKV_CALL(false, true); else QKV_CALL(false, false); }
+    } else {
+        return fail(NC_ERR_ARG, "qkv_post: activation dtype %d", adt);
+    }
+#undef QKV_CALL
+    return launch_status("k_qkv_post");
+}
+
+int silu_mul_launch(int adt, const float* raw, int raw_pitch, int f, uint8_t* out, int out_pitch, int rows,
+                    hipStream_t st)
+{
+    if (rows <= 0) return NC_OK;
+    const dim3 grid((f + 255) / 256, rows);
+    if (adt == NC_Q8) hipLaunchKernelGGL((k_silu_mul<Q8>), grid, dim3(256), 0, st, raw, raw_pitch, f, out, out_pitch);
+    else if (adt == NC_F16) hipLaunchKernelGGL((k_silu_mul<F16>), grid, dim3(256), 0, st, raw, raw_pitch, f, out, out_pitch);
+    else return fail(NC_ERR_ARG, "silu_mul: activation dtype %d", adt);
+    return launch_status("k_silu_mul");
+}
+
+int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, int out_pitch, int adt, int rows,
+                 float post_scale, hipStream_t st)
+{
+    if (rows <= 0) return NC_OK;
+    const int d = table->cols;
+    const dim3 grid((d + 255) / 256, rows);
+    const uint32_t* c = (const uint32_t*)table->data;
+    const uint16_t* dl = (const uint16_t*)table->deltas;
+    if (table->dtype == NC_Q4 && adt == NC_Q8)
+        hipLaunchKernelGGL((k_embed<Q4, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale);
+    else if (table->dtype == NC_Q8 && adt == NC_Q8)
+        hipLaunchKernelGGL((k_embed<Q8, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale);
+    else if (table->dtype == NC_F16 && adt == NC_F16)
+        hipLaunchKernelGGL((k_embed<F16, F16>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale);
+    else
+        return fail(NC_ERR_ARG, "token_embed: table dtype %d with activation dtype %d", table->dtype, adt);
+    return launch_status("k_embed");
+}
+
+int argmax_launch(const float* x, int n, int32_t* out, hipStream_t st)
+{
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, x, n, out);
+    return launch_status("k_argmax");
+}
+
+int ew_launch(int op, int adt, const uint8_t* a, int a_pitch, const uint8_t* b, int b_pitch, const uint16_t* bias,
+              float s, uint8_t* out, int out_pitch, int cols, int rows, hipStream_t st)
+{
+    if (rows <= 0) return NC_OK;
+    const dim3 grid((cols + 255) / 256, rows);
+#define EW_CALL(OPV) hipLaunchKernelGGL((k_ew<ADT, OPV>), grid, dim3(256), 0, st, a, a_pitch, b, b_pitch, bias, s, out, out_pitch, cols)
+    NC_ADT_DISPATCH(adt, {
+        switch (op) {
+        case kSilu: EW_CALL(kSilu); break;
+        case kMul: EW_CALL(kMul); break;
+        case kAdd: EW_CALL(kAdd); break;
+        case kScale: EW_CALL(kScale); break;
+        default: EW_CALL(kBias); break;
+        }
+    });
+#undef EW_CALL
+    return launch_status("k_ew");
+}
+
+int rope_launch(int adt, const uint8_t* in, int in_pitch, uint8_t* out, int out_pitch, int cols, const float* table,
+                int d_half, int start, int rows, hipStream_t st)
+{
+    if (rows <= 0) return NC_OK;
+    if (cols % 64) return fail(NC_ERR_ARG, "rotary_emb: width %d is not a multiple of the 64-wide head", cols);
+    const dim3 grid(cols / 64, rows);
+    NC_ADT_DISPATCH(adt, hipLaunchKernelGGL((k_rope<ADT>), grid, dim3(64), 0, st, in, in_pitch, out, out_pitch, cols,
+                                            (const float2*)table, d_half, start));
+    return launch_status("k_rope");
+}
+
+}  // namespace nc
+
+// ================================================================ C-ABI ==
+
+using namespace nc;
+
+static bool act_ok(const nc_tensor* t) { return t && t->data && is_act(t->dtype); }
+
+static uint8_t* row_ptr(const nc_tensor* t, int r) { return (uint8_t*)t->data + (size_t)r * t->pitch; }
+
+extern "C" {
+
+int nc_rms_norm(const nc_tensor* x, const uint16_t* w, nc_tensor* out, int d_norm, int start, int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(act_ok(x) && act_ok(out) && w, "rms_norm: bad tensor");
+    NC_CHECK_ARG(x->dtype == out->dtype && x->cols == out->cols, "rms_norm: shape/dtype mismatch");
+    NC_CHECK_ARG(start >= 0 && n_ctx <= x->rows && n_ctx <= out->rows, "rms_norm: rows [%d, %d)", start, n_ctx);
+    return norm_launch(kRms, x->dtype, false, row_ptr(x, start), x->pitch, nullptr, 0, 1.0f, nullptr, 0, w, nullptr,
+                       row_ptr(out, start), out->pitch, d_norm, x->cols, n_ctx - start, 1.0f, stream_of(stream));
+}
+
+int nc_layer_norm(const nc_tensor* x, const uint16_t* w, const uint16_t* b, nc_tensor* out, int start, int n_ctx,
+                  void* stream)
+{
+    NC_CHECK_ARG(act_ok(x) && act_ok(out) && w && b, "layer_norm: bad tensor");
+    NC_CHECK_ARG(x->dtype == out->dtype && x->cols == out->cols, "layer_norm: shape/dtype mismatch");
+    NC_CHECK_ARG(start >= 0 && n_ctx <= x->rows && n_ctx <= out->rows, "layer_norm: rows [%d, %d)", start, n_ctx);
+    return norm_launch(kLayerNorm, x->dtype, false, row_ptr(x, start), x->pitch, nullptr, 0, 1.0f, nullptr, 0, w, b,
+                       row_ptr(out, start), out->pitch, x->cols, x->cols, n_ctx - start, 1.0f, stream_of(stream));
+}
+
+int nc_rope_table(int max_ctx, int d_head, float rope_pct, float* out)
+{
+    NC_CHECK_ARG(out && max_ctx > 0 && d_head > 0, "rope_table: bad arguments");
+    const int rope_d = static_cast<int>((float)d_head * rope_pct);
+    const int d_half = rope_d / 2;
+    const float d = static_cast<float>(rope_d);
+    for (int i = 0; i < max_ctx; i++) {
+        const float m = static_cast<float>(i);
+        for (int j = 0; j < d_half; j++) {
+            const float th = m * std::pow(10000.0f, -(2.0f * j / d));
+            out[2 * ((size_t)i * d_half + j)] = std::cos(th);
+            out[2 * ((size_t)i * d_half + j) + 1] = std::sin(th);
+        }
+    }
+    return NC_OK;
+}
+
+int nc_rotary_emb(const nc_tensor* x, nc_tensor* out, int d_head, float rope_pct, const float* table, int start,
+                  int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(act_ok(x) && act_ok(out) && table, "rotary_emb: bad tensor");
+    NC_CHECK_ARG(d_head == 64, "rotary_emb: head size %d (the kernels are built for 64)", d_head);
+    NC_CHECK_ARG(x->dtype == out->dtype && x->cols == out->cols, "rotary_emb: shape/dtype mismatch");
+    NC_CHECK_ARG(start >= 0 && n_ctx <= x->rows && n_ctx <= out->rows, "rotary_emb: rows [%d, %d)", start, n_ctx);
+    const int d_half = static_cast<int>((float)d_head * rope_pct) / 2;
+    return rope_launch(x->dtype, row_ptr(x, start), x->pitch, row_ptr(out, start), out->pitch, x->cols, table, d_half,
+                       start, n_ctx - start, stream_of(stream));
+}
+
+static int ew_api(int op, const nc_tensor* a, const nc_tensor* b, const uint16_t* bias, float s, nc_tensor* out,
+                  int start, int n_ctx, void* stream, const char* name)
+{
+    NC_CHECK_ARG(act_ok(a) && act_ok(out), "%s: bad tensor", name);
+    NC_CHECK_ARG(a->dtype == out->dtype && a->cols == out->cols, "%s: shape/dtype mismatch", name);
+    if (b) NC_CHECK_ARG(act_ok(b) && b->dtype == a->dtype && b->cols == a->cols, "%s: operand mismatch", name);
+    NC_CHECK_ARG(start >= 0 && n_ctx <= a->rows && n_ctx <= out->rows, "%s: rows [%d, %d)", name, start, n_ctx);
+    return ew_launch(op, a->dtype, row_ptr(a, start), a->pitch, b ? row_ptr(b, start) : nullptr, b ? b->pitch : 0,
+                     bias, s, row_ptr(out, start), out->pitch, a->cols, n_ctx - start, stream_of(stream));
+}
+
+int nc_silu(const nc_tensor* x, nc_tensor* out, int start, int n_ctx, void* stream)
+{
+    return ew_api(kSilu, x, nullptr, nullptr, 0.0f, out, start, n_ctx, stream, "silu");
+}
+
+int nc_multiply(const nc_tensor* a, const nc_tensor* b, nc_tensor* out, int start, int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(b, "multiply: null operand");
+    return ew_api(kMul, a, b, nullptr, 0.0f, out, start, n_ctx, stream, "multiply");
+}
+
+int nc_add(const nc_tensor* a, const nc_tensor* b, nc_tensor* out, int start, int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(b, "add: null operand");
+    return ew_api(kAdd, a, b, nullptr, 0.0f, out, start, n_ctx, stream, "add");
+}
+
+int nc_scale(nc_tensor* x, float s, int start, int n_ctx, void* stream)
+{
+    return ew_api(kScale, x, nullptr, nullptr, s, x, start, n_ctx, stream, "scale");
+}
+
+int nc_bias_add(nc_tensor* x, const uint16_t* b, int start, int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(b, "bias_add: null bias");
+    return ew_api(kBias, x, nullptr, b, 0.0f, x, start, n_ctx, stream, "bias_add");
+}
+
+int nc_token_embed(const nc_tensor* table, const int32_t* tokens, nc_tensor* out, int start, int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(table && table->data && tokens && act_ok(out), "token_embed: bad tensor");
+    NC_CHECK_ARG(table->cols == out->cols, "token_embed: width mismatch");
+    NC_CHECK_ARG(start >= 0 && n_ctx <= out->rows, "token_embed: rows [%d, %d)", start, n_ctx);
+    return embed_launch(table, tokens + start, row_ptr(out, start), out->pitch, out->dtype, n_ctx - start, 1.0f,
+                        stream_of(stream));
+}
+
+int nc_argmax(const float* x, int n, int32_t* out, void* stream)
+{
+    NC_CHECK_ARG(x && out && n > 0, "argmax: bad arguments");
+    return argmax_launch(x, n, out, stream_of(stream));
+}
+
+}  // extern "C"
+
+namespace nc {
+__global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = expf_ref(x[i]);
+}
+}  // namespace nc
+
+// The kernels' expf evaluated on the host (the same source), so the
+// algorithm can be checked against the host libm without a GPU.
+extern "C" float nc_expf_host(float x) { return nc::expf_ref(x); }
+
+// The device's std::exp(float) (gten/ops.cpp:752,1072) over an array.
+extern "C" int nc_expf(const float* x, float* y, int64_t n, void* stream)
+{
+    NC_CHECK_ARG(x && y && n >= 0, "expf: bad arguments");
+    if (!n) return NC_OK;
+    hipLaunchKernelGGL(k_expf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream_of(stream), x, y, n);
+    return launch_status("k_expf");
+}

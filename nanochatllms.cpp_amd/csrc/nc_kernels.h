@@ -1,0 +1,49 @@
+// nc_kernels.h -- host-side launchers of the gfx950 kernels (internal API
+// used by the C-ABI ops and the model runtime).
+#pragma once
+
+#include "nc_runtime.h"
+
+namespace nc {
+
+enum NormKindHost { kNormRms = 0, kNormLayer = 1 };
+enum EwOpHost { kEwSilu = 0, kEwMul = 1, kEwAdd = 2, kEwScale = 3, kEwBias = 4 };
+
+// fp32 rows -> activation rows (write_row_from_float).
+int write_rows(const float* in, int in_pitch, uint8_t* out, int out_pitch, int dtype, int cols, int rows,
+               hipStream_t st);
+
+// x rows (pointer at the first row) times weight rows -> fp32 dots.
+int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
+               hipStream_t st);
+
+// Norm over segments of d_norm values; with `add` the input is
+// a + requant(braw) (scaled by bscale and requantized when bscale != 1),
+// stored to h_out.
+int norm_launch(int kind, int adt, bool add, const uint8_t* a, int a_pitch, const float* braw, int b_pitch,
+                float bscale, uint8_t* h_out, int h_pitch, const uint16_t* w, const uint16_t* bias, uint8_t* out,
+                int out_pitch, int d_norm, int row_cols, int rows, float post_scale, hipStream_t st);
+
+int qkv_post_launch(int adt, const float* raw, int raw_pitch, int hq, int hkv, const uint16_t* bq, const uint16_t* bk,
+                    const uint16_t* bv, const uint16_t* qn_w, const uint16_t* kn_w, const float* table, int d_half,
+                    int start, int rows, uint8_t* q_out, int q_pitch, uint8_t* k_cache, int k_pitch,
+                    uint8_t* v_cache, int v_pitch, hipStream_t st);
+
+int silu_mul_launch(int adt, const float* raw, int raw_pitch, int f, uint8_t* out, int out_pitch, int rows,
+                    hipStream_t st);
+
+int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, int out_pitch, int adt, int rows,
+                 float post_scale, hipStream_t st);
+
+int argmax_launch(const float* x, int n, int32_t* out, hipStream_t st);
+
+int ew_launch(int op, int adt, const uint8_t* a, int a_pitch, const uint8_t* b, int b_pitch, const uint16_t* bias,
+              float s, uint8_t* out, int out_pitch, int cols, int rows, hipStream_t st);
+
+int rope_launch(int adt, const uint8_t* in, int in_pitch, uint8_t* out, int out_pitch, int cols, const float* table,
+                int d_half, int start, int rows, hipStream_t st);
+
+int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k_pitch, const uint8_t* vc, int v_pitch,
+                uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st);
+
+}  // namespace nc

@@ -1,0 +1,291 @@
+// nc_matvec.hip -- decode/prefill matrix-vector products for gfx950.
+//
+// Replaces matmul_2d_impl + vec_dot_product_{q8,q8_q4,f16} (gten/ops.cpp:
+// 208-242, 292-490, 579-614).  The reference's AVX dot products fix a
+// summation order that these kernels keep exactly:
+//   Q8/Q4: per 32-value block i, four int32 lane sums L_k(i) over the
+//          elements j with (j mod 8) in {2k, 2k+1}; t_k(i) = float(L_k) *
+//          (d_x * d_w); acc_k = ((0 + t_k(0)) + t_k(1)) + ... in block order;
+//          result (acc_0 + acc_1) + (acc_2 + acc_3).
+//   F16:   eight fp32 lanes (lane = index mod 8), acc_j = x*w + acc_j over
+//          the 8-wide chunks in order, result f0 + f1 + ... + f7 left to right.
+//
+// Q8/Q4 kernel: a 256-thread workgroup owns R weight rows.  Every thread
+// loads whole weight blocks (16 B of Q4 codes or 32 B of Q8 codes, lane-
+// permuted at upload so each lane's 8 codes sit in one or two dwords),
+// computes the four exact integer lane sums with v_dot4 and the four fp32
+// terms, and parks the terms in LDS; then 4R threads each fold one
+// (row, lane) chain in block order.  Loads and integer work are spread over
+// every block of the workgroup's rows; only the cheap fp32 fold is serial.
+// The activation row is staged once per workgroup in LDS with the lane
+// permutation, its per-lane code sums (for the Q4 "-7" offset) and delta.
+// Weights are held in registers across activation rows, so prefill reads
+// every weight once per launch.
+//
+// F16 kernel: thread = (row, lane j); each thread reads 16-byte runs of its
+// own lane (the weight layout interleaves 64-column groups over 8-row
+// groups, so a wavefront reads 1 KiB contiguous) and folds its chain in
+// order; the eight lanes of a row meet through wavefront shuffles.
+#include "nc_device.h"
+#include "nc_kernels.h"
+
+namespace nc {
+
+constexpr int kMvThreads = 256;
+constexpr int kMvMaxItems = 4;  // weight blocks per thread held in registers
+
+__device__ __forceinline__ uint32_t pick_pair(uint32_t lo, uint32_t hi, int odd)
+{
+    // bytes (2*odd, 2*odd+1) of lo followed by the same bytes of hi
+    return odd ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
+}
+
+// Stage block i of a Q8 activation row: 16 dwords
+// [xa0 xb0 xa1 xb1 xa2 xb2 xa3 xb3 | c0 c1 c2 c3 | dx 0 0 0]
+// xa_k = codes {2k,2k+1,2k+8,2k+9}, xb_k = codes {2k+16,2k+17,2k+24,2k+25},
+// c_k = -7 * (sum of those eight codes).
+__device__ __forceinline__ void stage_x_block(const uint8_t* xrow, int nb, int i, uint32_t* dst)
+{
+    const uint4* q = reinterpret_cast<const uint4*>(xrow + (size_t)i * 32);
+    const uint4 a = q[0], b = q[1];
+    const uint32_t X[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const uint16_t d16 = reinterpret_cast<const uint16_t*>(xrow + (size_t)nb * 32)[i];
+    uint32_t o[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t xa = pick_pair(X[k >> 1], X[2 + (k >> 1)], k & 1);
+        const uint32_t xb = pick_pair(X[4 + (k >> 1)], X[6 + (k >> 1)], k & 1);
+        o[2 * k] = xa;
+        o[2 * k + 1] = xb;
+        const int s = __builtin_amdgcn_sdot4((int)xa, 0x01010101, __builtin_amdgcn_sdot4((int)xb, 0x01010101, 0, false),
+                                             false);
+        o[8 + k] = (uint32_t)(-7 * s);
+    }
+    o[12] = __float_as_uint(h2f(d16));
+    o[13] = o[14] = o[15] = 0;
+    uint4* d = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+    for (int v = 0; v < 4; v++) d[v] = make_uint4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
+}
+
+template <int WT, int R>
+__global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restrict__ x, int x_pitch, int n_xrows,
+                                                        const uint32_t* __restrict__ wq,
+                                                        const uint16_t* __restrict__ wd, float* __restrict__ out,
+                                                        int out_pitch, int N, int nb)
+{
+    constexpr int WD = WT == Q4 ? 4 : 8;  // code dwords per block
+    extern __shared__ __align__(16) uint32_t lds[];
+    uint32_t* xs = lds;
+    const int tp = ((nb + 3) & ~3) + 4;
+    float* T = reinterpret_cast<float*>(lds + nb * 16);
+    const int tid = threadIdx.x;
+    const int row0 = blockIdx.x * R;
+    const int nitems = R * nb;
+
+    uint32_t w[kMvMaxItems][WD];
+    float dw[kMvMaxItems];
+    int tix[kMvMaxItems], bix[kMvMaxItems];
+#pragma unroll
+    for (int it = 0; it < kMvMaxItems; it++) {
+        const int j = tid + it * kMvThreads;
+        tix[it] = -1;
+        bix[it] = 0;
+        dw[it] = 0.0f;
+#pragma unroll
+        for (int v = 0; v < WD; v++) w[it][v] = 0;
+        if (j < nitems) {
+            const int r = j / nb, i = j - r * nb;
+            if (row0 + r < N) {
+                const size_t b = (size_t)(row0 + r) * nb + i;
+                const uint4* src = reinterpret_cast<const uint4*>(wq + b * WD);
+#pragma unroll
+                for (int v = 0; v < WD / 4; v++) {
+                    const uint4 u = src[v];
+                    w[it][4 * v] = u.x;
+                    w[it][4 * v + 1] = u.y;
+                    w[it][4 * v + 2] = u.z;
+                    w[it][4 * v + 3] = u.w;
+                }
+                dw[it] = h2f(wd[b]);
+                tix[it] = r * 4 * tp + i;
+                bix[it] = i;
+            }
+        }
+    }
+
+    for (int p = 0; p < n_xrows; p++) {
+        const uint8_t* xr = x + (size_t)p * x_pitch;
+        for (int i = tid; i < nb; i += kMvThreads) stage_x_block(xr, nb, i, xs + i * 16);
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < kMvMaxItems; it++) {
+            if (tix[it] < 0) continue;
+            const uint4* s = reinterpret_cast<const uint4*>(xs + bix[it] * 16);
+            const uint4 s0 = s[0], s1 = s[1], s2 = s[2], s3 = s[3];
+            const uint32_t xa[4] = {s0.x, s0.z, s1.x, s1.z};
+            const uint32_t xb[4] = {s0.y, s0.w, s1.y, s1.w};
+            const int c[4] = {(int)s2.x, (int)s2.y, (int)s2.z, (int)s2.w};
+            const float dd = __uint_as_float(s3.x) * dw[it];
+            float* t = T + tix[it];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                int L;
+                if (WT == Q4) {
+                    const uint32_t P = w[it][k];
+                    L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)xa[k], c[k], false);
+                    L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)xb[k], L, false);
+                } else {
+                    L = __builtin_amdgcn_sdot4((int)w[it][2 * k], (int)xa[k], 0, false);
+                    L = __builtin_amdgcn_sdot4((int)w[it][2 * k + 1], (int)xb[k], L, false);
+                }
+                t[k * tp] = (float)L * dd;
+            }
+        }
+        __syncthreads();
+        if (tid < kWave) {
+            float acc = 0.0f;
+            if (tid < 4 * R) acc = seq_sum(T + tid * tp, nb);
+            const int g = tid & ~3;
+            const float a0 = __shfl(acc, g), a1 = __shfl(acc, g + 1), a2 = __shfl(acc, g + 2), a3 = __shfl(acc, g + 3);
+            const float res = (a0 + a1) + (a2 + a3);
+            const int row = row0 + (tid >> 2);
+            if (tid < 4 * R && (tid & 3) == 0 && row < N) out[(size_t)p * out_pitch + row] = res;
+        }
+        __syncthreads();
+    }
+}
+
+// F16: 8 rows x 8 lanes per wavefront, 32 rows per workgroup.
+__global__ __launch_bounds__(kMvThreads) void k_matvec_f16(const uint8_t* __restrict__ x, int x_pitch, int n_xrows,
+                                                          const uint16_t* __restrict__ w, float* __restrict__ out,
+                                                          int out_pitch, int N, int K)
+{
+    extern __shared__ __align__(16) float xsf[];  // [K/64][8 lanes][8]
+    const int tid = threadIdx.x;
+    const int j = tid & 7;
+    const int row = blockIdx.x * 32 + (tid >> 3);
+    const int G = K / 64;
+    const int npad = (N + 7) & ~7;
+    const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)row * 8 + j;  // group 0
+    const size_t gstride = (size_t)npad * 8;                                        // uint4s per group
+
+    for (int p = 0; p < n_xrows; p++) {
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(x + (size_t)p * x_pitch);
+        for (int e = tid; e < K; e += kMvThreads) {
+            const int g = e >> 6, m = (e >> 3) & 7, jj = e & 7;
+            xsf[(g * 8 + jj) * 8 + m] = h2f(xr[e]);
+        }
+        __syncthreads();
+        float acc = 0.0f;
+        if (row < N) {
+            for (int g = 0; g < G; g++) {
+                const uint4 u = wrow[(size_t)g * gstride];
+                const float4 xa = *reinterpret_cast<const float4*>(xsf + (g * 8 + j) * 8);
+                const float4 xb = *reinterpret_cast<const float4*>(xsf + (g * 8 + j) * 8 + 4);
+                const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+                const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                for (int m = 0; m < 8; m++) {
+                    const uint16_t h = (uint16_t)(m & 1 ? wv[m >> 1] >> 16 : wv[m >> 1] & 0xFFFFu);
+                    acc = xv[m] * h2f(h) + acc;
+                }
+            }
+        }
+        const int base = tid & ~7;
+        float s = __shfl(acc, base);
+#pragma unroll
+        for (int l = 1; l < 8; l++) s = s + __shfl(acc, base + l);
+        if (j == 0 && row < N) out[(size_t)p * out_pitch + row] = s;
+        __syncthreads();
+    }
+}
+
+// out[r, c] = dot(x[r], w[c]) for x rows [0, n_rows) (pointers already at
+// the first row), fp32 out with `out_pitch` floats per row.
+int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
+               hipStream_t st)
+{
+    const int N = w->rows, K = w->cols;
+    if (w->dtype == NC_Q4 || w->dtype == NC_Q8) {
+        if (x_dtype != NC_Q8) return fail(NC_ERR_ARG, "matmul: Q%d weights need Q8 activations", w->dtype == NC_Q4 ? 4 : 8);
+        if (K % 32) return fail(NC_ERR_ARG, "matmul: K=%d is not a multiple of 32", K);
+        const int nb = K / 32;
+        constexpr int R = 4;
+        if (R * nb > kMvThreads * kMvMaxItems) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);
+        const int tp = ((nb + 3) & ~3) + 4;
+        const size_t lds = (size_t)nb * 64 + (size_t)R * 4 * tp * 4;
+        const dim3 grid((N + R - 1) / R);
+        if (w->dtype == NC_Q4)
+            hipLaunchKernelGGL((k_matvec_q<Q4, R>), grid, dim3(kMvThreads), lds, st, x, x_pitch, n_rows,
+                               (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+        else
+            hipLaunchKernelGGL((k_matvec_q<Q8, R>), grid, dim3(kMvThreads), lds, st, x, x_pitch, n_rows,
+                               (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+        return launch_status("k_matvec_q");
+    }
+    if (w->dtype == NC_F16) {
+        if (x_dtype != NC_F16) return fail(NC_ERR_ARG, "matmul: F16 weights need F16 activations");
+        if (K % 64) return fail(NC_ERR_ARG, "matmul: F16 path needs K %% 64 == 0, K=%d", K);
+        const size_t lds = (size_t)K * 4;
+        if (lds > 64 * 1024) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);
+        const dim3 grid((N + 31) / 32);
+        hipLaunchKernelGGL(k_matvec_f16, grid, dim3(kMvThreads), lds, st, x, x_pitch, n_rows,
+                           (const uint16_t*)w->data, out, out_pitch, N, K);
+        return launch_status("k_matvec_f16");
+    }
+    return fail(NC_ERR_ARG, "matmul: weight dtype %d", w->dtype);
+}
+
+}  // namespace nc
+
+// ================================================================ C-ABI ==
+
+using namespace nc;
+
+namespace {
+
+// Library-owned fp32 staging for matmul_2d calls whose output is an
+// activation dtype (grown on demand, never inside a captured graph).
+float* g_stage = nullptr;
+size_t g_stage_bytes = 0;
+
+int stage_buffer(size_t bytes, float** out)
+{
+    if (bytes > g_stage_bytes) {
+        if (g_stage) (void)hipFree(g_stage);
+        g_stage = nullptr;
+        g_stage_bytes = 0;
+        hipError_t e = hipMalloc(&g_stage, bytes);
+        if (e != hipSuccess) return fail(NC_ERR_NOMEM, "matmul staging (%zu bytes): %s", bytes, hipGetErrorString(e));
+        g_stage_bytes = bytes;
+    }
+    *out = g_stage;
+    return NC_OK;
+}
+
+}  // namespace
+
+extern "C" int nc_matmul_2d(const nc_tensor* x, const nc_tensor* w, nc_tensor* out, int start, int n_ctx, void* stream)
+{
+    NC_CHECK_ARG(x && w && out && x->data && w->data && out->data, "matmul_2d: null tensor");
+    NC_CHECK_ARG(x->cols == w->cols, "matmul_2d: x has %d columns, w has %d", x->cols, w->cols);
+    NC_CHECK_ARG(out->cols == w->rows, "matmul_2d: out has %d columns, w has %d rows", out->cols, w->rows);
+    NC_CHECK_ARG(start >= 0 && start <= n_ctx && n_ctx <= x->rows && n_ctx <= out->rows, "matmul_2d: rows [%d, %d)",
+                 start, n_ctx);
+    const int rows = n_ctx - start;
+    if (rows == 0) return NC_OK;
+    hipStream_t st = stream_of(stream);
+    const uint8_t* xr = (const uint8_t*)x->data + (size_t)start * x->pitch;
+    if (out->dtype == NC_F32) {
+        NC_CHECK_ARG(out->pitch % 4 == 0, "matmul_2d: fp32 pitch %d", out->pitch);
+        return matvec_raw(xr, x->dtype, x->pitch, rows, w, (float*)((uint8_t*)out->data + (size_t)start * out->pitch),
+                          out->pitch / 4, st);
+    }
+    float* stage;
+    int s = stage_buffer((size_t)rows * w->rows * 4, &stage);
+    if (s) return s;
+    if ((s = matvec_raw(xr, x->dtype, x->pitch, rows, w, stage, w->rows, st))) return s;
+    return write_rows(stage, w->rows, (uint8_t*)out->data + (size_t)start * out->pitch, out->pitch, out->dtype, w->rows,
+                      rows, st);
+}

@@ -1,0 +1,612 @@
+// nc_model.cpp -- the reference's decoder models on one MI355X.
+//
+// One class covers the four model families of the reference (tinyllama/,
+// zephyr/, minicpm/, openelm/): they share the pre-norm block structure and
+// differ in the norm kind, qkv bias, partial RoPE, QK norm, tied embeddings,
+// per-layer widths and MiniCPM's scalings.  The dataflow and every
+// requantization point follow the reference's block forwards
+// (tinyllama/tinyllama.cpp:88-138, zephyr/zephyr.cpp:24-76,
+// minicpm/minicpm.cpp:42-110, openelm/openelm.cpp:33-146); the kernels fuse
+// neighbouring ops but reproduce each intermediate write/read of the
+// activation dtype.
+//
+// HBM layout per model:
+//   weights: q|k|v rows and gate|up rows stored as one fused matrix each
+//            (one matvec launch), o and down separate, norms fp16;
+//   per layer: K and V caches [max_ctx, kv_dim] and the two residual stream
+//            outputs [max_ctx, d] in the activation dtype (rows = positions);
+//   scratch shared by the layers for the rows being processed.
+// Decode keeps the token stream on the device: argmax writes the next token
+// where the next step's embedding reads it, so steps need no host round trip.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+#include "nc_kernels.h"
+
+namespace nc {
+
+namespace {
+
+struct Layer {
+    int hq, hkv, qd, kvd, f;
+    nc_tensor qkv{}, o{}, gu{}, down{};
+    uint16_t *attn_norm = nullptr, *attn_norm_b = nullptr, *mlp_norm = nullptr, *mlp_norm_b = nullptr;
+    uint16_t *bq = nullptr, *bk = nullptr, *bv = nullptr, *qn = nullptr, *kn = nullptr;
+    uint8_t *kc = nullptr, *vc = nullptr, *res1 = nullptr, *res2 = nullptr;
+};
+
+__global__ void k_fill_u16(uint16_t* p, uint16_t v, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void k_f32_to_f16(const float* in, uint16_t* out, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = __builtin_bit_cast(uint16_t, (_Float16)in[i]);
+}
+
+// fp32 rows -> rows [row_off, row_off + rows) of an F16 weight of npad rows.
+__global__ void k_f16_rows(const float* __restrict__ w, int rows, int cols, int row_off, int npad,
+                           uint16_t* __restrict__ out)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)rows * cols) return;
+    const int r = (int)(i / cols), c = (int)(i - (int64_t)r * cols);
+    const int g = c >> 6, m = (c >> 3) & 7, j = c & 7;
+    out[(((size_t)g * npad + row_off + r) * 8 + j) * 8 + m] = __builtin_bit_cast(uint16_t, (_Float16)w[i]);
+}
+
+}  // namespace
+
+class Decoder {
+public:
+    nc_model_config cfg{};
+    int adt = NC_Q8;
+    int d = 0;
+    hipStream_t st = nullptr;
+    std::vector<void*> allocs;
+    nc_tensor emb{}, lm{};
+    uint16_t *norm_w = nullptr, *norm_b = nullptr;
+    std::vector<Layer> L;
+    float* rope = nullptr;
+    int d_half = 0;
+    uint8_t *x0 = nullptr, *xn = nullptr, *q_act = nullptr, *attn = nullptr, *m_act = nullptr;
+    float *qkv_raw = nullptr, *o_raw = nullptr, *gu_raw = nullptr, *down_raw = nullptr, *logits = nullptr;
+    int32_t* tokens = nullptr;
+    int n_cur = 0;        // tokens in the sequence processed so far
+    int n_prompt = 0;     // prompt length of the current generation
+    int max_qkv = 0, max_qd = 0, max_f = 0;
+
+    ~Decoder()
+    {
+        for (void* p : allocs) (void)hipFree(p);
+    }
+
+    bool tied() const { return cfg.arch == NC_ARCH_MINICPM || cfg.arch == NC_ARCH_OPENELM; }
+    int pitch(int cols) const { return act_pitch(adt, cols); }
+
+    int alloc(void** p, size_t bytes)
+    {
+        int s = nc_malloc(p, bytes ? bytes : 16);
+        if (s) return s;
+        allocs.push_back(*p);
+        hipError_t e = hipMemsetAsync(*p, 0, bytes ? bytes : 16, st);
+        return e == hipSuccess ? NC_OK : hip_fail(e, "hipMemsetAsync");
+    }
+    template <class T>
+    int alloc_t(T** p, size_t bytes)
+    {
+        void* v;
+        int s = alloc(&v, bytes);
+        *p = static_cast<T*>(v);
+        return s;
+    }
+
+    int alloc_weight(nc_tensor* t, int dtype, int rows, int cols)
+    {
+        size_t cb, db;
+        int s = nc_weight_bytes(dtype, rows, cols, &cb, &db);
+        if (s) return s;
+        t->dtype = dtype;
+        t->rows = rows;
+        t->cols = cols;
+        t->pitch = 0;
+        if ((s = alloc(&t->data, cb))) return s;
+        if (db && (s = alloc(&t->deltas, db))) return s;
+        return NC_OK;
+    }
+
+    int create(const nc_model_config* c)
+    {
+        cfg = *c;
+        NC_CHECK_ARG(c->wdtype == NC_F16 || c->wdtype == NC_Q8 || c->wdtype == NC_Q4, "model: weight dtype %d",
+                     c->wdtype);
+        NC_CHECK_ARG(c->n_layers > 0 && c->n_layers <= NC_MAX_LAYERS, "model: %d layers", c->n_layers);
+        NC_CHECK_ARG(c->d_head == 64, "model: head size %d (kernels are built for 64)", c->d_head);
+        NC_CHECK_ARG(c->n_embd % 64 == 0 && c->max_ctx > 0 && c->n_vocab > 0, "model: bad shape");
+        NC_CHECK_ARG(c->arch >= NC_ARCH_LLAMA && c->arch <= NC_ARCH_OPENELM, "model: arch %d", c->arch);
+        if (!initialized()) {
+            int s = nc_init(0);
+            if (s) return s;
+        }
+        st = stream_of(nullptr);
+        adt = c->wdtype == NC_F16 ? NC_F16 : NC_Q8;
+        d = c->n_embd;
+        const int mc = c->max_ctx;
+        int s;
+        if ((s = alloc_weight(&emb, c->wdtype, c->n_vocab, d))) return s;
+        if (!tied() && (s = alloc_weight(&lm, c->wdtype, c->n_vocab, d))) return s;
+        if ((s = alloc_t(&norm_w, (size_t)d * 2))) return s;
+        if (c->arch == NC_ARCH_ZEPHYR && (s = alloc_t(&norm_b, (size_t)d * 2))) return s;
+        L.resize(c->n_layers);
+        for (int l = 0; l < c->n_layers; l++) {
+            Layer& y = L[l];
+            y.hq = c->n_heads[l];
+            y.hkv = c->n_kv_heads[l];
+            y.f = c->n_ffn[l];
+            NC_CHECK_ARG(y.hq > 0 && y.hkv > 0 && y.hq % y.hkv == 0 && y.f % 64 == 0, "model: layer %d shape", l);
+            y.qd = y.hq * 64;
+            y.kvd = y.hkv * 64;
+            max_qkv = std::max(max_qkv, y.qd + 2 * y.kvd);
+            max_qd = std::max(max_qd, y.qd);
+            max_f = std::max(max_f, y.f);
+            if ((s = alloc_weight(&y.qkv, c->wdtype, y.qd + 2 * y.kvd, d))) return s;
+            if ((s = alloc_weight(&y.o, c->wdtype, d, y.qd))) return s;
+            if ((s = alloc_weight(&y.gu, c->wdtype, 2 * y.f, d))) return s;
+            if ((s = alloc_weight(&y.down, c->wdtype, d, y.f))) return s;
+            if ((s = alloc_t(&y.attn_norm, (size_t)d * 2)) || (s = alloc_t(&y.mlp_norm, (size_t)d * 2))) return s;
+            if (c->arch == NC_ARCH_ZEPHYR) {
+                if ((s = alloc_t(&y.attn_norm_b, (size_t)d * 2)) || (s = alloc_t(&y.mlp_norm_b, (size_t)d * 2))) return s;
+                if ((s = alloc_t(&y.bq, (size_t)y.qd * 2)) || (s = alloc_t(&y.bk, (size_t)y.kvd * 2)) ||
+                    (s = alloc_t(&y.bv, (size_t)y.kvd * 2)))
+                    return s;
+            }
+            if (c->arch == NC_ARCH_OPENELM)
+                if ((s = alloc_t(&y.qn, 128)) || (s = alloc_t(&y.kn, 128))) return s;
+            if ((s = alloc_t(&y.kc, (size_t)mc * pitch(y.kvd))) || (s = alloc_t(&y.vc, (size_t)mc * pitch(y.kvd))))
+                return s;
+            if ((s = alloc_t(&y.res1, (size_t)mc * pitch(d))) || (s = alloc_t(&y.res2, (size_t)mc * pitch(d)))) return s;
+        }
+        if ((s = alloc_t(&x0, (size_t)mc * pitch(d))) || (s = alloc_t(&xn, (size_t)mc * pitch(d))) ||
+            (s = alloc_t(&q_act, (size_t)mc * pitch(max_qd))) || (s = alloc_t(&attn, (size_t)mc * pitch(max_qd))) ||
+            (s = alloc_t(&m_act, (size_t)mc * pitch(max_f))) ||
+            (s = alloc_t(&qkv_raw, (size_t)mc * max_qkv * 4)) || (s = alloc_t(&o_raw, (size_t)mc * d * 4)) ||
+            (s = alloc_t(&gu_raw, (size_t)mc * 2 * max_f * 4)) || (s = alloc_t(&down_raw, (size_t)mc * d * 4)) ||
+            (s = alloc_t(&logits, (size_t)c->n_vocab * 4)) || (s = alloc_t(&tokens, (size_t)(mc + 1) * 4)))
+            return s;
+        // RoPE table from the host libm, the reference's expression
+        d_half = static_cast<int>((float)c->d_head * c->rope_pct) / 2;
+        std::vector<float> tab((size_t)mc * std::max(d_half, 1) * 2);
+        if ((s = nc_rope_table(mc, c->d_head, c->rope_pct, tab.data()))) return s;
+        if ((s = alloc_t(&rope, tab.size() * 4))) return s;
+        hipError_t e = hipMemcpyAsync(rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        return e == hipSuccess ? NC_OK : hip_fail(e, "rope table upload");
+    }
+
+    // ------------------------------------------------------------ weights --
+
+    // Location of weight (layer, slot): the fused matrix and its row offset,
+    // or an fp16 vector.
+    struct Loc {
+        nc_tensor* mat = nullptr;
+        int row_off = 0, rows = 0, cols = 0;
+        uint16_t* vec = nullptr;
+        int n = 0;
+        int kind = 0;  // 0 matrix, 1 gain (1.0), 2 zero bias, 3 random fp16 vector
+    };
+
+    int locate(int layer, int slot, Loc* o)
+    {
+        *o = Loc{};
+        if (layer < 0) {
+            switch ((unsigned)slot) {
+            case NC_TID_EMB: o->mat = &emb; o->rows = cfg.n_vocab; o->cols = d; return NC_OK;
+            case NC_TID_LM:
+                if (tied()) return fail(NC_ERR_ARG, "model: lm head is tied to the embedding");
+                o->mat = &lm; o->rows = cfg.n_vocab; o->cols = d; return NC_OK;
+            case NC_TID_NORM: o->vec = norm_w; o->n = d; o->kind = 1; return NC_OK;
+            case NC_TID_NORM_B:
+                if (!norm_b) return fail(NC_ERR_ARG, "model: no final norm bias");
+                o->vec = norm_b; o->n = d; o->kind = 2; return NC_OK;
+            default: return fail(NC_ERR_ARG, "model: global slot %#x", (unsigned)slot);
+            }
+        }
+        NC_CHECK_ARG(layer < cfg.n_layers, "model: layer %d", layer);
+        Layer& y = L[layer];
+        switch (slot) {
+        case NC_W_Q: o->mat = &y.qkv; o->rows = y.qd; o->cols = d; return NC_OK;
+        case NC_W_K: o->mat = &y.qkv; o->row_off = y.qd; o->rows = y.kvd; o->cols = d; return NC_OK;
+        case NC_W_V: o->mat = &y.qkv; o->row_off = y.qd + y.kvd; o->rows = y.kvd; o->cols = d; return NC_OK;
+        case NC_W_O: o->mat = &y.o; o->rows = d; o->cols = y.qd; return NC_OK;
+        case NC_W_GATE: o->mat = &y.gu; o->rows = y.f; o->cols = d; return NC_OK;
+        case NC_W_UP: o->mat = &y.gu; o->row_off = y.f; o->rows = y.f; o->cols = d; return NC_OK;
+        case NC_W_DOWN: o->mat = &y.down; o->rows = d; o->cols = y.f; return NC_OK;
+        case NC_W_ATTN_NORM: o->vec = y.attn_norm; o->n = d; o->kind = 1; return NC_OK;
+        case NC_W_MLP_NORM: o->vec = y.mlp_norm; o->n = d; o->kind = 1; return NC_OK;
+        case NC_W_ATTN_NORM_B: o->vec = y.attn_norm_b; o->n = d; o->kind = 2; break;
+        case NC_W_MLP_NORM_B: o->vec = y.mlp_norm_b; o->n = d; o->kind = 2; break;
+        case NC_W_Q_BIAS: o->vec = y.bq; o->n = y.qd; o->kind = 3; break;
+        case NC_W_K_BIAS: o->vec = y.bk; o->n = y.kvd; o->kind = 3; break;
+        case NC_W_V_BIAS: o->vec = y.bv; o->n = y.kvd; o->kind = 3; break;
+        case NC_W_Q_NORM: o->vec = y.qn; o->n = 64; o->kind = 1; break;
+        case NC_W_K_NORM: o->vec = y.kn; o->n = 64; o->kind = 1; break;
+        default: return fail(NC_ERR_ARG, "model: slot %d", slot);
+        }
+        if (!o->vec) return fail(NC_ERR_ARG, "model: this architecture has no slot %d", slot);
+        return NC_OK;
+    }
+
+    // Byte offsets of the sub-matrix in a fused Q4/Q8 weight.
+    static size_t code_off(const nc_tensor* m, int row_off)
+    {
+        return (size_t)row_off * (m->cols / 32) * (m->dtype == NC_Q8 ? 32 : 16);
+    }
+
+    int init_synthetic(uint64_t seed)
+    {
+        size_t max_n = (size_t)cfg.n_vocab * d;
+        for (const Layer& y : L)
+            max_n = std::max(max_n, std::max((size_t)2 * y.f * d, (size_t)(y.qd + 2 * y.kvd) * d));
+        float* tmp = nullptr;
+        int s = nc_malloc((void**)&tmp, max_n * 4);
+        if (s) return s;
+        std::unique_ptr<void, void (*)(void*)> guard(tmp, [](void* p) { (void)hipFree(p); });
+        auto one = [&](int layer, int slot) -> int {
+            Loc o;
+            int r = locate(layer, slot, &o);
+            if (r) return NC_OK;  // slot not present in this architecture
+            const uint32_t tid = layer < 0 ? (uint32_t)slot : (uint32_t)(layer * 32 + slot);
+            if (o.mat) {
+                const int64_t n = (int64_t)o.rows * o.cols;
+                if ((r = nc_gen_normal(seed, tid, 0.02f, n, tmp, st))) return r;
+                if (o.mat->dtype == NC_F16) {
+                    hipLaunchKernelGGL(k_f16_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, tmp, o.rows,
+                                       o.cols, o.row_off, (o.mat->rows + 7) & ~7, (uint16_t*)o.mat->data);
+                    return launch_status("k_f16_rows");
+                }
+                nc_tensor sub = *o.mat;
+                sub.rows = o.rows;
+                sub.data = (uint8_t*)o.mat->data + code_off(o.mat, o.row_off);
+                sub.deltas = (uint16_t*)o.mat->deltas + (size_t)o.row_off * (o.cols / 32);
+                return nc_weight_quantize(tmp, &sub, st);
+            }
+            const unsigned grid = (unsigned)((o.n + 255) / 256);
+            if (o.kind == 3) {
+                if ((r = nc_gen_normal(seed, tid, 0.02f, o.n, tmp, st))) return r;
+                hipLaunchKernelGGL(k_f32_to_f16, dim3(grid), dim3(256), 0, st, tmp, o.vec, (int64_t)o.n);
+            } else {
+                hipLaunchKernelGGL(k_fill_u16, dim3(grid), dim3(256), 0, st, o.vec,
+                                   (uint16_t)(o.kind == 1 ? 0x3C00u : 0u), (int64_t)o.n);
+            }
+            return launch_status("weight fill");
+        };
+        const unsigned globals[4] = {NC_TID_EMB, NC_TID_NORM, NC_TID_NORM_B, NC_TID_LM};
+        for (unsigned g : globals)
+            if ((s = one(-1, (int)g))) return s;
+        for (int l = 0; l < cfg.n_layers; l++)
+            for (int slot = 0; slot <= NC_W_K_NORM; slot++)
+                if ((s = one(l, slot))) return s;
+        hipError_t e = hipStreamSynchronize(st);
+        return e == hipSuccess ? NC_OK : hip_fail(e, "init_synthetic");
+    }
+
+    int set_weight(int layer, int slot, const void* ref, size_t n_bytes)
+    {
+        Loc o;
+        int s = locate(layer, slot, &o);
+        if (s) return s;
+        hipError_t e = hipSuccess;
+        if (o.vec) {
+            NC_CHECK_ARG(n_bytes == (size_t)o.n * 2, "set_weight: %zu bytes for %d fp16 values", n_bytes, o.n);
+            e = hipMemcpy(o.vec, ref, n_bytes, hipMemcpyHostToDevice);
+            return e == hipSuccess ? NC_OK : hip_fail(e, "set_weight");
+        }
+        const int dt = o.mat->dtype;
+        const size_t want = dt == NC_F16 ? (size_t)o.rows * o.cols * 2
+                                         : (size_t)o.rows * (o.cols / 32) * (dt == NC_Q8 ? 34 : 18);
+        NC_CHECK_ARG(n_bytes == want, "set_weight: payload %zu bytes, expected %zu", n_bytes, want);
+        if (dt == NC_F16) {
+            // per 64-column group, the sub-matrix rows are one contiguous run
+            const int npad = (o.mat->rows + 7) & ~7, G = o.cols / 64;
+            const uint16_t* src = static_cast<const uint16_t*>(ref);
+            std::vector<uint16_t> run((size_t)o.rows * 64);
+            for (int g = 0; g < G && e == hipSuccess; g++) {
+                for (int r = 0; r < o.rows; r++)
+                    for (int m = 0; m < 8; m++)
+                        for (int j = 0; j < 8; j++) run[((size_t)r * 8 + j) * 8 + m] = src[(size_t)r * o.cols + 64 * g + 8 * m + j];
+                e = hipMemcpy((uint16_t*)o.mat->data + ((size_t)g * npad + o.row_off) * 64, run.data(), run.size() * 2,
+                              hipMemcpyHostToDevice);
+            }
+            return e == hipSuccess ? NC_OK : hip_fail(e, "set_weight");
+        }
+        size_t cb, db;
+        if ((s = nc_weight_bytes(dt, o.rows, o.cols, &cb, &db))) return s;
+        std::vector<uint8_t> codes(cb), deltas(db);
+        if ((s = nc_weight_from_reference(ref, dt, o.rows, o.cols, codes.data(), deltas.data()))) return s;
+        e = hipMemcpy((uint8_t*)o.mat->data + code_off(o.mat, o.row_off), codes.data(), cb, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy((uint16_t*)o.mat->deltas + (size_t)o.row_off * (o.cols / 32), deltas.data(), db,
+                          hipMemcpyHostToDevice);
+        return e == hipSuccess ? NC_OK : hip_fail(e, "set_weight");
+    }
+
+    // Inverse of set_weight: the stored weight in the reference's bytes.
+    int get_weight(int layer, int slot, void* ref, size_t n_bytes)
+    {
+        Loc o;
+        int s = locate(layer, slot, &o);
+        if (s) return s;
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "get_weight");
+        if (o.vec) {
+            NC_CHECK_ARG(n_bytes == (size_t)o.n * 2, "get_weight: %zu bytes for %d fp16 values", n_bytes, o.n);
+            e = hipMemcpy(ref, o.vec, n_bytes, hipMemcpyDeviceToHost);
+            return e == hipSuccess ? NC_OK : hip_fail(e, "get_weight");
+        }
+        const int dt = o.mat->dtype;
+        const size_t want = dt == NC_F16 ? (size_t)o.rows * o.cols * 2
+                                         : (size_t)o.rows * (o.cols / 32) * (dt == NC_Q8 ? 34 : 18);
+        NC_CHECK_ARG(n_bytes == want, "get_weight: buffer %zu bytes, expected %zu", n_bytes, want);
+        uint8_t* out = static_cast<uint8_t*>(ref);
+        if (dt == NC_F16) {
+            const int npad = (o.mat->rows + 7) & ~7, G = o.cols / 64;
+            std::vector<uint16_t> run((size_t)o.rows * 64);
+            uint16_t* dst = reinterpret_cast<uint16_t*>(out);
+            for (int g = 0; g < G; g++) {
+                e = hipMemcpy(run.data(), (uint16_t*)o.mat->data + ((size_t)g * npad + o.row_off) * 64, run.size() * 2,
+                              hipMemcpyDeviceToHost);
+                if (e != hipSuccess) return hip_fail(e, "get_weight");
+                for (int r = 0; r < o.rows; r++)
+                    for (int m = 0; m < 8; m++)
+                        for (int j = 0; j < 8; j++) dst[(size_t)r * o.cols + 64 * g + 8 * m + j] = run[((size_t)r * 8 + j) * 8 + m];
+            }
+            return NC_OK;
+        }
+        size_t cb, db;
+        if ((s = nc_weight_bytes(dt, o.rows, o.cols, &cb, &db))) return s;
+        std::vector<uint8_t> codes(cb);
+        std::vector<uint16_t> deltas(db / 2);
+        e = hipMemcpy(codes.data(), (uint8_t*)o.mat->data + code_off(o.mat, o.row_off), cb, hipMemcpyDeviceToHost);
+        if (e == hipSuccess)
+            e = hipMemcpy(deltas.data(), (uint16_t*)o.mat->deltas + (size_t)o.row_off * (o.cols / 32), db,
+                          hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(e, "get_weight");
+        const size_t nblk = db / 2;
+        for (size_t b = 0; b < nblk; b++) {
+            if (dt == NC_Q8) {
+                uint8_t* blk = out + b * 34;
+                std::memcpy(blk, &deltas[b], 2);
+                for (int el = 0; el < 32; el++) {
+                    const int k = (el & 7) >> 1, pos = (el & 1) + (((el & 15) >> 3) << 1);
+                    blk[2 + el] = codes[b * 32 + (2 * k + (el >> 4)) * 4 + pos];
+                }
+            } else {
+                uint8_t* blk = out + b * 18;
+                std::memcpy(blk, &deltas[b], 2);
+                for (int j = 0; j < 16; j++) {
+                    const int k = (j & 7) >> 1, pos = (j & 1) + ((j >> 3) << 1);
+                    blk[2 + j] = codes[b * 16 + k * 4 + pos];
+                }
+            }
+        }
+        return NC_OK;
+    }
+
+    // ------------------------------------------------------------ forward --
+
+    int norm_kind() const { return cfg.arch == NC_ARCH_ZEPHYR ? kNormLayer : kNormRms; }
+    float branch_scale() const
+    {
+        // MiniCPMConfig::scale_depth / std::sqrt(n_layers) with the reference's
+        // constants (minicpm/minicpm.h:14,19; minicpm/minicpm.cpp:57)
+        return cfg.arch == NC_ARCH_MINICPM ? (float)((double)1.4f / std::sqrt(40.0)) : 1.0f;
+    }
+
+    // Model::logits for rows [sp, n): tokens already on the device.  The
+    // last row's logits land in `logits`.
+    int forward(int sp, int n)
+    {
+        const int R = n - sp;
+        const int pd = pitch(d);
+        const bool minicpm = cfg.arch == NC_ARCH_MINICPM;
+        const float bs = branch_scale();
+        int s;
+        // embedding (+ MiniCPM's x12, minicpm.cpp:96)
+        if ((s = embed_launch(&emb, tokens + sp, x0 + (size_t)sp * pd, pd, adt, R, minicpm ? 12.0f : 1.0f, st))) return s;
+        // first attention norm on the embeddings
+        if ((s = norm_launch(norm_kind(), adt, false, x0 + (size_t)sp * pd, pd, nullptr, 0, 1.0f, nullptr, 0,
+                             L[0].attn_norm, L[0].attn_norm_b, xn, pd, d, d, R, 1.0f, st)))
+            return s;
+        const uint8_t* xin = x0;
+        for (int l = 0; l < cfg.n_layers; l++) {
+            Layer& y = L[l];
+            const int pq = pitch(y.qd), pkv = pitch(y.kvd), pf = pitch(y.f);
+            const int nqkv = y.qd + 2 * y.kvd;
+            if ((s = matvec_raw(xn, adt, pd, R, &y.qkv, qkv_raw, nqkv, st))) return s;
+            if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, sp, R,
+                                     q_act, pq, y.kc, pkv, y.vc, pkv, st)))
+                return s;
+            if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, sp, n, st))) return s;
+            if ((s = matvec_raw(attn, adt, pq, R, &y.o, o_raw, d, st))) return s;
+            // h = x + attn (MiniCPM: attn scaled first), then the MLP norm
+            if ((s = norm_launch(norm_kind(), adt, true, xin + (size_t)sp * pd, pd, o_raw, d, bs,
+                                 y.res1 + (size_t)sp * pd, pd, y.mlp_norm, y.mlp_norm_b, xn, pd, d, d, R, 1.0f, st)))
+                return s;
+            if ((s = matvec_raw(xn, adt, pd, R, &y.gu, gu_raw, 2 * y.f, st))) return s;
+            if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
+            if ((s = matvec_raw(m_act, adt, pf, R, &y.down, down_raw, d, st))) return s;
+            // out = h + mlp, then the next layer's attention norm (or the final norm)
+            const bool last = l + 1 == cfg.n_layers;
+            const uint16_t* nw = last ? norm_w : L[l + 1].attn_norm;
+            const uint16_t* nb = last ? norm_b : L[l + 1].attn_norm_b;
+            const float post = last && minicpm ? 1.0f / 9 : 1.0f;  // minicpm.cpp:104-105
+            if ((s = norm_launch(norm_kind(), adt, true, y.res1 + (size_t)sp * pd, pd, down_raw, d, bs,
+                                 y.res2 + (size_t)sp * pd, pd, nw, nb, xn, pd, d, d, R, post, st)))
+                return s;
+            xin = y.res2;
+        }
+        // lm head on the last row only, fp32 out (gten/modules.cpp:48-59,111-122)
+        const nc_tensor* head = tied() ? &emb : &lm;
+        return matvec_raw(xn + (size_t)(R - 1) * pd, adt, pd, 1, head, logits, cfg.n_vocab, st);
+    }
+
+    int logits_call(const int32_t* toks, int n, int sp, float* out)
+    {
+        NC_CHECK_ARG(toks && out && n > 0 && n <= cfg.max_ctx && sp >= 0 && sp < n,
+                     "logits: %d tokens from %d with max_ctx %d", n, sp, cfg.max_ctx);
+        NC_CHECK_ARG(sp == 0 || sp <= n_cur, "logits: start_pos %d beyond the %d cached rows", sp, n_cur);
+        hipError_t e = hipMemcpyAsync(tokens, toks, (size_t)n * 4, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return hip_fail(e, "token upload");
+        int s = forward(sp, n);
+        if (s) return s;
+        n_cur = n;
+        e = hipMemcpyAsync(out, logits, (size_t)cfg.n_vocab * 4, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        return e == hipSuccess ? NC_OK : hip_fail(e, "logits download");
+    }
+
+    int prefill(const int32_t* prompt, int np)
+    {
+        NC_CHECK_ARG(prompt && np > 0 && np < cfg.max_ctx + 1, "prefill: %d prompt tokens, max_ctx %d", np, cfg.max_ctx);
+        hipError_t e = hipMemcpyAsync(tokens, prompt, (size_t)np * 4, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return hip_fail(e, "token upload");
+        int s = forward(0, np);
+        if (s) return s;
+        if ((s = argmax_launch(logits, cfg.n_vocab, tokens + np, st))) return s;
+        n_cur = np;
+        n_prompt = np;
+        return NC_OK;
+    }
+
+    // n_steps more greedy steps; the pending token sits at tokens[n_cur].
+    int decode(int n_steps)
+    {
+        NC_CHECK_ARG(n_cur > 0, "decode: no prefill");
+        NC_CHECK_ARG(n_cur + n_steps <= cfg.max_ctx, "decode: %d + %d steps exceed max_ctx %d", n_cur, n_steps,
+                     cfg.max_ctx);
+        for (int i = 0; i < n_steps; i++) {
+            const int n = n_cur + 1;
+            int s = forward(n - 1, n);
+            if (s) return s;
+            if ((s = argmax_launch(logits, cfg.n_vocab, tokens + n, st))) return s;
+            n_cur = n;
+        }
+        return NC_OK;
+    }
+
+    // Generated tokens so far: tokens[n_prompt + 1 .. n_cur + 1).
+    int fetch_generated(int32_t* out, int max_out, int* n_out)
+    {
+        const int cnt = std::min(max_out, n_cur + 1 - n_prompt);
+        hipError_t e = hipMemcpyAsync(out, tokens + n_prompt, (size_t)cnt * 4, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "token download");
+        int k = 0;
+        while (k < cnt && out[k] != cfg.eos) k++;  // greedy_sample stops at eos
+        *n_out = k;
+        return NC_OK;
+    }
+
+    int layer_out(int layer, int row, void* ref)
+    {
+        NC_CHECK_ARG(layer >= 0 && layer < cfg.n_layers && row >= 0 && row < cfg.max_ctx, "layer_out: %d/%d", layer,
+                     row);
+        const int pd = pitch(d);
+        std::vector<uint8_t> buf(pd);
+        hipError_t e = hipStreamSynchronize(st);
+        if (e == hipSuccess) e = hipMemcpy(buf.data(), L[layer].res2 + (size_t)row * pd, pd, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(e, "layer_out");
+        return nc_act_to_reference(buf.data(), ref, adt, 1, d);
+    }
+};
+
+}  // namespace nc
+
+using nc::Decoder;
+
+extern "C" {
+
+int nc_model_create(const nc_model_config* cfg, void** model)
+{
+    NC_CHECK_ARG(cfg && model, "model_create: null argument");
+    *model = nullptr;
+    auto* m = new Decoder();
+    int s = m->create(cfg);
+    if (s) {
+        delete m;
+        return s;
+    }
+    *model = m;
+    return NC_OK;
+}
+
+int nc_model_free(void* model)
+{
+    delete static_cast<Decoder*>(model);
+    return NC_OK;
+}
+
+int nc_model_init_synthetic(void* model, uint64_t seed)
+{
+    NC_CHECK_ARG(model, "model: null");
+    return static_cast<Decoder*>(model)->init_synthetic(seed);
+}
+
+int nc_model_set_weight(void* model, int layer, int slot, const void* ref_bytes, size_t n_bytes)
+{
+    NC_CHECK_ARG(model && ref_bytes, "model: null");
+    return static_cast<Decoder*>(model)->set_weight(layer, slot, ref_bytes, n_bytes);
+}
+
+int nc_model_get_weight(void* model, int layer, int slot, void* ref_bytes, size_t n_bytes)
+{
+    NC_CHECK_ARG(model && ref_bytes, "model: null");
+    return static_cast<Decoder*>(model)->get_weight(layer, slot, ref_bytes, n_bytes);
+}
+
+int nc_model_logits(void* model, const int32_t* tokens, int n_tokens, int start_pos, float* logits)
+{
+    NC_CHECK_ARG(model, "model: null");
+    return static_cast<Decoder*>(model)->logits_call(tokens, n_tokens, start_pos, logits);
+}
+
+int nc_model_layer_out(void* model, int layer, int row, void* ref_bytes)
+{
+    NC_CHECK_ARG(model && ref_bytes, "model: null");
+    return static_cast<Decoder*>(model)->layer_out(layer, row, ref_bytes);
+}
+
+int nc_model_prefill(void* model, const int32_t* prompt, int n_prompt)
+{
+    NC_CHECK_ARG(model, "model: null");
+    return static_cast<Decoder*>(model)->prefill(prompt, n_prompt);
+}
+
+int nc_model_decode(void* model, int n_steps, int32_t* out)
+{
+    NC_CHECK_ARG(model, "model: null");
+    auto* m = static_cast<Decoder*>(model);
+    int s = m->decode(n_steps);
+    if (s || !out) return s;
+    int n;
+    return m->fetch_generated(out, m->n_cur + 1 - m->n_prompt, &n);
+}
+
+int nc_model_generate(void* model, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out, int* n_out)
+{
+    NC_CHECK_ARG(model && out && n_out && n_gen > 0, "model_generate: bad arguments");
+    auto* m = static_cast<Decoder*>(model);
+    NC_CHECK_ARG(n_prompt + n_gen - 1 <= m->cfg.max_ctx, "model_generate: %d + %d exceeds max_ctx %d", n_prompt, n_gen,
+                 m->cfg.max_ctx);
+    int s = m->prefill(prompt, n_prompt);
+    if (!s) s = m->decode(n_gen - 1);
+    if (!s) s = m->fetch_generated(out, n_gen, n_out);
+    return s;
+}
+
+}  // extern "C"

@@ -1,0 +1,73 @@
+"""Writes the golden fixtures under tests/golden/ from the reference's own code.
+
+Runs in the build container only (it needs oracle/_ref/libgten_ref.so, the
+reference's gten sources compiled by oracle/Makefile).  For every workload it
+builds the model from the reference's modules with the synthetic weights,
+runs Model::logits on the prompt (start_pos = 0) and the reference's greedy
+loop, and records the prompt, the generated tokens, digests of the prefill
+logits and of every layer's residual-stream row, and the top prefill logits.
+Small models of every architecture are recorded the same way, with their
+full logits.
+
+    python tests/golden/make_golden.py [workload ...]
+"""
+import hashlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+import oracle_lib as OL  # noqa: E402
+from workloads import SMALL, config_of, prompt_of  # noqa: E402
+from nc_pkg import nc  # noqa: E402
+
+
+
+def sha(b):
+    return hashlib.sha256(np.ascontiguousarray(b).tobytes()).hexdigest()
+
+
+def record(name, w, full_logits=False):
+    ref = OL.Reference()
+    cfg = config_of(w)
+    t0 = time.time()
+    m = ref.model_create(cfg, w["seed"])
+    prompt = prompt_of(w)
+    logits = np.zeros(cfg.n_vocab, np.float32)
+    ref.model_logits(m, OL.ptr(prompt), len(prompt), 0, OL.ptr(logits))
+    adt = OL.F16 if w["wdtype"] == OL.F16 else OL.Q8
+    rb = OL.row_bytes(adt, cfg.n_embd)
+    layers = []
+    for l in range(cfg.n_layers):
+        p = ref.model_layer_out(m, l, len(prompt) - 1)
+        layers.append(sha(np.ctypeslib.as_array((OL.C.c_uint8 * rb).from_address(p))))
+    top = np.argsort(-logits, kind="stable")[:16]
+    out = np.zeros(w["gen"], np.int32)
+    n = ref.generate_greedy(m, OL.ptr(prompt), len(prompt), w["gen"], OL.ptr(out))
+    ref.model_free(m)
+    fx = dict(workload=name, seed=w["seed"], prompt=prompt.tolist(), tokens=out[:n].tolist(),
+              prefill_logits_sha256=sha(logits), layer_out_sha256=layers,
+              prefill_top=[[int(i), float(logits[i])] for i in top], seconds=round(time.time() - t0, 1))
+    with open(os.path.join(HERE, f"{name}.json"), "w") as f:
+        json.dump(fx, f)
+    if full_logits:
+        np.save(os.path.join(HERE, f"{name}.prefill_logits.npy"), logits)
+    print(name, n, "tokens", fx["seconds"], "s", flush=True)
+
+
+def main(argv):
+    names = argv or list(SMALL) + list(nc.WORKLOADS)
+    for name in names:
+        if name in SMALL:
+            record(name, SMALL[name], full_logits=True)
+        else:
+            record(name, nc.WORKLOADS[name], full_logits=name == "tinyllama-q4")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
