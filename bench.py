@@ -1,0 +1,175 @@
+#!/usr/bin/env python3
+"""Decode throughput of the gfx950 path on one MI355X, with the matvec
+kernel's roofline fraction and the reference CPU path timed beside it.
+
+Workload (default): TinyLlama-1.1B-shaped decoder, Q4 weights (Q8
+activations), vocab 32000, synthetic N(0, 0.02) weights generated on the
+device, a 64-token prompt and greedy decode with the KV cache growing to 320
+positions.  A step is one greedy decode step (Model::logits with start_pos =
+n - 1, device argmax, token fed back on the device).
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+Prints one JSON line.  `value` is decode tokens/s over exactly K timed steps
+(warmup steps run first, on the same sequence).  `roofline` is for the
+quantized matvec kernel: algorithmic bytes per launch (weights once +
+activation row + fp32 outputs) over the launch's average duration, both
+measured with HIP events on the model stream during the timed steps.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+import numpy as np  # noqa: E402
+
+from nc_pkg import nc  # noqa: E402
+
+METRIC = "decode tok/s (1 GPU) + Q4/Q8 matvec HBM GB/s as % of MI355X peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def workload_config(name):
+    return nc.workload_config(name)
+
+
+def prompt_tokens(w):
+    """The workload prompt (same generator as the tests), computed here
+    without the checker: splitmix64 of (seed, stream, index) -> [0, vocab)."""
+    mask = (1 << 64) - 1
+
+    def mix(z):
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        return z ^ (z >> 31)
+
+    seed = w["seed"] + nc.PROMPT_SEED_OFFSET
+    out = []
+    for i in range(w["prompt"]):
+        h = mix((seed * 0x9E3779B97F4A7C15 + 0x70CE5 * 0xD1B54A32D192ED03 + i) & mask)
+        out.append(((h >> 32) * w["n_vocab"]) >> 32)
+    return np.array(out, np.int32)
+
+
+def cpu_baseline(w, prompt, budget_s=12.0):
+    """The reference's own CPU path (oracle/_ref, built from its sources) on
+    the same workload: untimed prefill, then greedy decode steps timed until
+    the budget is spent.  Falls back to the oracle restatement ("port")."""
+    import oracle_lib as OL
+    kind = "reference" if OL.have_reference() else "port"
+    lib = OL.Reference() if kind == "reference" else OL.Oracle()
+    cfg = nc.workload_config(w["name"], cls=OL.Config)
+    m = lib.model_create(cfg, w["seed"])
+    toks = list(prompt)
+    logits = np.zeros(cfg.n_vocab, np.float32)
+    arr = np.array(toks, np.int32)
+    lib.model_logits(m, OL.ptr(arr), len(arr), 0, OL.ptr(logits))
+    toks.append(int(np.argmax(logits)))
+    steps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and len(toks) < cfg.max_ctx:
+        arr = np.array(toks, np.int32)
+        lib.model_logits(m, OL.ptr(arr), len(arr), len(arr) - 1, OL.ptr(logits))
+        toks.append(int(np.argmax(logits)))
+        steps += 1
+    dt = time.perf_counter() - t0
+    lib.model_free(m)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{steps} greedy decode steps after an untimed {len(prompt)}-token prefill "
+                      f"({dt:.1f} s), same weights and prompt, OpenMP threads = {threads}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=192)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--workload", default="tinyllama-q4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch every kernel directly instead of replaying "
+                    "the captured decode-step graph (for profilers that do not follow graph launches)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); decode of these models runs as one "
+              "independent stream per GPU, so N GPUs serve N streams at the 1-GPU rate.", file=sys.stderr)
+        sys.exit(2)
+    w = dict(nc.WORKLOADS[args.workload], name=args.workload)
+    if args.warmup + args.steps > w["gen"] - 1:
+        sys.exit(f"--warmup + --steps must be <= {w['gen'] - 1} for {args.workload}")
+
+    if args.no_graph:
+        os.environ["NC_DECODE_GRAPH"] = "0"
+    nc.init(0)
+    cfg = workload_config(args.workload)
+    model = nc.Model(cfg)
+    model.init_synthetic(w["seed"])
+    prompt = prompt_tokens(w)
+
+    # prefill (timed separately), warmup steps, then the timed steps (each
+    # step one replay of the captured decode-step graph)
+    L = nc.lib()
+    nc.check(L.nc_synchronize())
+    t0 = time.perf_counter()
+    model.prefill(prompt)
+    nc.check(L.nc_synchronize())
+    prefill_s = time.perf_counter() - t0
+    model.decode(args.warmup)
+    nc.check(L.nc_synchronize())
+    t0 = time.perf_counter()
+    model.decode(args.steps)
+    nc.check(L.nc_synchronize())
+    dt = time.perf_counter() - t0
+    # matvec timing: the same steps again (same positions, same tokens) with
+    # direct launches, each matvec bracketed by HIP events on the model stream
+    model.prefill(prompt)
+    model.decode(args.warmup)
+    launches_per_step = 4 * cfg.n_layers + 1
+    model.profile_begin(launches_per_step * args.steps)
+    t1 = time.perf_counter()
+    model.decode(args.steps)
+    nc.check(L.nc_synchronize())
+    dt_direct = time.perf_counter() - t1
+    prof = model.profile_end()
+    model.close()
+
+    tok_s = args.steps / dt
+    avg_ms = prof["total_ms"] / max(prof["launches"], 1)
+    avg_bytes = prof["total_bytes"] / max(prof["launches"], 1)
+    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if cfg.wdtype in (nc.Q4, nc.Q8) else "f16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: d_model {cfg.n_embd}, {cfg.n_layers} layers, "
+                               f"{cfg.n_heads[0]}/{cfg.n_kv_heads[0]} heads, ffn {cfg.n_ffn[0]}, "
+                               f"vocab {cfg.n_vocab}, prompt {w['prompt']}, decode {w['gen']} greedy tokens",
+                   "prompt": w["prompt"], "max_ctx": cfg.max_ctx,
+                   "timed_positions": [w["prompt"] + args.warmup, w["prompt"] + args.warmup + args.steps]},
+        "prefill_tok_s": round(w["prompt"] / prefill_s, 1),
+        "direct_launch_tok_s": round(args.steps / dt_direct, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_matvec_q (every matvec launch of the timed steps, replayed with direct launches)",
+                     "avg_launch_us": round(avg_ms * 1e3, 3), "avg_launch_bytes": round(avg_bytes),
+                     "launches": prof["launches"]},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w, prompt)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -195,6 +195,15 @@ int nc_model_generate(void* model, const int32_t* prompt, int n_prompt, int n_ge
  * calls (no host round trip between steps) and appends the tokens. */
 int nc_model_prefill(void* model, const int32_t* prompt, int n_prompt);
 int nc_model_decode(void* model, int n_steps, int32_t* out);
+/* Timing of the model's matvec launches (the reference's Linear time,
+ * print_perf in src/tinyllama/tinyllama.cpp:140-193, measured per launch):
+ * between begin and end, HIP events on the model's stream bracket up to
+ * max_launches matvec launches; end reports their count, summed duration,
+ * summed algorithmic HBM bytes (weights once + activation rows + fp32
+ * outputs) and the shortest / longest launch. */
+int nc_model_profile_begin(void* model, int max_launches);
+int nc_model_profile_end(void* model, int* launches, double* total_ms, double* total_bytes, double* min_ms,
+                         double* max_ms);
 
 #ifdef __cplusplus
 }

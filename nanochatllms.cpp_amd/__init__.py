@@ -134,6 +134,8 @@ def lib():
         "nc_model_get_weight": (I, [VP, I, I, VP, SZ]), "nc_model_logits": (I, [VP, VP, I, I, VP]),
         "nc_model_layer_out": (I, [VP, I, I, VP]), "nc_model_generate": (I, [VP, VP, I, I, VP, C.POINTER(I)]),
         "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
+        "nc_model_profile_begin": (I, [VP, I]),
+        "nc_model_profile_end": (I, [VP, C.POINTER(I)] + [C.POINTER(C.c_double)] * 4),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -234,6 +236,16 @@ class Model:
 
     def decode(self, n_steps):
         check(lib().nc_model_decode(self.h, n_steps, None), "decode")
+
+    def profile_begin(self, max_launches):
+        check(lib().nc_model_profile_begin(self.h, max_launches), "profile_begin")
+
+    def profile_end(self):
+        n = C.c_int()
+        vals = [C.c_double() for _ in range(4)]
+        check(lib().nc_model_profile_end(self.h, C.byref(n), *[C.byref(v) for v in vals]), "profile_end")
+        total_ms, total_bytes, min_ms, max_ms = (v.value for v in vals)
+        return dict(launches=n.value, total_ms=total_ms, total_bytes=total_bytes, min_ms=min_ms, max_ms=max_ms)
 
     def close(self):
         if self.h:

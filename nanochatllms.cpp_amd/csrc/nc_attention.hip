@@ -38,18 +38,37 @@ __device__ __forceinline__ void lane_dwords(const uint8_t* codes, uint32_t xa[4]
     }
 }
 
+constexpr int kAttnThreads = 256;
+constexpr int kAttnMaxV = 8;  // uint4 V-staging loads per thread prefetched into registers
+
+// Bytes of one position's V head slice in shared memory: Q8 codes (64) +
+// fp16 deltas (2 x 2) rounded to 16, or 64 fp16 values.
 template <int ADT>
-__global__ __launch_bounds__(256) void k_attn(const uint8_t* __restrict__ q, int q_pitch,
-                                              const uint8_t* __restrict__ kc, int k_pitch,
-                                              const uint8_t* __restrict__ vc, int v_pitch,
-                                              uint8_t* __restrict__ out, int out_pitch, int hq, int hkv, int start,
-                                              int n_ctx, float scale)
+__host__ __device__ constexpr int v_stage_bytes()
 {
+    return ADT == Q8 ? 80 : 128;
+}
+
+template <int ADT>
+__global__ __launch_bounds__(kAttnThreads) void k_attn(const uint8_t* __restrict__ q, int q_pitch,
+                                                       const uint8_t* __restrict__ kc, int k_pitch,
+                                                       const uint8_t* __restrict__ vc, int v_pitch,
+                                                       uint8_t* __restrict__ out, int out_pitch, int hq, int hkv,
+                                                       int start, int n_ctx, float scale,
+                                                       const int* __restrict__ dpos)
+{
+    // decode under graph replay: one query row at the position held on the device
+    if (dpos) {
+        start = dpos[0];
+        n_ctx = start + 1;
+    }
     extern __shared__ __align__(16) float sm[];
     const int npad = (n_ctx + 3) & ~3;
-    float* S = sm;            // scores / probabilities, n_ctx
-    float* red = S + npad;    // 256
-    float* acc = red + 256;   // [8][64]
+    float* S = sm;                                                   // scores / probabilities
+    float* red = S + npad;                                           // 64
+    float* acc = red + 64;                                           // [8][64]
+    uint8_t* Vs = reinterpret_cast<uint8_t*>(acc + 512);             // [n_ctx][v_stage_bytes]
+    constexpr int VB = v_stage_bytes<ADT>();
     const int tid = threadIdx.x;
     const int h = blockIdx.x;
     const int qr = blockIdx.y;       // row within q / out (pointers start at row `start`)
@@ -58,6 +77,21 @@ __global__ __launch_bounds__(256) void k_attn(const uint8_t* __restrict__ q, int
     const int qcols = hq * 64, kvcols = hkv * 64;
     const int qd = act_delta_offset(qcols), kvd = act_delta_offset(kvcols);
     const uint8_t* qrow = q + (size_t)qr * q_pitch;
+
+    // ---- V head slice: the first kAttnMaxV loads per thread are issued before
+    // the scores and parked in shared memory after them; any rest follows
+    constexpr int VPARTS = ADT == Q8 ? 4 : 8;  // 16-byte code/value loads per position
+    const int vtotal = n_ctx * VPARTS;
+    uint4 vreg[kAttnMaxV];
+    uint32_t dreg[kAttnMaxV];
+#pragma unroll
+    for (int i = 0; i < kAttnMaxV; i++) {
+        const int idx = tid + i * kAttnThreads;
+        const int c = idx < vtotal ? idx / VPARTS : 0, part = idx % VPARTS;
+        const uint8_t* vrow = vc + (size_t)c * v_pitch;
+        vreg[i] = reinterpret_cast<const uint4*>(vrow + g * (ADT == Q8 ? 64 : 128))[part];
+        dreg[i] = ADT == Q8 ? reinterpret_cast<const uint32_t*>(vrow + kvd)[g] : 0u;
+    }
 
     // ---- scores
     if (ADT == Q8) {
@@ -68,7 +102,7 @@ __global__ __launch_bounds__(256) void k_attn(const uint8_t* __restrict__ q, int
             lane_dwords(qrow + h * 64 + b * 32, qa[b], qb[b]);
             dq[b] = h2f(reinterpret_cast<const uint16_t*>(qrow + qd)[h * 2 + b]);
         }
-        for (int c = tid; c < n_ctx; c += 256) {
+        for (int c = tid; c < n_ctx; c += kAttnThreads) {
             float s = -INFINITY;
             if (c <= row) {
                 const uint8_t* krow = kc + (size_t)c * k_pitch;
@@ -94,7 +128,7 @@ __global__ __launch_bounds__(256) void k_attn(const uint8_t* __restrict__ q, int
         const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + h * 64;
 #pragma unroll
         for (int e = 0; e < 64; e++) qv[e] = h2f(qh[e]);
-        for (int c = tid; c < n_ctx; c += 256) {
+        for (int c = tid; c < n_ctx; c += kAttnThreads) {
             float s = -INFINITY;
             if (c <= row) {
                 const uint16_t* kh = reinterpret_cast<const uint16_t*>(kc + (size_t)c * k_pitch) + g * 64;
@@ -109,25 +143,44 @@ __global__ __launch_bounds__(256) void k_attn(const uint8_t* __restrict__ q, int
             S[c] = s;
         }
     }
+#pragma unroll
+    for (int i = 0; i < kAttnMaxV; i++) {
+        const int idx = tid + i * kAttnThreads;
+        if (idx < vtotal) {
+            const int c = idx / VPARTS, part = idx % VPARTS;
+            reinterpret_cast<uint4*>(Vs + (size_t)c * VB)[part] = vreg[i];
+            if (ADT == Q8 && part == 0) reinterpret_cast<uint32_t*>(Vs + (size_t)c * VB + 64)[0] = dreg[i];
+        }
+    }
+    for (int idx = tid + kAttnMaxV * kAttnThreads; idx < vtotal; idx += kAttnThreads) {
+        const int c = idx / VPARTS, part = idx % VPARTS;
+        const uint8_t* vrow = vc + (size_t)c * v_pitch;
+        reinterpret_cast<uint4*>(Vs + (size_t)c * VB)[part] =
+            reinterpret_cast<const uint4*>(vrow + g * (ADT == Q8 ? 64 : 128))[part];
+        if (ADT == Q8 && part == 0)
+            reinterpret_cast<uint32_t*>(Vs + (size_t)c * VB + 64)[0] = reinterpret_cast<const uint32_t*>(vrow + kvd)[g];
+    }
     __syncthreads();
 
-    // ---- softmax
+    // ---- softmax: max (order-free), expf, sequential sum, divide, requantize
     float mx = -INFINITY;
-    for (int c = tid; c < n_ctx; c += 256) mx = fmaxf(mx, S[c]);
-    red[tid] = mx;
+    for (int c = tid; c < n_ctx; c += kAttnThreads) mx = fmaxf(mx, S[c]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-        __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int c = tid; c < n_ctx; c += kAttnThreads) S[c] = expf_ref(S[c] - mx);
+    __syncthreads();
+    if (tid < kWave) {
+        const float sum = seq_sum(S, n_ctx);
+        if (tid == 0) red[8] = sum;
     }
-    mx = red[0];
-    for (int c = tid; c < n_ctx; c += 256) S[c] = expf_ref(S[c] - mx);
     __syncthreads();
-    const float sum = seq_sum(S, n_ctx);
-    __syncthreads();
+    const float sum = red[8];
     // every thread walks its positions in 32-lane blocks; lanes past n_ctx
     // still take part in the block reduction with valid = false
-    for (int c0 = 0; c0 < n_ctx; c0 += 256) {
+    for (int c0 = 0; c0 < n_ctx; c0 += kAttnThreads) {
         const int c = c0 + tid;
         const bool valid = c < n_ctx;
         const float p = valid ? S[c] / sum : 0.0f;
@@ -136,50 +189,56 @@ __global__ __launch_bounds__(256) void k_attn(const uint8_t* __restrict__ q, int
     }
     __syncthreads();
 
-    // ---- P @ V: thread = (column j, lanes l0, l0 + 1)
+    // ---- P @ V from shared memory: thread = (column j, lanes l0, l0 + 1)
+    const int j = tid & 63;
+    auto vval = [&](int c) -> float {
+        const uint8_t* vr = Vs + (size_t)c * VB;
+        if (ADT == Q8)
+            return (float)reinterpret_cast<const int8_t*>(vr)[j] * h2f(reinterpret_cast<const uint16_t*>(vr + 64)[j >> 5]);
+        return h2f(reinterpret_cast<const uint16_t*>(vr)[j]);
+    };
     {
-        const int j = tid & 63;
         const int l0 = (tid >> 6) * 2;
         const int n8 = (n_ctx / 8) * 8;
 #pragma unroll
         for (int li = 0; li < 2; li++) {
             const int l = l0 + li;
             float a = 0.0f;
-            for (int c = l; c < n8; c += 8) {
-                const uint8_t* vrow = vc + (size_t)c * v_pitch;
-                a = S[c] * act_load<ADT>(vrow, g * 64 + j, kvd) + a;
-            }
+            for (int c = l; c < n8; c += 8) a = S[c] * vval(c) + a;  // positions in order
             acc[l * 64 + j] = a;
         }
     }
     __syncthreads();
     if (tid < 64) {
-        const int j = tid;
         float s = acc[j];
 #pragma unroll
         for (int l = 1; l < 8; l++) s = s + acc[l * 64 + j];
-        for (int c = (n_ctx / 8) * 8; c < n_ctx; c++)
-            s = s + S[c] * act_load<ADT>(vc + (size_t)c * v_pitch, g * 64 + j, kvd);
+        for (int c = (n_ctx / 8) * 8; c < n_ctx; c++) s = s + S[c] * vval(c);
         act_store<ADT>(out + (size_t)qr * out_pitch, h * 64 + j, qd, s, true);
     }
 }
 
 int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k_pitch, const uint8_t* vc, int v_pitch,
-                uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st)
+                uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st, const int* dpos,
+                int max_ctx)
 {
-    const int rows = n_ctx - start;
+    // with dpos the single query row and the context come from the device;
+    // n_ctx then only bounds the shared-memory size (max_ctx)
+    const int rows = dpos ? 1 : n_ctx - start;
     if (rows <= 0) return NC_OK;
     if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "qkv_attn: %d query heads over %d kv heads", hq, hkv);
     const float scale = 1.0f / sqrtf(64.0f);
-    const size_t lds = ((size_t)((n_ctx + 3) & ~3) + 256 + 512) * 4;
-    if (lds > 64 * 1024) return fail(NC_ERR_ARG, "qkv_attn: context %d too long", n_ctx);
+    const int lds_ctx = dpos ? max_ctx : n_ctx;
+    const int vb = adt == NC_Q8 ? v_stage_bytes<Q8>() : v_stage_bytes<F16>();
+    const size_t lds = ((size_t)((lds_ctx + 3) & ~3) + 64 + 512) * 4 + (size_t)lds_ctx * vb;
+    if (lds > 64 * 1024) return fail(NC_ERR_ARG, "qkv_attn: context %d too long", lds_ctx);
     const dim3 grid(hq, rows);
     if (adt == NC_Q8)
-        hipLaunchKernelGGL((k_attn<Q8>), grid, dim3(256), lds, st, q, q_pitch, kc, k_pitch, vc, v_pitch, out, out_pitch,
-                           hq, hkv, start, n_ctx, scale);
+        hipLaunchKernelGGL((k_attn<Q8>), grid, dim3(kAttnThreads), lds, st, q, q_pitch, kc, k_pitch, vc, v_pitch, out, out_pitch,
+                           hq, hkv, start, n_ctx, scale, dpos);
     else if (adt == NC_F16)
-        hipLaunchKernelGGL((k_attn<F16>), grid, dim3(256), lds, st, q, q_pitch, kc, k_pitch, vc, v_pitch, out, out_pitch,
-                           hq, hkv, start, n_ctx, scale);
+        hipLaunchKernelGGL((k_attn<F16>), grid, dim3(kAttnThreads), lds, st, q, q_pitch, kc, k_pitch, vc, v_pitch, out, out_pitch,
+                           hq, hkv, start, n_ctx, scale, dpos);
     else
         return fail(NC_ERR_ARG, "qkv_attn: activation dtype %d", adt);
     return launch_status("k_attn");
@@ -204,5 +263,5 @@ extern "C" int nc_qkv_attn(const nc_tensor* q, const nc_tensor* k, const nc_tens
     return attn_launch(q->dtype, (const uint8_t*)q->data + (size_t)start * q->pitch, q->pitch,
                        (const uint8_t*)k->data, k->pitch, (const uint8_t*)v->data, v->pitch,
                        (uint8_t*)out->data + (size_t)start * out->pitch, out->pitch, n_heads, n_kv_heads, start, n_ctx,
-                       stream_of(stream));
+                       stream_of(stream), nullptr, n_ctx);
 }

@@ -107,19 +107,35 @@ __device__ __forceinline__ float f16_roundtrip(float x) { return h2f(f2h(x)); }
 // Sequential fp32 sum of buf[0..n) in index order, every calling lane
 // reading the same addresses (an LDS broadcast), so every lane ends with the
 // sum.  This is the scalar accumulation loop of the reference's norms and
-// softmax (gten/ops.cpp:673-683,833-835,1069-1075).
+// softmax (gten/ops.cpp:673-683,833-835,1069-1075).  The adds form one
+// dependent chain (about 6 cycles per add on gfx950); each CH-value chunk is
+// read from LDS with all its loads in flight at once before its adds run
+// (CH trades registers for fewer LDS round trips).
+template <int CH = 64>
 __device__ __forceinline__ float seq_sum(const float* buf, int n)
 {
     float s = 0.0f;
-    int i = 0;
-    for (; i + 4 <= n; i += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(buf + i);
+    int c = 0;
+    for (; c + CH <= n; c += CH) {
+        float4 v[CH / 4];
+#pragma unroll
+        for (int j = 0; j < CH / 4; j++) v[j] = reinterpret_cast<const float4*>(buf + c)[j];
+#pragma unroll
+        for (int j = 0; j < CH / 4; j++) {
+            s = s + v[j].x;
+            s = s + v[j].y;
+            s = s + v[j].z;
+            s = s + v[j].w;
+        }
+    }
+    for (; c + 4 <= n; c += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(buf + c);
         s = s + v.x;
         s = s + v.y;
         s = s + v.z;
         s = s + v.w;
     }
-    for (; i < n; i++) s = s + buf[i];
+    for (; c < n; c++) s = s + buf[c];
     return s;
 }
 

@@ -8,6 +8,7 @@
 // the decode step take the fp32 output of a matvec and first apply the
 // requantization the reference's Linear::forward performs on it
 // (gten/modules.cpp:89-104), so their results equal the unfused op chain.
+#include <algorithm>
 #include <cmath>
 #include <vector>
 
@@ -47,22 +48,27 @@ enum NormKind { kRms = 0, kLayerNorm = 1 };
 //   LN : vec_layer_norm_f32 (gten/ops.cpp:669-698): sequential mean and
 //        variance, y = ((x - mean) / (sqrtf(var) + 1e-5f)) * w + b.
 // post_scale != 1 applies ops::scale to the stored result (MiniCPM).
+// Up to 1024 threads share the elementwise work; the sequential sums run on
+// wavefront 0 alone while the others wait at the barrier.
 template <int ADT, int KIND, bool ADD>
-__global__ __launch_bounds__(256) void k_norm(const uint8_t* __restrict__ a, int a_pitch,
-                                              const float* __restrict__ braw, int b_pitch, float bscale,
-                                              uint8_t* __restrict__ h_out, int h_pitch,
-                                              const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
-                                              uint8_t* __restrict__ out, int out_pitch, int n, int row_cols,
-                                              float post_scale)
+__global__ __launch_bounds__(1024) void k_norm(const uint8_t* __restrict__ a, int a_pitch,
+                                               const float* __restrict__ braw, int b_pitch, float bscale,
+                                               uint8_t* __restrict__ h_out, int h_pitch,
+                                               const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
+                                               uint8_t* __restrict__ out, int out_pitch, int n, int row_cols,
+                                               float post_scale, const int* __restrict__ dpos)
 {
     __shared__ __align__(16) float buf[kNormMaxCols];
+    __shared__ float stat[2];
     const int tid = threadIdx.x;
     const int bs = blockDim.x;
     const int per = n / bs;
     const int r = blockIdx.y;
     const int seg0 = blockIdx.x * n;  // first column of this segment in the row
     const int dofs = act_delta_offset(row_cols);
-    const uint8_t* arow = a + (size_t)r * a_pitch;
+    // under graph replay the input / stored-sum rows sit at the device-held position
+    const size_t prow = dpos ? (size_t)dpos[0] : (size_t)r;
+    const uint8_t* arow = a + prow * a_pitch;
     uint8_t* orow = out + (size_t)r * out_pitch;
 
     float xv[kNormMaxPerThread];
@@ -76,29 +82,35 @@ __global__ __launch_bounds__(256) void k_norm(const uint8_t* __restrict__ a, int
             if (bscale != 1.0f) b = act_roundtrip<ADT>(b * bscale, true);
             const float s = x + b;
             x = act_roundtrip<ADT>(s, true);
-            act_store<ADT>(h_out + (size_t)r * h_pitch, e, dofs, s, true);
+            act_store<ADT>(h_out + prow * h_pitch, e, dofs, s, true);
         }
         xv[m] = x;
         buf[tid + m * bs] = KIND == kRms ? x * x : x;
     }
     __syncthreads();
-    const float s1 = seq_sum(buf, n);
-    float mean = 0.0f, denom;
-    if (KIND == kRms) {
-        const float rms = sqrtf(s1 / (float)n);
-        denom = rms + 1e-6f;
-    } else {
-        mean = s1 / (float)n;
-        __syncthreads();
+    if (tid < kWave) {
+        const float s1 = seq_sum(buf, n);
+        if (tid == 0) {
+            stat[0] = KIND == kLayerNorm ? s1 / (float)n : 0.0f;
+            stat[1] = sqrtf(s1 / (float)n) + 1e-6f;  // RMS: rms + eps
+        }
+    }
+    __syncthreads();
+    if (KIND == kLayerNorm) {
+        const float mu = stat[0];
 #pragma unroll
         for (int m = 0; m < kNormMaxPerThread; m++) {
             if (m >= per) continue;
-            buf[tid + m * bs] = (xv[m] - mean) * (xv[m] - mean);
+            buf[tid + m * bs] = (xv[m] - mu) * (xv[m] - mu);
         }
         __syncthreads();
-        const float ssq = seq_sum(buf, n);
-        denom = sqrtf(ssq / (float)n) + 1e-05f;
+        if (tid < kWave) {
+            const float ssq = seq_sum(buf, n);
+            if (tid == 0) stat[1] = sqrtf(ssq / (float)n) + 1e-05f;
+        }
     }
+    __syncthreads();
+    const float mean = stat[0], denom = stat[1];
 #pragma unroll
     for (int m = 0; m < kNormMaxPerThread; m++) {
         if (m >= per) continue;
@@ -160,13 +172,13 @@ __global__ __launch_bounds__(64) void k_qkv_post(const float* __restrict__ raw, 
                                                  const uint16_t* __restrict__ kn_w, const float2* __restrict__ table,
                                                  int d_half, int start, uint8_t* __restrict__ q_out, int q_pitch,
                                                  uint8_t* __restrict__ k_cache, int k_pitch,
-                                                 uint8_t* __restrict__ v_cache, int v_pitch)
+                                                 uint8_t* __restrict__ v_cache, int v_pitch, const int* __restrict__ dpos)
 {
     __shared__ __align__(16) float buf[64];
     const int lane = threadIdx.x;
     const int seg = blockIdx.x;
     const int r = blockIdx.y;
-    const int pos = start + r;
+    const int pos = (dpos ? dpos[0] : start) + r;
     const int kind = seg < hq ? 0 : (seg < hq + hkv ? 1 : 2);
     const int h = kind == 0 ? seg : (kind == 1 ? seg - hq : seg - hq - hkv);
     float x = act_roundtrip<ADT>(raw[(size_t)r * raw_pitch + seg * 64 + lane], true);
@@ -243,10 +255,10 @@ __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ raw,
 template <int WDT, int ADT>
 __global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ codes, const uint16_t* __restrict__ deltas,
                                                int vocab, const int32_t* __restrict__ tokens, uint8_t* __restrict__ out,
-                                               int out_pitch, int d, float post_scale)
+                                               int out_pitch, int d, float post_scale, const int* __restrict__ dpos)
 {
     const int e = blockIdx.x * 256 + threadIdx.x;
-    const int r = blockIdx.y;
+    const int r = dpos ? dpos[0] : (int)blockIdx.y;  // row of tokens / out
     const bool valid = e < d;
     const int ec = valid ? e : 0;
     int tok = tokens[r];
@@ -307,6 +319,45 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
     if (tid == 0) out[0] = si[0] == 0x7fffffff ? 0 : si[0];
 }
 
+// Greedy step epilogue for graph replay: every workgroup reduces a slice of
+// x to (value, first index), folded across workgroups with a 64-bit
+// atomicMax on key = (order-preserving bits of value) << 32 | ~index, so the
+// largest value wins and, among equal values, the smallest index.  The last
+// workgroup to finish writes the token to tokens[pos + 1], advances pos and
+// re-zeroes the scratch words for the next replay.
+__global__ __launch_bounds__(256) void k_argmax_advance(const float* __restrict__ x, int n, int32_t* __restrict__ tokens,
+                                                        int* __restrict__ dpos, unsigned long long* __restrict__ scratch)
+{
+    __shared__ unsigned long long sk[256];
+    const int tid = threadIdx.x;
+    unsigned long long best = 0;
+    for (int i = blockIdx.x * 256 + tid; i < n; i += gridDim.x * 256) {
+        const uint32_t u = __float_as_uint(x[i]);
+        const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        const unsigned long long key = ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (uint32_t)i);
+        best = key > best ? key : best;
+    }
+    sk[tid] = best;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s && sk[tid + s] > sk[tid]) sk[tid] = sk[tid + s];
+        __syncthreads();
+    }
+    if (tid == 0) {
+        atomicMax(&scratch[0], sk[0]);
+        __threadfence();
+        const unsigned long long ticket = atomicAdd(&scratch[1], 1ull);
+        if (ticket == gridDim.x - 1) {
+            const unsigned long long key = atomicOr(&scratch[0], 0ull);
+            const int pos = dpos[0];
+            tokens[pos + 1] = (int32_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+            dpos[0] = pos + 1;
+            atomicExch(&scratch[0], 0ull);
+            atomicExch(&scratch[1], 0ull);
+        }
+    }
+}
+
 // ============================================================ launchers ==
 
 #define NC_ADT_DISPATCH(adt, KERNEL_CALL)                              \
@@ -326,11 +377,18 @@ int write_rows(const float* in, int in_pitch, uint8_t* out, int out_pitch, int d
     return launch_status("k_write_rows");
 }
 
-static int norm_block(int n) { return n >= 256 ? 256 : n; }
+// Threads per norm workgroup: the largest multiple of 64 up to 1024 that
+// divides the segment (each thread then owns n / bs values).
+static int norm_block(int n)
+{
+    for (int bs = 1024; bs >= 64; bs -= 64)
+        if (n % bs == 0) return bs;
+    return n;
+}
 
 int norm_launch(int kind, int adt, bool add, const uint8_t* a, int a_pitch, const float* braw, int b_pitch,
                 float bscale, uint8_t* h_out, int h_pitch, const uint16_t* w, const uint16_t* bias, uint8_t* out,
-                int out_pitch, int d_norm, int row_cols, int rows, float post_scale, hipStream_t st)
+                int out_pitch, int d_norm, int row_cols, int rows, float post_scale, hipStream_t st, const int* dpos)
 {
     if (rows <= 0) return NC_OK;
     const int bs = norm_block(d_norm);
@@ -340,7 +398,7 @@ int norm_launch(int kind, int adt, bool add, const uint8_t* a, int a_pitch, cons
     const dim3 grid(row_cols / d_norm, rows);
 #define NORM_CALL(K, A)                                                                                           \
     hipLaunchKernelGGL((k_norm<ADT, K, A>), grid, dim3(bs), 0, st, a, a_pitch, braw, b_pitch, bscale, h_out, h_pitch, \
-                       w, bias, out, out_pitch, d_norm, row_cols, post_scale)
+                       w, bias, out, out_pitch, d_norm, row_cols, post_scale, dpos)
     if (adt == NC_Q8) {
         constexpr int ADT = Q8;
         if (kind == kRms) { if (add) NORM_CALL(kRms, true); else NORM_CALL(kRms, false); }
@@ -357,14 +415,14 @@ int norm_launch(int kind, int adt, bool add, const uint8_t* a, int a_pitch, cons
 int qkv_post_launch(int adt, const float* raw, int raw_pitch, int hq, int hkv, const uint16_t* bq, const uint16_t* bk,
                     const uint16_t* bv, const uint16_t* qn_w, const uint16_t* kn_w, const float* table, int d_half,
                     int start, int rows, uint8_t* q_out, int q_pitch, uint8_t* k_cache, int k_pitch,
-                    uint8_t* v_cache, int v_pitch, hipStream_t st)
+                    uint8_t* v_cache, int v_pitch, hipStream_t st, const int* dpos)
 {
     if (rows <= 0) return NC_OK;
     const dim3 grid(hq + 2 * hkv, rows);
     const bool bias = bq != nullptr, qkn = qn_w != nullptr;
 #define QKV_CALL(B, N)                                                                                              \
     hipLaunchKernelGGL((k_qkv_post<ADT, B, N>), grid, dim3(64), 0, st, raw, raw_pitch, hq, hkv, bq, bk, bv, qn_w, kn_w, \
-                       (const float2*)table, d_half, start, q_out, q_pitch, k_cache, k_pitch, v_cache, v_pitch)
+                       (const float2*)table, d_half, start, q_out, q_pitch, k_cache, k_pitch, v_cache, v_pitch, dpos)
     if (adt == NC_Q8) {
         constexpr int ADT = Q8;
         if (bias) { if (qkn) QKV_CALL(true, true); else QKV_CALL(true, false); }
@@ -392,7 +450,7 @@ int silu_mul_launch(int adt, const float* raw, int raw_pitch, int f, uint8_t* ou
 }
 
 int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, int out_pitch, int adt, int rows,
-                 float post_scale, hipStream_t st)
+                 float post_scale, hipStream_t st, const int* dpos)
 {
     if (rows <= 0) return NC_OK;
     const int d = table->cols;
@@ -400,11 +458,14 @@ int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, in
     const uint32_t* c = (const uint32_t*)table->data;
     const uint16_t* dl = (const uint16_t*)table->deltas;
     if (table->dtype == NC_Q4 && adt == NC_Q8)
-        hipLaunchKernelGGL((k_embed<Q4, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale);
+        hipLaunchKernelGGL((k_embed<Q4, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale,
+                           dpos);
     else if (table->dtype == NC_Q8 && adt == NC_Q8)
-        hipLaunchKernelGGL((k_embed<Q8, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale);
+        hipLaunchKernelGGL((k_embed<Q8, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale,
+                           dpos);
     else if (table->dtype == NC_F16 && adt == NC_F16)
-        hipLaunchKernelGGL((k_embed<F16, F16>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale);
+        hipLaunchKernelGGL((k_embed<F16, F16>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale,
+                           dpos);
     else
         return fail(NC_ERR_ARG, "token_embed: table dtype %d with activation dtype %d", table->dtype, adt);
     return launch_status("k_embed");
@@ -414,6 +475,14 @@ int argmax_launch(const float* x, int n, int32_t* out, hipStream_t st)
 {
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, x, n, out);
     return launch_status("k_argmax");
+}
+
+int argmax_advance_launch(const float* x, int n, int32_t* tokens, int* dpos, unsigned long long* scratch,
+                          hipStream_t st)
+{
+    const int grid = std::min(64, (n + 255) / 256);
+    hipLaunchKernelGGL(k_argmax_advance, dim3(grid), dim3(256), 0, st, x, n, tokens, dpos, scratch);
+    return launch_status("k_argmax_advance");
 }
 
 int ew_launch(int op, int adt, const uint8_t* a, int a_pitch, const uint8_t* b, int b_pitch, const uint16_t* bias,
@@ -464,7 +533,7 @@ int nc_rms_norm(const nc_tensor* x, const uint16_t* w, nc_tensor* out, int d_nor
     NC_CHECK_ARG(x->dtype == out->dtype && x->cols == out->cols, "rms_norm: shape/dtype mismatch");
     NC_CHECK_ARG(start >= 0 && n_ctx <= x->rows && n_ctx <= out->rows, "rms_norm: rows [%d, %d)", start, n_ctx);
     return norm_launch(kRms, x->dtype, false, row_ptr(x, start), x->pitch, nullptr, 0, 1.0f, nullptr, 0, w, nullptr,
-                       row_ptr(out, start), out->pitch, d_norm, x->cols, n_ctx - start, 1.0f, stream_of(stream));
+                       row_ptr(out, start), out->pitch, d_norm, x->cols, n_ctx - start, 1.0f, stream_of(stream), nullptr);
 }
 
 int nc_layer_norm(const nc_tensor* x, const uint16_t* w, const uint16_t* b, nc_tensor* out, int start, int n_ctx,
@@ -474,7 +543,7 @@ int nc_layer_norm(const nc_tensor* x, const uint16_t* w, const uint16_t* b, nc_t
     NC_CHECK_ARG(x->dtype == out->dtype && x->cols == out->cols, "layer_norm: shape/dtype mismatch");
     NC_CHECK_ARG(start >= 0 && n_ctx <= x->rows && n_ctx <= out->rows, "layer_norm: rows [%d, %d)", start, n_ctx);
     return norm_launch(kLayerNorm, x->dtype, false, row_ptr(x, start), x->pitch, nullptr, 0, 1.0f, nullptr, 0, w, b,
-                       row_ptr(out, start), out->pitch, x->cols, x->cols, n_ctx - start, 1.0f, stream_of(stream));
+                       row_ptr(out, start), out->pitch, x->cols, x->cols, n_ctx - start, 1.0f, stream_of(stream), nullptr);
 }
 
 int nc_rope_table(int max_ctx, int d_head, float rope_pct, float* out)
@@ -551,7 +620,7 @@ int nc_token_embed(const nc_tensor* table, const int32_t* tokens, nc_tensor* out
     NC_CHECK_ARG(table->cols == out->cols, "token_embed: width mismatch");
     NC_CHECK_ARG(start >= 0 && n_ctx <= out->rows, "token_embed: rows [%d, %d)", start, n_ctx);
     return embed_launch(table, tokens + start, row_ptr(out, start), out->pitch, out->dtype, n_ctx - start, 1.0f,
-                        stream_of(stream));
+                        stream_of(stream), nullptr);
 }
 
 int nc_argmax(const float* x, int n, int32_t* out, void* stream)

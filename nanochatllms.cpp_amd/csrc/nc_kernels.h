@@ -13,29 +13,41 @@ enum EwOpHost { kEwSilu = 0, kEwMul = 1, kEwAdd = 2, kEwScale = 3, kEwBias = 4 }
 int write_rows(const float* in, int in_pitch, uint8_t* out, int out_pitch, int dtype, int cols, int rows,
                hipStream_t st);
 
-// x rows (pointer at the first row) times weight rows -> fp32 dots.
+// x rows (pointer at the first row) times weight rows -> fp32 dots.  With
+// events, the launch records them at the kernel's own start and end.
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
-               hipStream_t st);
+               hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 
 // Norm over segments of d_norm values; with `add` the input is
 // a + requant(braw) (scaled by bscale and requantized when bscale != 1),
-// stored to h_out.
+// stored to h_out.  dpos != nullptr: a and h_out rows are taken at the
+// device-held position (one row).
 int norm_launch(int kind, int adt, bool add, const uint8_t* a, int a_pitch, const float* braw, int b_pitch,
                 float bscale, uint8_t* h_out, int h_pitch, const uint16_t* w, const uint16_t* bias, uint8_t* out,
-                int out_pitch, int d_norm, int row_cols, int rows, float post_scale, hipStream_t st);
+                int out_pitch, int d_norm, int row_cols, int rows, float post_scale, hipStream_t st,
+                const int* dpos = nullptr);
 
+// dpos != nullptr: the (single) row's position is read from the device.
 int qkv_post_launch(int adt, const float* raw, int raw_pitch, int hq, int hkv, const uint16_t* bq, const uint16_t* bk,
                     const uint16_t* bv, const uint16_t* qn_w, const uint16_t* kn_w, const float* table, int d_half,
                     int start, int rows, uint8_t* q_out, int q_pitch, uint8_t* k_cache, int k_pitch,
-                    uint8_t* v_cache, int v_pitch, hipStream_t st);
+                    uint8_t* v_cache, int v_pitch, hipStream_t st, const int* dpos = nullptr);
 
 int silu_mul_launch(int adt, const float* raw, int raw_pitch, int f, uint8_t* out, int out_pitch, int rows,
                     hipStream_t st);
 
+// dpos != nullptr: embeds the single token tokens[*dpos] (tokens = the
+// sequence base).
 int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, int out_pitch, int adt, int rows,
-                 float post_scale, hipStream_t st);
+                 float post_scale, hipStream_t st, const int* dpos = nullptr);
 
 int argmax_launch(const float* x, int n, int32_t* out, hipStream_t st);
+
+// Greedy step epilogue under graph replay: argmax of x written to
+// tokens[*dpos + 1], then *dpos advanced.  `scratch` is 16 zeroed bytes the
+// kernel leaves zeroed.
+int argmax_advance_launch(const float* x, int n, int32_t* tokens, int* dpos, unsigned long long* scratch,
+                          hipStream_t st);
 
 int ew_launch(int op, int adt, const uint8_t* a, int a_pitch, const uint8_t* b, int b_pitch, const uint16_t* bias,
               float s, uint8_t* out, int out_pitch, int cols, int rows, hipStream_t st);
@@ -43,7 +55,10 @@ int ew_launch(int op, int adt, const uint8_t* a, int a_pitch, const uint8_t* b, 
 int rope_launch(int adt, const uint8_t* in, int in_pitch, uint8_t* out, int out_pitch, int cols, const float* table,
                 int d_half, int start, int rows, hipStream_t st);
 
+// dpos != nullptr: one query row at position *dpos over *dpos + 1 cached
+// rows (decode under graph replay); max_ctx sizes the shared memory.
 int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k_pitch, const uint8_t* vc, int v_pitch,
-                uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st);
+                uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st,
+                const int* dpos = nullptr, int max_ctx = 0);
 
 }  // namespace nc

@@ -26,6 +26,8 @@
 // own lane (the weight layout interleaves 64-column groups over 8-row
 // groups, so a wavefront reads 1 KiB contiguous) and folds its chain in
 // order; the eight lanes of a row meet through wavefront shuffles.
+#include <hip/hip_ext.h>
+
 #include "nc_device.h"
 #include "nc_kernels.h"
 
@@ -44,12 +46,22 @@ __device__ __forceinline__ uint32_t pick_pair(uint32_t lo, uint32_t hi, int odd)
 // [xa0 xb0 xa1 xb1 xa2 xb2 xa3 xb3 | c0 c1 c2 c3 | dx 0 0 0]
 // xa_k = codes {2k,2k+1,2k+8,2k+9}, xb_k = codes {2k+16,2k+17,2k+24,2k+25},
 // c_k = -7 * (sum of those eight codes).
-__device__ __forceinline__ void stage_x_block(const uint8_t* xrow, int nb, int i, uint32_t* dst)
+struct XRaw {
+    uint4 a, b;
+    uint16_t d16;
+};
+
+__device__ __forceinline__ XRaw load_x_block(const uint8_t* xrow, int nb, int i)
 {
     const uint4* q = reinterpret_cast<const uint4*>(xrow + (size_t)i * 32);
-    const uint4 a = q[0], b = q[1];
+    return XRaw{q[0], q[1], reinterpret_cast<const uint16_t*>(xrow + (size_t)nb * 32)[i]};
+}
+
+__device__ __forceinline__ void stage_x_block(const XRaw& x, uint32_t* dst)
+{
+    const uint4 a = x.a, b = x.b;
     const uint32_t X[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    const uint16_t d16 = reinterpret_cast<const uint16_t*>(xrow + (size_t)nb * 32)[i];
+    const uint16_t d16 = x.d16;
     uint32_t o[16];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -83,40 +95,30 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restri
     const int row0 = blockIdx.x * R;
     const int nitems = R * nb;
 
-    uint32_t w[kMvMaxItems][WD];
-    float dw[kMvMaxItems];
+    // the first activation row's block is requested first, then every weight
+    // load of this thread (unconditionally, at a clamped index), so both
+    // latencies overlap; x is consumed first
+    XRaw x0{};
+    if (tid < nb) x0 = load_x_block(x, nb, tid);
+    uint4 w[kMvMaxItems][WD / 4];
+    uint16_t dw16[kMvMaxItems];
     int tix[kMvMaxItems], bix[kMvMaxItems];
 #pragma unroll
     for (int it = 0; it < kMvMaxItems; it++) {
         const int j = tid + it * kMvThreads;
-        tix[it] = -1;
-        bix[it] = 0;
-        dw[it] = 0.0f;
+        const int r = j / nb, i = j - r * nb;
+        const bool ok = j < nitems && row0 + r < N;
+        tix[it] = ok ? r * 4 * tp + i : -1;
+        bix[it] = i;
+        const size_t b = ok ? (size_t)(row0 + r) * nb + i : 0;
+        const uint4* src = reinterpret_cast<const uint4*>(wq + b * WD);
 #pragma unroll
-        for (int v = 0; v < WD; v++) w[it][v] = 0;
-        if (j < nitems) {
-            const int r = j / nb, i = j - r * nb;
-            if (row0 + r < N) {
-                const size_t b = (size_t)(row0 + r) * nb + i;
-                const uint4* src = reinterpret_cast<const uint4*>(wq + b * WD);
-#pragma unroll
-                for (int v = 0; v < WD / 4; v++) {
-                    const uint4 u = src[v];
-                    w[it][4 * v] = u.x;
-                    w[it][4 * v + 1] = u.y;
-                    w[it][4 * v + 2] = u.z;
-                    w[it][4 * v + 3] = u.w;
-                }
-                dw[it] = h2f(wd[b]);
-                tix[it] = r * 4 * tp + i;
-                bix[it] = i;
-            }
-        }
+        for (int v = 0; v < WD / 4; v++) w[it][v] = src[v];
+        dw16[it] = wd[b];
     }
-
     for (int p = 0; p < n_xrows; p++) {
         const uint8_t* xr = x + (size_t)p * x_pitch;
-        for (int i = tid; i < nb; i += kMvThreads) stage_x_block(xr, nb, i, xs + i * 16);
+        if (tid < nb) stage_x_block(p == 0 ? x0 : load_x_block(xr, nb, tid), xs + tid * 16);
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < kMvMaxItems; it++) {
@@ -126,18 +128,26 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restri
             const uint32_t xa[4] = {s0.x, s0.z, s1.x, s1.z};
             const uint32_t xb[4] = {s0.y, s0.w, s1.y, s1.w};
             const int c[4] = {(int)s2.x, (int)s2.y, (int)s2.z, (int)s2.w};
-            const float dd = __uint_as_float(s3.x) * dw[it];
+            const float dd = __uint_as_float(s3.x) * h2f(dw16[it]);
             float* t = T + tix[it];
+            uint32_t W[WD];
+#pragma unroll
+            for (int v = 0; v < WD / 4; v++) {
+                W[4 * v] = w[it][v].x;
+                W[4 * v + 1] = w[it][v].y;
+                W[4 * v + 2] = w[it][v].z;
+                W[4 * v + 3] = w[it][v].w;
+            }
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 int L;
                 if (WT == Q4) {
-                    const uint32_t P = w[it][k];
+                    const uint32_t P = W[k];
                     L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)xa[k], c[k], false);
                     L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)xb[k], L, false);
                 } else {
-                    L = __builtin_amdgcn_sdot4((int)w[it][2 * k], (int)xa[k], 0, false);
-                    L = __builtin_amdgcn_sdot4((int)w[it][2 * k + 1], (int)xb[k], L, false);
+                    L = __builtin_amdgcn_sdot4((int)W[2 * k], (int)xa[k], 0, false);
+                    L = __builtin_amdgcn_sdot4((int)W[2 * k + 1], (int)xb[k], L, false);
                 }
                 t[k * tp] = (float)L * dd;
             }
@@ -145,7 +155,7 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restri
         __syncthreads();
         if (tid < kWave) {
             float acc = 0.0f;
-            if (tid < 4 * R) acc = seq_sum(T + tid * tp, nb);
+            if (tid < 4 * R) acc = seq_sum<16>(T + tid * tp, nb);
             const int g = tid & ~3;
             const float a0 = __shfl(acc, g), a1 = __shfl(acc, g + 1), a2 = __shfl(acc, g + 2), a3 = __shfl(acc, g + 3);
             const float res = (a0 + a1) + (a2 + a3);
@@ -204,8 +214,16 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_f16(const uint8_t* __rest
 // out[r, c] = dot(x[r], w[c]) for x rows [0, n_rows) (pointers already at
 // the first row), fp32 out with `out_pitch` floats per row.
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
-               hipStream_t st)
+               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop)
 {
+    // with events, the dispatch itself records them (the kernel's own start and end)
+#define NC_MV_LAUNCH(KERNEL, GRID, LDS, ...)                                                              \
+    do {                                                                                                  \
+        if (ev_start)                                                                                     \
+            hipExtLaunchKernelGGL(KERNEL, GRID, dim3(kMvThreads), LDS, st, ev_start, ev_stop, 0, __VA_ARGS__); \
+        else                                                                                              \
+            hipLaunchKernelGGL(KERNEL, GRID, dim3(kMvThreads), LDS, st, __VA_ARGS__);                     \
+    } while (0)
     const int N = w->rows, K = w->cols;
     if (w->dtype == NC_Q4 || w->dtype == NC_Q8) {
         if (x_dtype != NC_Q8) return fail(NC_ERR_ARG, "matmul: Q%d weights need Q8 activations", w->dtype == NC_Q4 ? 4 : 8);
@@ -217,11 +235,11 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
         const size_t lds = (size_t)nb * 64 + (size_t)R * 4 * tp * 4;
         const dim3 grid((N + R - 1) / R);
         if (w->dtype == NC_Q4)
-            hipLaunchKernelGGL((k_matvec_q<Q4, R>), grid, dim3(kMvThreads), lds, st, x, x_pitch, n_rows,
-                               (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+            NC_MV_LAUNCH((k_matvec_q<Q4, R>), grid, lds, x, x_pitch, n_rows, (const uint32_t*)w->data,
+                         (const uint16_t*)w->deltas, out, out_pitch, N, nb);
         else
-            hipLaunchKernelGGL((k_matvec_q<Q8, R>), grid, dim3(kMvThreads), lds, st, x, x_pitch, n_rows,
-                               (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+            NC_MV_LAUNCH((k_matvec_q<Q8, R>), grid, lds, x, x_pitch, n_rows, (const uint32_t*)w->data,
+                         (const uint16_t*)w->deltas, out, out_pitch, N, nb);
         return launch_status("k_matvec_q");
     }
     if (w->dtype == NC_F16) {
@@ -230,11 +248,11 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
         const size_t lds = (size_t)K * 4;
         if (lds > 64 * 1024) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);
         const dim3 grid((N + 31) / 32);
-        hipLaunchKernelGGL(k_matvec_f16, grid, dim3(kMvThreads), lds, st, x, x_pitch, n_rows,
-                           (const uint16_t*)w->data, out, out_pitch, N, K);
+        NC_MV_LAUNCH(k_matvec_f16, grid, lds, x, x_pitch, n_rows, (const uint16_t*)w->data, out, out_pitch, N, K);
         return launch_status("k_matvec_f16");
     }
     return fail(NC_ERR_ARG, "matmul: weight dtype %d", w->dtype);
+#undef NC_MV_LAUNCH
 }
 
 }  // namespace nc

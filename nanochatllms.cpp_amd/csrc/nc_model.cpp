@@ -19,6 +19,7 @@
 // Decode keeps the token stream on the device: argmax writes the next token
 // where the next step's embedding reads it, so steps need no host round trip.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -81,9 +82,83 @@ public:
     int n_prompt = 0;     // prompt length of the current generation
     int max_qkv = 0, max_qd = 0, max_f = 0;
 
+    // Matvec launch timing: a start/end event pair recorded on the model's
+    // stream around every matvec launch while profiling is on.
+    struct Profile {
+        bool on = false;
+        std::vector<hipEvent_t> ev;
+        std::vector<double> bytes;
+        size_t used = 0;
+    } prof;
+
     ~Decoder()
     {
+        if (step_graph) (void)hipGraphExecDestroy(step_graph);
+        for (hipEvent_t e : prof.ev) (void)hipEventDestroy(e);
         for (void* p : allocs) (void)hipFree(p);
+    }
+
+    // Algorithmic HBM bytes of one matvec launch: every weight byte once,
+    // plus each activation row read and each fp32 output row written.
+    static double matvec_bytes(const nc_tensor* w, int rows)
+    {
+        const double N = w->rows, K = w->cols;
+        double wb, xb;
+        if (w->dtype == NC_F16) { wb = 2.0 * N * K; xb = 2.0 * K; }
+        else { wb = N * (K / 32) * (w->dtype == NC_Q8 ? 34.0 : 18.0); xb = (K / 32) * 34.0; }
+        return wb + rows * (xb + 4.0 * N);
+    }
+
+    int mv(const uint8_t* x, int x_pitch, int rows, const nc_tensor* w, float* out, int out_pitch)
+    {
+        const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
+        int s = timed ? matvec_raw(x, adt, x_pitch, rows, w, out, out_pitch, st, prof.ev[prof.used],
+                                   prof.ev[prof.used + 1])
+                      : matvec_raw(x, adt, x_pitch, rows, w, out, out_pitch, st);
+        if (s) return s;
+        if (timed) {
+            prof.used += 2;
+            prof.bytes.push_back(matvec_bytes(w, rows));
+        }
+        return NC_OK;
+    }
+
+    int profile_begin(int max_launches)
+    {
+        NC_CHECK_ARG(max_launches > 0, "profile_begin: %d launches", max_launches);
+        while (prof.ev.size() < (size_t)max_launches * 2) {
+            hipEvent_t e;
+            hipError_t r = hipEventCreate(&e);
+            if (r != hipSuccess) return hip_fail(r, "hipEventCreate");
+            prof.ev.push_back(e);
+        }
+        prof.used = 0;
+        prof.bytes.clear();
+        prof.on = true;
+        return NC_OK;
+    }
+
+    int profile_end(int* launches, double* total_ms, double* total_bytes, double* min_ms, double* max_ms)
+    {
+        prof.on = false;
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "profile_end");
+        double tot = 0, mn = 1e30, mx = 0, by = 0;
+        for (size_t i = 0; i + 1 < prof.used; i += 2) {
+            float ms = 0;
+            if ((e = hipEventElapsedTime(&ms, prof.ev[i], prof.ev[i + 1])) != hipSuccess)
+                return hip_fail(e, "hipEventElapsedTime");
+            tot += ms;
+            mn = std::min(mn, (double)ms);
+            mx = std::max(mx, (double)ms);
+        }
+        for (double b : prof.bytes) by += b;
+        *launches = (int)(prof.used / 2);
+        *total_ms = tot;
+        *total_bytes = by;
+        *min_ms = prof.used ? mn : 0;
+        *max_ms = mx;
+        return NC_OK;
     }
 
     bool tied() const { return cfg.arch == NC_ARCH_MINICPM || cfg.arch == NC_ARCH_OPENELM; }
@@ -135,6 +210,7 @@ public:
         }
         st = stream_of(nullptr);
         adt = c->wdtype == NC_F16 ? NC_F16 : NC_Q8;
+        if (const char* g = std::getenv("NC_DECODE_GRAPH")) use_graph = std::atoi(g) != 0;
         d = c->n_embd;
         const int mc = c->max_ctx;
         int s;
@@ -408,51 +484,90 @@ public:
     }
 
     // Model::logits for rows [sp, n): tokens already on the device.  The
-    // last row's logits land in `logits`.
-    int forward(int sp, int n)
+    // last row's logits land in `logits`.  With dpos (graph capture of a
+    // decode step) the single row's position is read on the device instead
+    // and sp / n are unused.
+    int forward(int sp, int n, const int* dpos = nullptr)
     {
-        const int R = n - sp;
+        const int R = dpos ? 1 : n - sp;
         const int pd = pitch(d);
+        const size_t off = dpos ? 0 : (size_t)sp * pd;  // host-side offset of position-indexed rows
         const bool minicpm = cfg.arch == NC_ARCH_MINICPM;
         const float bs = branch_scale();
         int s;
         // embedding (+ MiniCPM's x12, minicpm.cpp:96)
-        if ((s = embed_launch(&emb, tokens + sp, x0 + (size_t)sp * pd, pd, adt, R, minicpm ? 12.0f : 1.0f, st))) return s;
+        if ((s = embed_launch(&emb, dpos ? tokens : tokens + sp, x0 + off, pd, adt, R, minicpm ? 12.0f : 1.0f, st,
+                              dpos)))
+            return s;
         // first attention norm on the embeddings
-        if ((s = norm_launch(norm_kind(), adt, false, x0 + (size_t)sp * pd, pd, nullptr, 0, 1.0f, nullptr, 0,
-                             L[0].attn_norm, L[0].attn_norm_b, xn, pd, d, d, R, 1.0f, st)))
+        if ((s = norm_launch(norm_kind(), adt, false, x0 + off, pd, nullptr, 0, 1.0f, nullptr, 0, L[0].attn_norm,
+                             L[0].attn_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
             return s;
         const uint8_t* xin = x0;
         for (int l = 0; l < cfg.n_layers; l++) {
             Layer& y = L[l];
             const int pq = pitch(y.qd), pkv = pitch(y.kvd), pf = pitch(y.f);
             const int nqkv = y.qd + 2 * y.kvd;
-            if ((s = matvec_raw(xn, adt, pd, R, &y.qkv, qkv_raw, nqkv, st))) return s;
+            if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv))) return s;
             if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, sp, R,
-                                     q_act, pq, y.kc, pkv, y.vc, pkv, st)))
+                                     q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
                 return s;
-            if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, sp, n, st))) return s;
-            if ((s = matvec_raw(attn, adt, pq, R, &y.o, o_raw, d, st))) return s;
+            if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, sp, n, st, dpos,
+                                 cfg.max_ctx)))
+                return s;
+            if ((s = mv(attn, pq, R, &y.o, o_raw, d))) return s;
             // h = x + attn (MiniCPM: attn scaled first), then the MLP norm
-            if ((s = norm_launch(norm_kind(), adt, true, xin + (size_t)sp * pd, pd, o_raw, d, bs,
-                                 y.res1 + (size_t)sp * pd, pd, y.mlp_norm, y.mlp_norm_b, xn, pd, d, d, R, 1.0f, st)))
+            if ((s = norm_launch(norm_kind(), adt, true, xin + off, pd, o_raw, d, bs, y.res1 + off, pd, y.mlp_norm,
+                                 y.mlp_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
                 return s;
-            if ((s = matvec_raw(xn, adt, pd, R, &y.gu, gu_raw, 2 * y.f, st))) return s;
+            if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f))) return s;
             if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
-            if ((s = matvec_raw(m_act, adt, pf, R, &y.down, down_raw, d, st))) return s;
+            if ((s = mv(m_act, pf, R, &y.down, down_raw, d))) return s;
             // out = h + mlp, then the next layer's attention norm (or the final norm)
             const bool last = l + 1 == cfg.n_layers;
             const uint16_t* nw = last ? norm_w : L[l + 1].attn_norm;
             const uint16_t* nb = last ? norm_b : L[l + 1].attn_norm_b;
             const float post = last && minicpm ? 1.0f / 9 : 1.0f;  // minicpm.cpp:104-105
-            if ((s = norm_launch(norm_kind(), adt, true, y.res1 + (size_t)sp * pd, pd, down_raw, d, bs,
-                                 y.res2 + (size_t)sp * pd, pd, nw, nb, xn, pd, d, d, R, post, st)))
+            if ((s = norm_launch(norm_kind(), adt, true, y.res1 + off, pd, down_raw, d, bs, y.res2 + off, pd, nw, nb,
+                                 xn, pd, d, d, R, post, st, dpos)))
                 return s;
             xin = y.res2;
         }
         // lm head on the last row only, fp32 out (gten/modules.cpp:48-59,111-122)
         const nc_tensor* head = tied() ? &emb : &lm;
-        return matvec_raw(xn + (size_t)(R - 1) * pd, adt, pd, 1, head, logits, cfg.n_vocab, st);
+        return mv(xn + (size_t)(R - 1) * pd, pd, 1, head, logits, cfg.n_vocab);
+    }
+
+    // One decode step as a HIP graph: forward at the device-held position,
+    // then the greedy token written behind it and the position advanced, so
+    // consecutive replays decode consecutive tokens with no host work.
+    hipGraphExec_t step_graph = nullptr;
+    int* step_pos = nullptr;  // device copy of the decode position
+    unsigned long long* am_scratch = nullptr;
+
+    int capture_step_graph()
+    {
+        int s;
+        if (!step_pos && ((s = alloc_t(&step_pos, 16)) || (s = alloc_t(&am_scratch, 16)))) return s;
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "capture: sync");
+        if ((e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+            return hip_fail(e, "hipStreamBeginCapture");
+        const bool was_on = prof.on;
+        prof.on = false;
+        s = forward(0, 0, step_pos);
+        if (!s) s = argmax_advance_launch(logits, cfg.n_vocab, tokens, step_pos, am_scratch, st);
+        prof.on = was_on;
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(st, &g);
+        if (s) {
+            if (g) (void)hipGraphDestroy(g);
+            return s;
+        }
+        if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+        e = hipGraphInstantiate(&step_graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        return e == hipSuccess ? NC_OK : hip_fail(e, "hipGraphInstantiate");
     }
 
     int logits_call(const int32_t* toks, int n, int sp, float* out)
@@ -484,15 +599,32 @@ public:
     }
 
     // n_steps more greedy steps; the pending token sits at tokens[n_cur].
+    // Steps replay the captured step graph; while matvec profiling is on they
+    // are launched directly so each matvec can be bracketed by events.
+    bool use_graph = true;
+
     int decode(int n_steps)
     {
         NC_CHECK_ARG(n_cur > 0, "decode: no prefill");
         NC_CHECK_ARG(n_cur + n_steps <= cfg.max_ctx, "decode: %d + %d steps exceed max_ctx %d", n_cur, n_steps,
                      cfg.max_ctx);
+        if (n_steps <= 0) return NC_OK;
+        int s;
+        if (use_graph && !prof.on) {
+            if (!step_graph && (s = capture_step_graph())) return s;
+            const int pos = n_cur;
+            hipError_t e = hipMemcpyAsync(step_pos, &pos, 4, hipMemcpyHostToDevice, st);
+            if (e != hipSuccess) return hip_fail(e, "decode: position upload");
+            // the upload reads host memory asynchronously: wait before `pos` dies
+            if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "decode: sync");
+            for (int i = 0; i < n_steps; i++)
+                if ((e = hipGraphLaunch(step_graph, st)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+            n_cur += n_steps;
+            return NC_OK;
+        }
         for (int i = 0; i < n_steps; i++) {
             const int n = n_cur + 1;
-            int s = forward(n - 1, n);
-            if (s) return s;
+            if ((s = forward(n - 1, n))) return s;
             if ((s = argmax_launch(logits, cfg.n_vocab, tokens + n, st))) return s;
             n_cur = n;
         }
@@ -595,6 +727,19 @@ int nc_model_decode(void* model, int n_steps, int32_t* out)
     if (s || !out) return s;
     int n;
     return m->fetch_generated(out, m->n_cur + 1 - m->n_prompt, &n);
+}
+
+int nc_model_profile_begin(void* model, int max_launches)
+{
+    NC_CHECK_ARG(model, "model: null");
+    return static_cast<Decoder*>(model)->profile_begin(max_launches);
+}
+
+int nc_model_profile_end(void* model, int* launches, double* total_ms, double* total_bytes, double* min_ms,
+                         double* max_ms)
+{
+    NC_CHECK_ARG(model && launches && total_ms && total_bytes && min_ms && max_ms, "model: null");
+    return static_cast<Decoder*>(model)->profile_end(launches, total_ms, total_bytes, min_ms, max_ms);
 }
 
 int nc_model_generate(void* model, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out, int* n_out)
