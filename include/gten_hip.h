@@ -121,6 +121,15 @@ int nc_qkv_attn(const nc_tensor* q, const nc_tensor* k, const nc_tensor* v, nc_t
 int nc_expf(const float* x, float* y, int64_t n, void* stream);
 /* The same function evaluated on the host CPU (no GPU needed). */
 float nc_expf_host(float x);
+/* The left-to-right fp32 sum of non-negative terms of rms_norm (src/gten/
+ * ops.cpp:833-835) as the fused decode kernels compute it on the device (a
+ * workgroup-parallel restatement with the sequential loop's result):
+ * out[b] = sum of t[b*n .. b*n+n), n a multiple of 256 up to 4096; fast[b]
+ * = 1 when the parallel path (not its sequential fallback) produced it. */
+int nc_block_seq_sum(const float* t, int n, int count, float* out, int* fast, void* stream);
+/* Host run of the same decomposition (no GPU): binades predicted from a
+ * double prefix scaled by (1 + skew); *fast = 1 when its checks passed. */
+float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int* fast);
 /* Greedy pick of greedy_sample (src/gten/sampler.cpp:33-41): first index of
  * the maximum. */
 int nc_argmax(const float* x, int n, int32_t* out, void* stream);

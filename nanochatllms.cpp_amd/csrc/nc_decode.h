@@ -1,0 +1,58 @@
+// nc_decode.h -- the fused matvec kernels of the single-row decode step
+// (Q8 activations, Q4/Q8 weights): prologue and epilogue kinds and the
+// launch arguments.
+#pragma once
+
+#include "nc_runtime.h"
+
+namespace nc {
+
+// Prologue: how the activation row the matvec consumes is produced.
+//   PRO_X       the stored Act row at x (attention output)
+//   PRO_RMS     rms_norm(x[pos]) with gain norm_w (then post_scale)
+//   PRO_RES_RMS h = Act(res_in[pos] + Act(raw_in [* bscale])) -- the
+//               residual add of the previous Linear's output -- stored to
+//               res_out[pos], then rms_norm(h) as PRO_RMS
+//   PRO_SWIGLU  Act(Act(silu(Act(g))) * Act(u)) of raw_in = [g | u]
+enum DmvPrologue { PRO_X = 0, PRO_RMS = 1, PRO_RES_RMS = 2, PRO_SWIGLU = 3 };
+// Epilogue: EPI_RAW writes the fp32 dot products; EPI_ARGMAX also writes the
+// greedy token to tokens[pos + 1] (and *pos_out = pos + 1 when dpos is set);
+// EPI_SWIGLU takes fused gate|up weights [2f, K] and writes
+// m_out = Act(Act(silu(Act(g))) * Act(u)) ([f] Act row; raw, when set, gets
+// the fp32 gate|up values).
+enum DmvEpilogue { EPI_RAW = 0, EPI_ARGMAX = 1, EPI_SWIGLU = 2 };
+
+struct DmvArgs {
+    const uint32_t* wq = nullptr;  // weight codes, lane-permuted blocks
+    const uint16_t* wd = nullptr;  // weight deltas
+    int N = 0, nb = 0;             // weight rows, 32-value blocks per row (K = 32 nb)
+    int ngroups = 0;               // set by the launcher
+    int pos = 0;                   // the row's position, or *dpos when dpos is set
+    const int* dpos = nullptr;
+    const uint8_t* x = nullptr;    // PRO_X: the row; PRO_RMS: [positions, K] Act rows
+    int x_pitch = 0;
+    const float* raw_in = nullptr;      // PRO_RES_RMS: [K] fp32; PRO_SWIGLU: [2K] fp32
+    const uint8_t* res_in = nullptr;    // PRO_RES_RMS: [positions, K] Act rows
+    uint8_t* res_out = nullptr;         // PRO_RES_RMS: [positions, K] Act rows (row pos written)
+    int res_pitch = 0;
+    float bscale = 1.0f;                // PRO_RES_RMS: scale of the branch output (1: none)
+    const uint16_t* norm_w = nullptr;   // PRO_RMS / PRO_RES_RMS gain (fp16)
+    float post_scale = 1.0f;            // scale of the normalized row (1: none)
+    float* raw = nullptr;               // fp32 dot products [N]
+    uint8_t* m_out = nullptr;           // EPI_SWIGLU
+    int32_t* tokens = nullptr;          // EPI_ARGMAX
+    int* pos_out = nullptr;
+    unsigned long long* amax = nullptr;  // EPI_ARGMAX scratch (kDmvArgmaxWords zeroed words, left zeroed)
+};
+
+constexpr int kDmvArgmaxWords = 320 + 4096;
+
+// Whether decode_matvec takes this weight dtype, shape and prologue.
+bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi);
+
+// One fused launch on `st`; with events, the dispatch records them at the
+// kernel's own start and end.
+int decode_matvec(const DmvArgs& a, int wdtype, int pro, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
+                  hipEvent_t ev1 = nullptr);
+
+}  // namespace nc

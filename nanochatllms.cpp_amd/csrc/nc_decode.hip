@@ -1,0 +1,585 @@
+// nc_decode.hip -- fused matvec kernels of the single-row decode step (Q8
+// activations, Q4/Q8 weights).
+//
+// Each Linear of a decode step is one launch that also produces its own
+// input row: the residual add of the previous Linear's output, the
+// rms_norm, or SwiGLU (prologues), so a layer takes four matvec launches
+// plus qkv_post and attention, and no workgroup waits for another.  Every
+// workgroup computes the prologue row itself (it is a few KB, read from L2)
+// while its first weights are in flight; workgroup 0 stores the residual
+// row the reference keeps.  The arithmetic is exactly that of the unfused
+// path (nc_matvec.hip, nc_elementwise.hip): the reference's block dot
+// product and fold order, and an Act write + read wherever the reference
+// stores an intermediate row:
+//   residual   h = Act(a + Act(y)) (MiniCPM: y = Act(Act(y) * scale)),
+//              Residual::forward, gten/modules.cpp:66-76, minicpm/minicpm.cpp:57-66
+//   rms_norm   y = h / (sqrt(sum h^2 / d) + 1e-6) * g, gten/ops.cpp:830-903,
+//              the sum of squares in index order (nc_seqsum.h)
+//   SwiGLU     Act(Act(silu(Act(g))) * Act(u)), tinyllama/tinyllama.cpp:88-97
+//   lm head    greedy token: first index of the largest logit (sampler.cpp:33-41)
+// Prologue rows are handled 8 values per thread, so a 32-value Q8 block is
+// one lane quad and its absmax takes two DPP steps.
+//
+// Workgroups walk row groups g, g + grid, ... (the grid is capped at what
+// the GPU holds at once) and request the next group's weights before they
+// fold the current one.
+#include <hip/hip_ext.h>
+
+#include <algorithm>
+
+#include "nc_act.h"
+#include "nc_decode.h"
+#include "nc_qdot.h"
+#include "nc_seqsum.h"
+
+namespace nc {
+
+constexpr int kDmvThreads = 256;
+constexpr int kDmvMaxItems = 4;     // weight blocks per thread and row group
+constexpr int kDmvNormChunks = 2;   // PRO_RMS / PRO_RES_RMS: 8-value chunks per thread (K <= 4096)
+constexpr int kDmvMaxGrid = 4096;
+
+// Q8 round trip of 8 values of one block held by a lane quad:
+// q8_quantize_block (gten/quants.cpp:16-30) -- absmax, delta = absmax/127,
+// fp16 delta stored, scale 1/delta from the fp32 delta, roundf -- and the
+// read back (code * fp16 delta).  Codes and delta returned for storing.
+struct Q8Chunk {
+    int8_t q[8];
+    uint16_t d16;
+};
+
+__device__ __forceinline__ Q8Chunk quad_quantize(const float (&v)[8])
+{
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+    a = quad_max(a);
+    const float delta = a / 127.0f;
+    Q8Chunk r;
+    r.d16 = f2h(delta);
+    const float scale = delta != 0.0f ? 1.0f / delta : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.q[i] = (int8_t)roundf(v[i] * scale);
+    return r;
+}
+
+__device__ __forceinline__ void quad_roundtrip(float (&v)[8])
+{
+    const Q8Chunk c = quad_quantize(v);
+    const float d = h2f(c.d16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)c.q[i] * d;
+}
+
+// Chunk ch (values 8ch .. 8ch+7) of a Q8 Act row of K values.
+__device__ __forceinline__ void load_act_chunk(const uint8_t* row, int K, int ch, float (&v)[8])
+{
+    const uint2 q = *reinterpret_cast<const uint2*>(row + (size_t)ch * 8);
+    const float d = h2f(reinterpret_cast<const uint16_t*>(row + K)[ch >> 2]);
+    const uint32_t w[2] = {q.x, q.y};
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)(int8_t)((w[i >> 2] >> (8 * (i & 3))) & 0xFFu) * d;
+}
+
+__device__ __forceinline__ void store_act_chunk(uint8_t* row, int K, int ch, const Q8Chunk& c)
+{
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)c.q[i] << (8 * (i & 3));
+    *reinterpret_cast<uint2*>(row + (size_t)ch * 8) = make_uint2(w[0], w[1]);
+    if ((ch & 3) == 0) reinterpret_cast<uint16_t*>(row + K)[ch >> 2] = c.d16;
+}
+
+__device__ __forceinline__ void load_f32_chunk(const float* p, int ch, float (&v)[8])
+{
+    const float4 a = reinterpret_cast<const float4*>(p)[2 * ch];
+    const float4 b = reinterpret_cast<const float4*>(p)[2 * ch + 1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// Argmax key: order-preserving float bits << 32 | ~index, so the largest
+// key is the first index of the largest value.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx)
+{
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// The prologue: builds the activation row the matvec consumes and stages
+// it in LDS by AVX lane (xs).  The inputs are requested first, then
+// load_w() requests the workgroup's first weights, and the row is built
+// while the weights are in flight (LDS barriers do not wait for global
+// loads).  sq: K floats of LDS for the squares and the Act row.  Ends with
+// an LDS barrier.
+template <int PRO, class LoadW>
+__device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t* xs, float* sq, SsShared& ssh,
+                                             LoadW&& load_w)
+{
+    const int tid = threadIdx.x;
+    const int nb = A.nb, K = nb * 32;
+    const int nch = K / 8;
+    uint8_t* xq = reinterpret_cast<uint8_t*>(sq);
+    if (PRO == PRO_X) {
+        XRaw xr{};
+        if (tid < nb) xr = load_x_block(A.x, nb, tid);
+        load_w();
+        if (tid < nb) stage_x_block(xr, xs + tid * 16);
+    } else if (PRO == PRO_SWIGLU) {
+        // m = Act(Act(silu(Act(g))) * Act(u)) chunk by chunk, into xq
+        float gv[8], uv[8];
+        int ch = tid;
+        const bool v0 = ch < nch;
+        load_f32_chunk(A.raw_in, v0 ? ch : 0, gv);
+        load_f32_chunk(A.raw_in + K, v0 ? ch : 0, uv);
+        load_w();
+        for (;;) {
+            const bool valid = ch < nch;
+            quad_roundtrip(gv);
+#pragma unroll
+            for (int i = 0; i < 8; i++) gv[i] = gv[i] / (1.0f + expf_ref(-gv[i]));
+            quad_roundtrip(gv);
+            quad_roundtrip(uv);
+            float mv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) mv[i] = gv[i] * uv[i];
+            const Q8Chunk q = quad_quantize(mv);
+            if (valid) store_act_chunk(xq, K, ch, q);
+            ch += kDmvThreads;
+            if (ch - tid >= nch) break;  // uniform: the next round has no valid chunk
+            const int cc = ch < nch ? ch : 0;
+            load_f32_chunk(A.raw_in, cc, gv);
+            load_f32_chunk(A.raw_in + K, cc, uv);
+        }
+        lds_barrier();
+        if (tid < nb) stage_x_block(load_x_block(xq, nb, tid), xs + tid * 16);
+    } else {
+        // h: the stored row (PRO_RMS) or the residual sum (PRO_RES_RMS)
+        float h[kDmvNormChunks][8], gain[kDmvNormChunks][8];
+        float av[kDmvNormChunks][8], ov[kDmvNormChunks][8];
+        const uint8_t* arow = (PRO == PRO_RMS ? A.x : A.res_in) + (size_t)pos * (PRO == PRO_RMS ? A.x_pitch : A.res_pitch);
+#pragma unroll
+        for (int j = 0; j < kDmvNormChunks; j++) {
+            const int ch = tid + j * kDmvThreads;
+            const int cc = ch < nch ? ch : 0;
+            load_act_chunk(arow, K, cc, av[j]);
+            if (PRO == PRO_RES_RMS) load_f32_chunk(A.raw_in, cc, ov[j]);
+            const uint4 gw = reinterpret_cast<const uint4*>(A.norm_w)[cc];
+            const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
+        }
+        load_w();
+#pragma unroll
+        for (int j = 0; j < kDmvNormChunks; j++) {
+            const int ch = tid + j * kDmvThreads;
+            const bool valid = ch < nch;
+            if (j * kDmvThreads >= nch) break;  // uniform
+            if (PRO == PRO_RES_RMS) {
+                quad_roundtrip(ov[j]);
+                if (A.bscale != 1.0f) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) ov[j][i] = ov[j][i] * A.bscale;
+                    quad_roundtrip(ov[j]);
+                }
+                float s[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) s[i] = av[j][i] + ov[j][i];
+                const Q8Chunk q = quad_quantize(s);
+                if (valid && blockIdx.x == 0) store_act_chunk(A.res_out + (size_t)pos * A.res_pitch, K, ch, q);
+                const float d = h2f(q.d16);
+#pragma unroll
+                for (int i = 0; i < 8; i++) h[j][i] = (float)q.q[i] * d;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) h[j][i] = av[j][i];
+            }
+            if (valid) {
+                const float4 s0 = make_float4(h[j][0] * h[j][0], h[j][1] * h[j][1], h[j][2] * h[j][2], h[j][3] * h[j][3]);
+                const float4 s1 = make_float4(h[j][4] * h[j][4], h[j][5] * h[j][5], h[j][6] * h[j][6], h[j][7] * h[j][7]);
+                reinterpret_cast<float4*>(sq)[2 * ch] = s0;
+                reinterpret_cast<float4*>(sq)[2 * ch + 1] = s1;
+            }
+        }
+        lds_barrier();
+        const float ss = block_seq_sum_nonneg(sq, K, ssh);
+        const float denom = sqrtf(ss / (float)K) + 1e-6f;
+        // the normalized row as stored (codes, then deltas) over sq's bytes
+#pragma unroll
+        for (int j = 0; j < kDmvNormChunks; j++) {
+            const int ch = tid + j * kDmvThreads;
+            if (j * kDmvThreads >= nch) break;  // uniform
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) y[i] = h[j][i] / denom * gain[j][i];
+            if (A.post_scale != 1.0f) {
+                quad_roundtrip(y);
+#pragma unroll
+                for (int i = 0; i < 8; i++) y[i] = y[i] * A.post_scale;
+            }
+            const Q8Chunk q = quad_quantize(y);
+            if (ch < nch) store_act_chunk(xq, K, ch, q);
+        }
+        lds_barrier();
+        if (tid < nb) stage_x_block(load_x_block(xq, nb, tid), xs + tid * 16);
+    }
+    lds_barrier();
+}
+
+template <int WT, int R, int PRO, int EPI>
+__global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
+{
+    constexpr int WD = WT == Q4 ? 4 : 8;
+    constexpr int WV = WD / 4;
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ SsShared ssh;
+    __shared__ unsigned long long s_key[R];
+    const int nb = A.nb;
+    const int tp = ((nb + 3) & ~3) + 4;
+    uint32_t* xs = lds;                                 // staged row: nb * 16 dwords
+    float* T = reinterpret_cast<float*>(xs + nb * 16);  // fold terms: R * 4 * tp
+    float* sq = T + R * 4 * tp;                         // prologue scratch
+    const int tid = threadIdx.x;
+    const int nitems = R * nb;
+    const int pos = A.dpos ? A.dpos[0] : A.pos;
+
+    uint4 wc[kDmvMaxItems][WV];
+    uint16_t dc[kDmvMaxItems];
+    auto load_group = [&](int g, uint4(&w)[kDmvMaxItems][WV], uint16_t(&dw)[kDmvMaxItems]) {
+#pragma unroll
+        for (int it = 0; it < kDmvMaxItems; it++) {
+            const int j = tid + it * kDmvThreads;
+            const int r = j / nb, i = j - r * nb;
+            const bool ok = j < nitems && g * R + r < A.N;
+            const size_t b = ok ? (size_t)(g * R + r) * nb + i : 0;
+            const uint4* src = reinterpret_cast<const uint4*>(A.wq + b * WD);
+#pragma unroll
+            for (int v = 0; v < WV; v++) w[it][v] = src[v];
+            dw[it] = A.wd[b];
+        }
+    };
+    int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
+    dmv_prologue<PRO>(A, pos, xs, sq, ssh, [&] { load_group(g, wc, dc); });
+
+    unsigned long long best = 0;  // EPI_ARGMAX: this workgroup's best key (thread 0)
+    for (; g < A.ngroups; g += gridDim.x) {
+        const int gn = g + gridDim.x;
+        uint4 wn[kDmvMaxItems][WV];
+        uint16_t dn[kDmvMaxItems];
+        if (gn < A.ngroups) load_group(gn, wn, dn);
+#pragma unroll
+        for (int it = 0; it < kDmvMaxItems; it++) {
+            const int j = tid + it * kDmvThreads;
+            if (j >= nitems) continue;
+            const int r = j / nb, i = j - r * nb;
+            float tv[4];
+            q_block_terms<WT>(xs + i * 16, wc[it], dc[it], tv);
+            float* t = T + r * 4 * tp + i;
+#pragma unroll
+            for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
+        }
+        lds_barrier();
+        if (tid < kWave) {
+            // thread 4r + k folds lane k of row r in block order
+            float acc = 0.0f;
+            if (tid < 4 * R) acc = seq_sum<16>(T + tid * tp, nb);
+            // lanes 4r..4r+3 hold row r's four lane sums; lane 4r reads
+            // the other three with quad_perm [1,0,3,2], [2,3,0,1], [3,2,1,0]
+            const float a1 = dpp_f<kDppQuadXor1>(acc);
+            const float a2 = dpp_f<kDppQuadXor2>(acc);
+            const float a3 = dpp_f<0x1B>(acc);
+            const float res = (acc + a1) + (a2 + a3);
+            const int row = g * R + (tid >> 2);
+            const bool mine = tid < 4 * R && (tid & 3) == 0 && row < A.N;
+            if (mine) A.raw[row] = res;
+            if (EPI == EPI_ARGMAX && (tid & 3) == 0 && tid < 4 * R)
+                s_key[tid >> 2] = mine ? argmax_key(res, row) : 0ull;
+        }
+        lds_barrier();
+        if (EPI == EPI_ARGMAX && tid == 0)
+            for (int r = 0; r < R; r++) best = s_key[r] > best ? s_key[r] : best;
+#pragma unroll
+        for (int it = 0; it < kDmvMaxItems; it++) {
+#pragma unroll
+            for (int v = 0; v < WV; v++) wc[it][v] = wn[it][v];
+            dc[it] = dn[it];
+        }
+    }
+
+    if (EPI == EPI_ARGMAX) {
+        // Two-level reduction over the workgroups: keys in slots, the last
+        // of each 32 workgroups reduces its slots, the last of those the
+        // rest.  Agent-scope stores and loads are coherent across the XCDs'
+        // L2s without a cache flush; the workgroup fences order each
+        // thread's own accesses.  Scratch layout (64-bit words): [0] top
+        // counter, [64, 192) level-1 results, [192, 320) level-1 counters,
+        // [320, 320 + grid) workgroup keys.
+        unsigned long long* top = A.amax;
+        unsigned long long* sub = A.amax + 64;
+        unsigned long long* cnt = A.amax + 192;
+        unsigned long long* slot = A.amax + 320;
+        const int G = gridDim.x, grp = blockIdx.x >> 5;
+        const int ngrp = (G + 31) >> 5;
+        if (tid < kWave) {
+            unsigned long long done = 0;
+            if (tid == 0) {
+                __hip_atomic_store(slot + blockIdx.x, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                done = __hip_atomic_fetch_add(cnt + grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            const int members = min(32, G - grp * 32);
+            done = __shfl(done, 0);
+            if (done == (unsigned long long)members - 1) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                unsigned long long k = tid < members
+                        ? __hip_atomic_load(slot + grp * 32 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : 0ull;
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) {
+                    const unsigned long long other = __shfl_xor(k, o);
+                    k = other > k ? other : k;
+                }
+                unsigned long long done2 = 0;
+                if (tid == 0) {
+                    __hip_atomic_store(cnt + grp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(sub + grp, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                    done2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                done2 = __shfl(done2, 0);
+                if (done2 == (unsigned long long)ngrp - 1) {
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                    unsigned long long b2 = 0;
+                    for (int q = tid; q < ngrp; q += kWave) {
+                        const unsigned long long o = __hip_atomic_load(sub + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        b2 = o > b2 ? o : b2;
+                    }
+#pragma unroll
+                    for (int o = 32; o >= 1; o >>= 1) {
+                        const unsigned long long other = __shfl_xor(b2, o);
+                        b2 = other > b2 ? other : b2;
+                    }
+                    if (tid == 0) {
+                        A.tokens[pos + 1] = (int32_t)(0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull));
+                        if (A.dpos) A.pos_out[0] = pos + 1;
+                        __hip_atomic_store(top, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Gate|up matvec with the SwiGLU epilogue: a workgroup owns output block b
+// (values 32b .. 32b+31) and computes its 32 gate rows (32b + r) and 32 up
+// rows (f + 32b + r) -- all of their weights requested up front -- in two
+// halves through the fold, then m = Act(Act(silu(Act(g))) * Act(u)) for the
+// block (tinyllama/tinyllama.cpp:88-97).  No workgroup waits for another.
+constexpr int kGluMaxItems = 18;  // 64 rows x nb blocks / 256 threads, nb <= 72
+
+template <int WT, int PRO>
+__global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
+{
+    constexpr int WD = WT == Q4 ? 4 : 8;
+    constexpr int WV = WD / 4;
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ SsShared ssh;
+    __shared__ float s_out[64];
+    const int nb = A.nb;
+    const int tp = ((nb + 3) & ~3) + 4;
+    uint32_t* xs = lds;
+    float* T = reinterpret_cast<float*>(xs + nb * 16);  // 32 rows x 4 lanes x tp
+    float* sq = T + 32 * 4 * tp;
+    const int tid = threadIdx.x;
+    const int f = A.N / 2, nblk = f / 32;
+    const int its = nb / 4, half = nb / 8;  // items per thread, per half
+    const int pos = A.dpos ? A.dpos[0] : A.pos;
+
+    uint4 w[kGluMaxItems][WV];
+    uint16_t dw[kGluMaxItems];
+    auto load_block = [&](int b) {
+#pragma unroll
+        for (int it = 0; it < kGluMaxItems; it++) {
+            if (it < its) {
+                const int j = tid + it * kDmvThreads;
+                const int r = j / nb, i = j - r * nb;
+                const int row = r < 32 ? 32 * b + r : f + 32 * b + (r - 32);
+                const size_t bi = (size_t)row * nb + i;
+                const uint4* src = reinterpret_cast<const uint4*>(A.wq + bi * WD);
+#pragma unroll
+                for (int v = 0; v < WV; v++) w[it][v] = src[v];
+                dw[it] = A.wd[bi];
+            }
+        }
+    };
+    int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks
+    dmv_prologue<PRO>(A, pos, xs, sq, ssh, [&] { load_block(b); });
+
+    for (; b < nblk; b += gridDim.x) {
+        if (b != (int)blockIdx.x) load_block(b);
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int it = 0; it < kGluMaxItems; it++) {
+                if (it >= h * half && it < (h + 1) * half) {
+                    const int j = tid + it * kDmvThreads;
+                    const int r = j / nb, i = j - r * nb;
+                    float tv[4];
+                    q_block_terms<WT>(xs + i * 16, w[it], dw[it], tv);
+                    float* t = T + (r - 32 * h) * 4 * tp + i;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
+                }
+            }
+            lds_barrier();
+            if (tid < 128) {
+                const float acc = seq_sum<16>(T + tid * tp, nb);
+                const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
+                if ((tid & 3) == 0) {
+                    s_out[32 * h + (tid >> 2)] = res;
+                    if (A.raw) A.raw[(h ? f : 0) + 32 * b + (tid >> 2)] = res;
+                }
+            }
+            lds_barrier();
+        }
+        if (tid < 32) {
+            const float gq = q8_roundtrip_lane(s_out[tid], true);
+            const float gs = q8_roundtrip_lane(gq / (1.0f + expf_ref(-gq)), true);
+            const float uq = q8_roundtrip_lane(s_out[32 + tid], true);
+            act_store<Q8>(A.m_out, 32 * b + tid, f, gs * uq, true);
+        }
+    }
+}
+
+// ============================================================ launcher ==
+
+namespace {
+
+int device_cus()
+{
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    return cus;
+}
+
+// Rows per group: the most rows whose blocks fit kDmvMaxItems per thread,
+// but no fewer than two groups per CU while a smaller group allows it.
+int dmv_rows(int nb, int N)
+{
+    int best = 0;
+    for (int r : {4, 8, 16}) {
+        if (r * nb > kDmvThreads * kDmvMaxItems) break;
+        if (best && (N + r - 1) / r < 2 * device_cus()) break;
+        best = r;
+    }
+    return best;
+}
+
+template <int WT, int R, int PRO, int EPI>
+int dmv_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    auto kern = k_dmv<WT, R, PRO, EPI>;
+    static int max_grid = 0;  // per instantiation: workgroups resident at once
+    if (!max_grid) {
+        int per_cu = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kDmvThreads, lds);
+        if (e != hipSuccess) return hip_fail(e, "decode matvec: occupancy");
+        max_grid = std::min(kDmvMaxGrid, std::max(1, per_cu) * device_cus());
+    }
+    A.ngroups = (A.N + R - 1) / R;
+    const dim3 grid(std::min(A.ngroups, max_grid));
+    if (ev0)
+        hipExtLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, ev0, ev1, 0, A);
+    else
+        hipLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, A);
+    return launch_status("k_dmv");
+}
+
+template <int WT, int PRO>
+int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    auto kern = k_dmv_glu<WT, PRO>;
+    static int max_grid = 0;
+    if (!max_grid) {
+        int per_cu = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kDmvThreads, lds);
+        if (e != hipSuccess) return hip_fail(e, "decode matvec: occupancy");
+        max_grid = std::min(kDmvMaxGrid, std::max(1, per_cu) * device_cus());
+    }
+    const dim3 grid(std::min(A.N / 64, max_grid));
+    if (ev0)
+        hipExtLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, ev0, ev1, 0, A);
+    else
+        hipLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, A);
+    return launch_status("k_dmv_glu");
+}
+
+template <int WT, int PRO, int EPI>
+int dmv_r(const DmvArgs& A, size_t lds0, int R, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    const int tp = ((A.nb + 3) & ~3) + 4;
+    const size_t lds = lds0 + (size_t)R * 4 * tp * 4;
+    if (R == 16) return dmv_go<WT, 16, PRO, EPI>(A, lds, st, ev0, ev1);
+    if (R == 8) return dmv_go<WT, 8, PRO, EPI>(A, lds, st, ev0, ev1);
+    return dmv_go<WT, 4, PRO, EPI>(A, lds, st, ev0, ev1);
+}
+
+}  // namespace
+
+bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi)
+{
+    if (wdtype != NC_Q4 && wdtype != NC_Q8) return false;
+    if (pro < PRO_X || pro > PRO_SWIGLU || epi < EPI_RAW || epi > EPI_SWIGLU) return false;
+    if (K <= 0 || K % 32 || N <= 0 || !dmv_rows(K / 32, N)) return false;
+    const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
+    if (norm && (K % kSsThreads || K > kDmvThreads * 8 * kDmvNormChunks)) return false;
+    if (epi == EPI_SWIGLU && (N % 64 || (K / 32) % 8 || K / 32 > 4 * kGluMaxItems || pro == PRO_SWIGLU))
+        return false;
+    return true;
+}
+
+int decode_matvec(const DmvArgs& A, int wdtype, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    if (!decode_matvec_supported(wdtype, A.nb * 32, A.N, pro, epi))
+        return fail(NC_ERR_ARG, "decode matvec: unsupported [%d x %d] dtype %d prologue %d epilogue %d", A.N,
+                    A.nb * 32, wdtype, pro, epi);
+    const int R = dmv_rows(A.nb, A.N);
+    const size_t K = (size_t)A.nb * 32;
+    // staged row (16 dwords per block), then the fold terms, then the
+    // prologue's squares / Act row
+    const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
+    const size_t lds0 = (size_t)A.nb * 64 + (norm ? K * 4 : (pro == PRO_X ? 0 : K + (size_t)A.nb * 2 + 16));
+    if (epi == EPI_SWIGLU) {
+        const int tp = ((A.nb + 3) & ~3) + 4;
+        const size_t lds = lds0 + (size_t)32 * 4 * tp * 4;
+        if (wdtype == NC_Q4) {
+            if (pro == PRO_RMS) return glu_go<Q4, PRO_RMS>(A, lds, st, ev0, ev1);
+            if (pro == PRO_RES_RMS) return glu_go<Q4, PRO_RES_RMS>(A, lds, st, ev0, ev1);
+            return glu_go<Q4, PRO_X>(A, lds, st, ev0, ev1);
+        }
+        if (pro == PRO_RMS) return glu_go<Q8, PRO_RMS>(A, lds, st, ev0, ev1);
+        if (pro == PRO_RES_RMS) return glu_go<Q8, PRO_RES_RMS>(A, lds, st, ev0, ev1);
+        return glu_go<Q8, PRO_X>(A, lds, st, ev0, ev1);
+    }
+#define DMV_EPI(WTV, PROV)                                                             \
+    if (epi == EPI_RAW) return dmv_r<WTV, PROV, EPI_RAW>(A, lds0, R, st, ev0, ev1);    \
+    return dmv_r<WTV, PROV, EPI_ARGMAX>(A, lds0, R, st, ev0, ev1);
+#define DMV_PRO(WTV)                                      \
+    switch (pro) {                                        \
+    case PRO_X: { DMV_EPI(WTV, PRO_X) }                   \
+    case PRO_RMS: { DMV_EPI(WTV, PRO_RMS) }               \
+    case PRO_RES_RMS: { DMV_EPI(WTV, PRO_RES_RMS) }       \
+    default: { DMV_EPI(WTV, PRO_SWIGLU) }                 \
+    }
+    if (wdtype == NC_Q4) { DMV_PRO(Q4) }
+    DMV_PRO(Q8)
+#undef DMV_PRO
+#undef DMV_EPI
+}
+
+}  // namespace nc

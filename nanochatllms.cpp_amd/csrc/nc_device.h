@@ -69,6 +69,42 @@ NC_HD float expf_ref(float x)
     return (float)y;
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// accesses, not for its global loads (which may stay in flight across it).
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// DPP lane moves (gfx9 encodings): quad_perm, row_shr:n (0x110 + n),
+// wave_shr:1 (0x138), row_bcast:15 (0x142), row_bcast:31 (0x143).  Lanes
+// without a source read 0 (bound_ctrl) or keep `old` (masked rows).
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = true>
+__device__ __forceinline__ int dpp_i(int v, int old = 0)
+{
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, BOUND_ZERO);
+}
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = true>
+__device__ __forceinline__ float dpp_f(float v, float old = 0.0f)
+{
+    return __builtin_bit_cast(float, dpp_i<CTRL, ROW_MASK, BOUND_ZERO>(__builtin_bit_cast(int, v),
+                                                                      __builtin_bit_cast(int, old)));
+}
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppWaveShr1 = 0x138;
+constexpr int kDppBcast15 = 0x142;
+constexpr int kDppBcast31 = 0x143;
+
+// Maximum over the 4 lanes of a quad (all four lanes active).
+__device__ __forceinline__ float quad_max(float v)
+{
+    v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+    return fmaxf(v, dpp_f<kDppQuadXor2>(v));
+}
+
 // Reduction of a value across the 32 lanes of a half-wave (xor butterfly).
 __device__ __forceinline__ float half_wave_max(float v)
 {

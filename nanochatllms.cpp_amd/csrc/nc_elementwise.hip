@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "nc_act.h"
+#include "nc_seqsum.h"
 #include "nc_kernels.h"
 
 namespace nc {
@@ -632,6 +633,23 @@ int nc_argmax(const float* x, int n, int32_t* out, void* stream)
 }  // extern "C"
 
 namespace nc {
+// One vector of n terms per workgroup through the block sum.
+__global__ __launch_bounds__(kSsThreads) void k_block_seq_sum(const float* __restrict__ t, int n, float* __restrict__ out,
+                                                             int* __restrict__ fast)
+{
+    extern __shared__ __align__(16) float buf[];
+    __shared__ SsShared sh;
+    const float* tv = t + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += kSsThreads) buf[i] = tv[i];
+    __syncthreads();
+    bool f = false;
+    const float s = block_seq_sum_nonneg(buf, n, sh, &f);
+    if (threadIdx.x == 0) {
+        out[blockIdx.x] = s;
+        fast[blockIdx.x] = f;
+    }
+}
+
 __global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, int64_t n)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -642,6 +660,53 @@ __global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, int64
 // The kernels' expf evaluated on the host (the same source), so the
 // algorithm can be checked against the host libm without a GPU.
 extern "C" float nc_expf_host(float x) { return nc::expf_ref(x); }
+
+// The sequential sum of non-negative terms (gten/ops.cpp:833-835) as the
+// fused norm prologues compute it, over `count` vectors of n terms.
+extern "C" int nc_block_seq_sum(const float* t, int n, int count, float* out, int* fast, void* stream)
+{
+    NC_CHECK_ARG(t && out && fast && count >= 0, "block_seq_sum: bad arguments");
+    NC_CHECK_ARG(n > 0 && n % nc::kSsThreads == 0 && n <= nc::kSsThreads * nc::kSsMaxPer,
+                 "block_seq_sum: n=%d (a multiple of %d up to %d)", n, nc::kSsThreads, nc::kSsThreads * nc::kSsMaxPer);
+    if (!count) return NC_OK;
+    hipLaunchKernelGGL(nc::k_block_seq_sum, dim3(count), dim3(nc::kSsThreads), (size_t)n * 4, stream_of(stream), t, n,
+                       out, fast);
+    return launch_status("k_block_seq_sum");
+}
+
+// The same segment / crossing decomposition run on the host with the
+// kernels' step, composition and check functions, the binades predicted
+// from a double-precision prefix scaled by (1 + skew): a skew makes
+// predictions wrong on purpose, which the segment checks must catch (the
+// result stays the sequential sum; *fast says whether the checks passed).
+extern "C" float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int* fast)
+{
+    using namespace nc;
+    double P = 0.0;
+    int Eb = ss_binade((float)(P * (1.0 + skew)));
+    SsMap cur = ss_identity();
+    float s = 0.0f;
+    bool ok = true;
+    for (int i = 0; i < n && ok; i++) {
+        const double Pa = P + (double)t[i];
+        const int Ea = ss_binade((float)(Pa * (1.0 + skew)));
+        if (Ea == Eb) {
+            cur = ss_compose(cur, ss_step(t[i], Eb));
+        } else {
+            ok = ss_apply(s, cur, Eb);
+            s = s + t[i];
+            cur = ss_identity();
+        }
+        P = Pa;
+        Eb = Ea;
+    }
+    if (ok) ok = ss_apply(s, cur, Eb);
+    if (fast) *fast = ok;
+    if (ok) return s;
+    float r = 0.0f;
+    for (int i = 0; i < n; i++) r = r + t[i];
+    return r;
+}
 
 // The device's std::exp(float) (gten/ops.cpp:752,1072) over an array.
 extern "C" int nc_expf(const float* x, float* y, int64_t n, void* stream)

@@ -28,57 +28,13 @@
 // order; the eight lanes of a row meet through wavefront shuffles.
 #include <hip/hip_ext.h>
 
-#include "nc_device.h"
 #include "nc_kernels.h"
+#include "nc_qdot.h"
 
 namespace nc {
 
 constexpr int kMvThreads = 256;
 constexpr int kMvMaxItems = 4;  // weight blocks per thread held in registers
-
-__device__ __forceinline__ uint32_t pick_pair(uint32_t lo, uint32_t hi, int odd)
-{
-    // bytes (2*odd, 2*odd+1) of lo followed by the same bytes of hi
-    return odd ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
-}
-
-// Stage block i of a Q8 activation row: 16 dwords
-// [xa0 xb0 xa1 xb1 xa2 xb2 xa3 xb3 | c0 c1 c2 c3 | dx 0 0 0]
-// xa_k = codes {2k,2k+1,2k+8,2k+9}, xb_k = codes {2k+16,2k+17,2k+24,2k+25},
-// c_k = -7 * (sum of those eight codes).
-struct XRaw {
-    uint4 a, b;
-    uint16_t d16;
-};
-
-__device__ __forceinline__ XRaw load_x_block(const uint8_t* xrow, int nb, int i)
-{
-    const uint4* q = reinterpret_cast<const uint4*>(xrow + (size_t)i * 32);
-    return XRaw{q[0], q[1], reinterpret_cast<const uint16_t*>(xrow + (size_t)nb * 32)[i]};
-}
-
-__device__ __forceinline__ void stage_x_block(const XRaw& x, uint32_t* dst)
-{
-    const uint4 a = x.a, b = x.b;
-    const uint32_t X[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    const uint16_t d16 = x.d16;
-    uint32_t o[16];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint32_t xa = pick_pair(X[k >> 1], X[2 + (k >> 1)], k & 1);
-        const uint32_t xb = pick_pair(X[4 + (k >> 1)], X[6 + (k >> 1)], k & 1);
-        o[2 * k] = xa;
-        o[2 * k + 1] = xb;
-        const int s = __builtin_amdgcn_sdot4((int)xa, 0x01010101, __builtin_amdgcn_sdot4((int)xb, 0x01010101, 0, false),
-                                             false);
-        o[8 + k] = (uint32_t)(-7 * s);
-    }
-    o[12] = __float_as_uint(h2f(d16));
-    o[13] = o[14] = o[15] = 0;
-    uint4* d = reinterpret_cast<uint4*>(dst);
-#pragma unroll
-    for (int v = 0; v < 4; v++) d[v] = make_uint4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
-}
 
 template <int WT, int R>
 __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restrict__ x, int x_pitch, int n_xrows,
@@ -123,34 +79,11 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restri
 #pragma unroll
         for (int it = 0; it < kMvMaxItems; it++) {
             if (tix[it] < 0) continue;
-            const uint4* s = reinterpret_cast<const uint4*>(xs + bix[it] * 16);
-            const uint4 s0 = s[0], s1 = s[1], s2 = s[2], s3 = s[3];
-            const uint32_t xa[4] = {s0.x, s0.z, s1.x, s1.z};
-            const uint32_t xb[4] = {s0.y, s0.w, s1.y, s1.w};
-            const int c[4] = {(int)s2.x, (int)s2.y, (int)s2.z, (int)s2.w};
-            const float dd = __uint_as_float(s3.x) * h2f(dw16[it]);
+            float tv[4];
+            q_block_terms<WT>(xs + bix[it] * 16, w[it], dw16[it], tv);
             float* t = T + tix[it];
-            uint32_t W[WD];
 #pragma unroll
-            for (int v = 0; v < WD / 4; v++) {
-                W[4 * v] = w[it][v].x;
-                W[4 * v + 1] = w[it][v].y;
-                W[4 * v + 2] = w[it][v].z;
-                W[4 * v + 3] = w[it][v].w;
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                int L;
-                if (WT == Q4) {
-                    const uint32_t P = W[k];
-                    L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)xa[k], c[k], false);
-                    L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)xb[k], L, false);
-                } else {
-                    L = __builtin_amdgcn_sdot4((int)W[2 * k], (int)xa[k], 0, false);
-                    L = __builtin_amdgcn_sdot4((int)W[2 * k + 1], (int)xb[k], L, false);
-                }
-                t[k * tp] = (float)L * dd;
-            }
+            for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
         }
         __syncthreads();
         if (tid < kWave) {

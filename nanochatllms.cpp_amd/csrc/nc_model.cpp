@@ -24,6 +24,7 @@
 #include <memory>
 #include <vector>
 
+#include "nc_decode.h"
 #include "nc_kernels.h"
 
 namespace nc {
@@ -81,6 +82,11 @@ public:
     int n_cur = 0;        // tokens in the sequence processed so far
     int n_prompt = 0;     // prompt length of the current generation
     int max_qkv = 0, max_qd = 0, max_f = 0;
+    // Single-row steps run the fused decode kernels (nc_decode.hip) when the
+    // shapes allow it (Q8 activations, RMS norms); NC_DECODE_FUSED=0 keeps
+    // the op-by-op path.
+    bool fused = false;
+    unsigned long long* am_scratch = nullptr;  // zeroed argmax scratch of the greedy step
 
     // Matvec launch timing: a start/end event pair recorded on the model's
     // stream around every matvec launch while profiling is on.
@@ -254,6 +260,9 @@ public:
             (s = alloc_t(&gu_raw, (size_t)mc * 2 * max_f * 4)) || (s = alloc_t(&down_raw, (size_t)mc * d * 4)) ||
             (s = alloc_t(&logits, (size_t)c->n_vocab * 4)) || (s = alloc_t(&tokens, (size_t)(mc + 1) * 4)))
             return s;
+        if ((s = alloc_t(&am_scratch, (size_t)kDmvArgmaxWords * 8))) return s;
+        fused = fused_supported();
+        if (const char* f = std::getenv("NC_DECODE_FUSED")) fused = fused && std::atoi(f) != 0;
         // RoPE table from the host libm, the reference's expression
         d_half = static_cast<int>((float)c->d_head * c->rope_pct) / 2;
         std::vector<float> tab((size_t)mc * std::max(d_half, 1) * 2);
@@ -487,9 +496,10 @@ public:
     // last row's logits land in `logits`.  With dpos (graph capture of a
     // decode step) the single row's position is read on the device instead
     // and sp / n are unused.
-    int forward(int sp, int n, const int* dpos = nullptr)
+    int forward(int sp, int n, int* dpos = nullptr)
     {
         const int R = dpos ? 1 : n - sp;
+        if (R == 1 && fused) return forward_fused(sp, dpos);
         const int pd = pitch(d);
         const size_t off = dpos ? 0 : (size_t)sp * pd;  // host-side offset of position-indexed rows
         const bool minicpm = cfg.arch == NC_ARCH_MINICPM;
@@ -538,17 +548,135 @@ public:
         return mv(xn + (size_t)(R - 1) * pd, pd, 1, head, logits, cfg.n_vocab);
     }
 
+    bool fused_supported() const
+    {
+        if (adt != NC_Q8 || norm_kind() != kNormRms) return false;
+        const int wt = cfg.wdtype;
+        for (const Layer& y : L)
+            if (!decode_matvec_supported(wt, d, y.qd + 2 * y.kvd, PRO_RES_RMS, EPI_RAW) ||
+                !decode_matvec_supported(wt, y.qd, d, PRO_X, EPI_RAW) ||
+                !decode_matvec_supported(wt, d, 2 * y.f, PRO_RES_RMS, EPI_SWIGLU) ||
+                !decode_matvec_supported(wt, y.f, d, PRO_X, EPI_RAW))
+                return false;
+        return decode_matvec_supported(wt, d, cfg.n_vocab, PRO_RES_RMS, EPI_ARGMAX);
+    }
+
+    // Algorithmic HBM bytes of one fused launch: weights once, the prologue
+    // inputs, the residual row written and the fp32 outputs.
+    static double fused_bytes(const nc_tensor* w, int pro, int epi)
+    {
+        const double N = w->rows, K = w->cols, row = (K / 32) * 34.0;
+        double b = N * (K / 32) * (w->dtype == NC_Q8 ? 34.0 : 18.0);
+        b += epi == EPI_SWIGLU ? (N / 64) * 34.0 : 4.0 * N;
+        if (pro == PRO_X) b += row;
+        if (pro == PRO_RMS) b += row + 2.0 * K;
+        if (pro == PRO_RES_RMS) b += 2.0 * row + 4.0 * K + 2.0 * K;
+        if (pro == PRO_SWIGLU) b += 8.0 * K;
+        return b;
+    }
+
+    int dmv(DmvArgs a, const nc_tensor* w, int pro, int epi)
+    {
+        a.wq = (const uint32_t*)w->data;
+        a.wd = (const uint16_t*)w->deltas;
+        a.N = w->rows;
+        a.nb = w->cols / 32;
+        const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
+        int s = timed ? decode_matvec(a, w->dtype, pro, epi, st, prof.ev[prof.used], prof.ev[prof.used + 1])
+                      : decode_matvec(a, w->dtype, pro, epi, st);
+        if (s) return s;
+        if (timed) {
+            prof.used += 2;
+            prof.bytes.push_back(fused_bytes(w, pro, epi));
+        }
+        return NC_OK;
+    }
+
+    // One decode step (row `pos`, or *dpos under graph replay) with the fused
+    // kernels.  Each matvec builds its own input row: layer l's qkv takes
+    // the previous layer's MLP residual add and the attention norm, o takes
+    // the attention output, gate|up the attention residual add and the MLP
+    // norm (and ends with SwiGLU), down the SwiGLU row; the lm head takes the last residual
+    // add and the final norm and writes the greedy token to tokens[pos + 1]
+    // (advancing *dpos).  Residual rows are stored where forward() stores
+    // them (res1 / res2 at the position), with the same requantization
+    // points.
+    int forward_fused(int pos, int* dpos)
+    {
+        const int pd = pitch(d);
+        const bool minicpm = cfg.arch == NC_ARCH_MINICPM;
+        const float bs = branch_scale();
+        int s;
+        if ((s = embed_launch(&emb, dpos ? tokens : tokens + pos, x0 + (dpos ? 0 : (size_t)pos * pd), pd, adt, 1,
+                              minicpm ? 12.0f : 1.0f, st, dpos)))
+            return s;
+        DmvArgs base;
+        base.pos = pos;
+        base.dpos = dpos;
+        base.res_pitch = pd;
+        base.bscale = bs;
+        for (int l = 0; l < cfg.n_layers; l++) {
+            Layer& y = L[l];
+            const int pq = pitch(y.qd), pkv = pitch(y.kvd);
+            const int nqkv = y.qd + 2 * y.kvd;
+            DmvArgs a = base;
+            a.norm_w = y.attn_norm;
+            a.raw = qkv_raw;
+            if (l == 0) {
+                a.x = x0;
+                a.x_pitch = pd;
+                if ((s = dmv(a, &y.qkv, PRO_RMS, EPI_RAW))) return s;
+            } else {
+                a.res_in = L[l - 1].res1;
+                a.raw_in = down_raw;
+                a.res_out = L[l - 1].res2;
+                if ((s = dmv(a, &y.qkv, PRO_RES_RMS, EPI_RAW))) return s;
+            }
+            if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, pos, 1,
+                                     q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
+                return s;
+            if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, pos, pos + 1, st, dpos,
+                                 cfg.max_ctx)))
+                return s;
+            a = base;
+            a.x = attn;
+            a.raw = o_raw;
+            if ((s = dmv(a, &y.o, PRO_X, EPI_RAW))) return s;
+            a = base;
+            a.res_in = l == 0 ? x0 : L[l - 1].res2;
+            a.raw_in = o_raw;
+            a.res_out = y.res1;
+            a.norm_w = y.mlp_norm;
+            a.m_out = m_act;
+            if ((s = dmv(a, &y.gu, PRO_RES_RMS, EPI_SWIGLU))) return s;
+            a = base;
+            a.x = m_act;
+            a.raw = down_raw;
+            if ((s = dmv(a, &y.down, PRO_X, EPI_RAW))) return s;
+        }
+        DmvArgs a = base;
+        a.res_in = L[cfg.n_layers - 1].res1;
+        a.raw_in = down_raw;
+        a.res_out = L[cfg.n_layers - 1].res2;
+        a.norm_w = norm_w;
+        a.post_scale = minicpm ? 1.0f / 9 : 1.0f;  // minicpm.cpp:104-105
+        a.raw = logits;
+        a.tokens = tokens;
+        a.pos_out = dpos;
+        a.amax = am_scratch;
+        return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_ARGMAX);
+    }
+
     // One decode step as a HIP graph: forward at the device-held position,
     // then the greedy token written behind it and the position advanced, so
     // consecutive replays decode consecutive tokens with no host work.
     hipGraphExec_t step_graph = nullptr;
     int* step_pos = nullptr;  // device copy of the decode position
-    unsigned long long* am_scratch = nullptr;
 
     int capture_step_graph()
     {
         int s;
-        if (!step_pos && ((s = alloc_t(&step_pos, 16)) || (s = alloc_t(&am_scratch, 16)))) return s;
+        if (!step_pos && (s = alloc_t(&step_pos, 16))) return s;
         hipError_t e = hipStreamSynchronize(st);
         if (e != hipSuccess) return hip_fail(e, "capture: sync");
         if ((e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal)) != hipSuccess)
@@ -556,7 +684,7 @@ public:
         const bool was_on = prof.on;
         prof.on = false;
         s = forward(0, 0, step_pos);
-        if (!s) s = argmax_advance_launch(logits, cfg.n_vocab, tokens, step_pos, am_scratch, st);
+        if (!s && !fused) s = argmax_advance_launch(logits, cfg.n_vocab, tokens, step_pos, am_scratch, st);
         prof.on = was_on;
         hipGraph_t g = nullptr;
         e = hipStreamEndCapture(st, &g);
@@ -625,7 +753,7 @@ public:
         for (int i = 0; i < n_steps; i++) {
             const int n = n_cur + 1;
             if ((s = forward(n - 1, n))) return s;
-            if ((s = argmax_launch(logits, cfg.n_vocab, tokens + n, st))) return s;
+            if (!fused && (s = argmax_launch(logits, cfg.n_vocab, tokens + n, st))) return s;
             n_cur = n;
         }
         return NC_OK;
