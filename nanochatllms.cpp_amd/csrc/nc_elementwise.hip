@@ -684,23 +684,26 @@ extern "C" float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int*
     using namespace nc;
     double P = 0.0;
     int Eb = ss_binade((float)(P * (1.0 + skew)));
-    SsMap cur = ss_identity();
+    int c0 = 0, c1 = 0;
+    bool nz = false;
     float s = 0.0f;
     bool ok = true;
     for (int i = 0; i < n && ok; i++) {
         const double Pa = P + (double)t[i];
         const int Ea = ss_binade((float)(Pa * (1.0 + skew)));
         if (Ea == Eb) {
-            cur = ss_compose(cur, ss_step(t[i], Eb));
+            ss_advance(c0, c1, t[i], Eb, &c0, &c1);
+            nz = nz || t[i] != 0.0f;
         } else {
-            ok = ss_apply(s, cur, Eb);
+            ok = ss_apply(s, SsMap{c0, c1, nz}, Eb);
             s = s + t[i];
-            cur = ss_identity();
+            c0 = c1 = 0;
+            nz = false;
         }
         P = Pa;
         Eb = Ea;
     }
-    if (ok) ok = ss_apply(s, cur, Eb);
+    if (ok) ok = ss_apply(s, SsMap{c0, c1, nz}, Eb);
     if (fast) *fast = ok;
     if (ok) return s;
     float r = 0.0f;

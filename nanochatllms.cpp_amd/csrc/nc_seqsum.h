@@ -51,35 +51,36 @@ NC_HD SsMap ss_compose(const SsMap& a, const SsMap& b)
     return r;
 }
 
-// One step s -> RN(s + t) with s and the result in binade E: the units
-// added from parity 0 and from parity 1.  t / u is exact (a power-of-two
-// scale of a value below 2^(E+1), so below 2^24 units); a tie rounds to the
-// even result.
-NC_HD SsMap ss_step(float t, int E)
+// The open map (c0, c1) followed by one step s -> RN(s + x) with s and the
+// result in binade E: the step adds D = floor(q) + (frac(q) > 1/2) grid
+// units, q = x / u exact (a power-of-two scale of a value below 2^(E+1), so
+// below 2^24 units), plus one more on a tie when the current value is odd:
+// track 0 is at parity c0, track 1 at parity 1 + c1.
+NC_HD void ss_advance(int c0, int c1, float x, int E, int* n0, int* n1)
 {
-    const float q = __builtin_ldexpf(t, 150 - E);
+    const float q = __builtin_ldexpf(x, 150 - E);
     const float fl = __builtin_floorf(q);
     const float fr = q - fl;
     const int f = (int)fl;
-    const int up = fr > 0.5f ? 1 : 0;
-    const bool tie = fr == 0.5f;
-    SsMap m;
-    m.c0 = f + up + ((tie && (f & 1)) ? 1 : 0);   // parity 0: s/u + f odd when f odd
-    m.c1 = f + up + ((tie && !(f & 1)) ? 1 : 0);  // parity 1: odd when f even
-    m.nz = t != 0.0f;
-    return m;
+    const int base = f + (fr > 0.5f ? 1 : 0);
+    const int tie = fr == 0.5f ? 1 : 0;
+    *n0 = c0 + base + (tie & (c0 ^ f));
+    *n1 = c1 + base + (tie & (c1 ^ f ^ 1));
 }
 
 // Applies a segment map computed for binade E to the exact value s.
-// Returns false when s does not lie in E or the result leaves it.
+// Within binade E consecutive grid values have consecutive bit patterns
+// (E = 1 spans the subnormals too), so s + u C is bits(s) + C and the
+// parity of s / u is the last bit.  Returns false when s does not lie in E
+// or the result leaves it.
 NC_HD bool ss_apply(float& s, const SsMap& m, int E)
 {
     if (!m.nz) return true;
     if (E >= 255 || ss_binade(s) != E) return false;  // infinities and NaNs take the plain loop
-    const int units = (int)__builtin_ldexpf(s, 150 - E);  // exact: s is on the grid, < 2^24 units
-    const int after = units + ((units & 1) ? m.c1 : m.c0);
-    if (after >= (1 << 24)) return false;
-    s = __builtin_ldexpf((float)after, E - 150);
+    const int sb = __builtin_bit_cast(int, s);
+    const float r = __builtin_bit_cast(float, sb + ((sb & 1) ? m.c1 : m.c0));
+    if (ss_binade(r) != E) return false;
+    s = r;
     return true;
 }
 
@@ -87,13 +88,13 @@ NC_HD bool ss_apply(float& s, const SsMap& m, int E)
 
 constexpr int kSsThreads = 256;   // workgroup size the block sum is written for
 constexpr int kSsMaxPer = 16;     // terms per thread: n <= 4096
-constexpr int kSsMaxCross = 63;   // crossings handled before the fallback (one per lane of a wave)
+constexpr int kSsMaxCross = 63;   // crossings handled before the fallback
+constexpr int kSsMaxRec = 4;      // crossings one thread's chunk may hold before the fallback
 
 struct SsShared {
     float wf[kSsThreads / kWave];
     int wc0[kSsThreads / kWave], wc1[kSsThreads / kWave], wfl[kSsThreads / kWave], wcnt[kSsThreads / kWave];
-    int rc0[kSsMaxCross + 1], rc1[kSsMaxCross + 1], rE[kSsMaxCross + 1];
-    float rt[kSsMaxCross + 1];
+    int4 rec[kSsMaxCross + 1];  // crossing records: map (c0, c1), binade (0: no check), term bits
     int m;
     int ok;
     float result;
@@ -102,22 +103,23 @@ struct SsShared {
 // Segmented scan element: a parity map and flags (bit 0: nz, bit 1: the
 // element holds a crossing, i.e. its map restarts the open segment).
 struct SsSeg {
-    int c0, c1, f;
+    int c0, c1, f, n;  // n: crossings so far (a plain sum, not segmented)
 };
 
 // (a then b): b alone when b restarts, else the composition.
 __device__ __forceinline__ SsSeg ss_seg(const SsSeg& a, const SsSeg& b)
 {
-    if (b.f & 2) return b;
+    if (b.f & 2) return SsSeg{b.c0, b.c1, b.f, a.n + b.n};
     const SsMap m = ss_compose(SsMap{a.c0, a.c1, (a.f & 1) != 0}, SsMap{b.c0, b.c1, (b.f & 1) != 0});
-    return SsSeg{m.c0, m.c1, (m.nz ? 1 : 0) | (a.f & 2)};
+    return SsSeg{m.c0, m.c1, (m.nz ? 1 : 0) | (a.f & 2), a.n + b.n};
 }
 
 template <int CTRL, int ROW_MASK = 0xf, bool BZ = true>
 __device__ __forceinline__ SsSeg ss_dpp(const SsSeg& x)
 {
     // lanes without a source get 0s: the identity element
-    return SsSeg{dpp_i<CTRL, ROW_MASK, BZ>(x.c0), dpp_i<CTRL, ROW_MASK, BZ>(x.c1), dpp_i<CTRL, ROW_MASK, BZ>(x.f)};
+    return SsSeg{dpp_i<CTRL, ROW_MASK, BZ>(x.c0), dpp_i<CTRL, ROW_MASK, BZ>(x.c1), dpp_i<CTRL, ROW_MASK, BZ>(x.f),
+                 dpp_i<CTRL, ROW_MASK, BZ>(x.n)};
 }
 
 // Inclusive wave scans (row_shr steps within rows of 16, then the row
@@ -130,16 +132,6 @@ __device__ __forceinline__ float wave_scan_add(float v)
     v = v + dpp_f<0x118>(v);
     v = v + dpp_f<kDppBcast15, 0xa, false>(v);
     v = v + dpp_f<kDppBcast31, 0xc, false>(v);
-    return v;
-}
-__device__ __forceinline__ int wave_scan_add_i(int v)
-{
-    v = v + dpp_i<0x111>(v);
-    v = v + dpp_i<0x112>(v);
-    v = v + dpp_i<0x114>(v);
-    v = v + dpp_i<0x118>(v);
-    v = v + dpp_i<kDppBcast15, 0xa, false>(v);
-    v = v + dpp_i<kDppBcast31, 0xc, false>(v);
     return v;
 }
 __device__ __forceinline__ SsSeg wave_scan_seg(SsSeg x)
@@ -158,10 +150,18 @@ __device__ __forceinline__ SsSeg wave_scan_seg(SsSeg x)
 // threads of the workgroup; every thread returns the sum.  *fast (thread
 // 0's view) tells whether the parallel path was taken.  Synchronizes the
 // workgroup through LDS barriers only (global loads may stay in flight).
-__device__ float block_seq_sum_nonneg(const float* t, int n, SsShared& sh, bool* fast = nullptr)
+//
+// Thread j owns terms [j c, j c + c).  Thread 0 adds its chunk directly
+// (the exact start of everything after it, and the region where the running
+// sum crosses binades most often); every other thread walks its chunk once,
+// branch-free: binade predicted from an approximate prefix, step maps
+// composed, and up to four crossings recorded (more fall back).  A segmented
+// scan joins the chunks, and wave 0 replays the few records in order.
+template <int C>
+__device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* fast)
 {
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-    const int c = n / kSsThreads;
+    const int c = C ? C : n / kSsThreads;
     const int i0 = tid * c;
     float v[kSsMaxPer];
     if (c % 4 == 0) {
@@ -180,6 +180,8 @@ __device__ float block_seq_sum_nonneg(const float* t, int n, SsShared& sh, bool*
         for (int k = 0; k < kSsMaxPer; k++)
             if (k < c) v[k] = t[i0 + k];
     }
+    // chunk sum in order: for thread 0 this is the exact running sum after
+    // its chunk
     float cs = 0.0f;
 #pragma unroll
     for (int k = 0; k < kSsMaxPer; k++)
@@ -198,109 +200,108 @@ __device__ float block_seq_sum_nonneg(const float* t, int n, SsShared& sh, bool*
     I = I + WP;
     float A = dpp_f<kDppWaveShr1>(I);  // the previous lane's I
     if (lane == 0) A = WP;
-    // ---- walk 1: crossings of this chunk and the map after the last one
-    int ncross = 0;
-    SsMap tail = ss_identity();
-    {
+    // ---- walk (threads >= 1): binade of each step predicted from the
+    // approximate prefix; in-binade steps composed into the open map
+    // (c0, c1), crossing steps recorded with the map before them
+    int c0 = 0, c1 = 0, nz = 0, ncross = 0;
+    int4 rec[kSsMaxRec];  // (c0, c1, binade or 0, term bits) of this chunk's crossings
+#pragma unroll
+    for (int q = 0; q < kSsMaxRec; q++) rec[q] = make_int4(0, 0, 0, 0);
+    if (tid > 0) {
         float P = A;
         int Eb = ss_binade(A);
 #pragma unroll
         for (int k = 0; k < kSsMaxPer; k++) {
             if (k < c) {
-                const float Pa = k + 1 < c ? P + v[k] : I;
+                const float x = v[k];
+                const float Pa = k + 1 < c ? P + x : I;
                 const int Ea = ss_binade(Pa);
-                if (Ea == Eb) {
-                    tail = ss_compose(tail, ss_step(v[k], Eb));
-                } else {
-                    ncross++;
-                    tail = ss_identity();
+                const bool cross = Ea != Eb;
+                int n0, n1;
+                ss_advance(c0, c1, x, Eb, &n0, &n1);
+                const int nn = nz | (x != 0.0f ? 1 : 0);
+                if (__builtin_amdgcn_ballot_w64(cross)) {
+                    const int4 r = make_int4(c0, c1, nz ? Eb : 0, __builtin_bit_cast(int, x));
+#pragma unroll
+                    for (int q = 0; q < kSsMaxRec; q++)
+                        if (cross && ncross == q) rec[q] = r;
                 }
+                c0 = cross ? 0 : n0;
+                c1 = cross ? 0 : n1;
+                nz = cross ? 0 : nn;
+                ncross += cross ? 1 : 0;
                 P = Pa;
                 Eb = Ea;
             }
         }
     }
-    // ---- segmented scan of (tail, has-crossing) and scan of the counts
-    SsSeg x{tail.c0, tail.c1, (tail.nz ? 1 : 0) | (ncross > 0 ? 2 : 0)};
+    // ---- segmented scan of (open map, has-crossing) and scan of the counts
+    SsSeg x{c0, c1, nz | (ncross > 0 ? 2 : 0), ncross};
     x = wave_scan_seg(x);
-    int cnt = wave_scan_add_i(ncross);
+    const int over = __builtin_amdgcn_ballot_w64(ncross > kSsMaxRec) != 0;
     if (lane == kWave - 1) {
         sh.wc0[w] = x.c0;
         sh.wc1[w] = x.c1;
         sh.wfl[w] = x.f;
-        sh.wcnt[w] = cnt;
+        sh.wcnt[w] = x.n | (over << 30);
     }
     lds_barrier();
-    SsSeg pre{0, 0, 0};
-    int pre_cnt = 0;
-    for (int q = 0; q < w; q++) {
-        pre = ss_seg(pre, SsSeg{sh.wc0[q], sh.wc1[q], sh.wfl[q]});
-        pre_cnt += sh.wcnt[q];
-    }
+    SsSeg pre{0, 0, 0, 0};
+    int any_over = 0;
+    for (int q = 0; q < w; q++) pre = ss_seg(pre, SsSeg{sh.wc0[q], sh.wc1[q], sh.wfl[q], sh.wcnt[q] & 0xFFFF});
+    for (int q = 0; q < kSsThreads / kWave; q++) any_over |= sh.wcnt[q] >> 30;
     x = ss_seg(pre, x);
-    cnt += pre_cnt;
-    // exclusive values: the open segment entering this chunk, crossings before it
+    const int cnt = x.n;
+    // the open segment entering this chunk, and the crossings before it
     SsSeg in = ss_dpp<kDppWaveShr1>(x);
-    int base = dpp_i<kDppWaveShr1>(cnt);
-    if (lane == 0) {
-        in = pre;
-        base = pre_cnt;
-    }
-    // the final segment (after the last crossing) and the crossing count
-    if (tid == kSsThreads - 1) {
-        sh.m = cnt;
-        if (cnt <= kSsMaxCross) {
-            sh.rc0[cnt] = x.c0;
-            sh.rc1[cnt] = x.c1;
-            sh.rE[cnt] = (x.f & 1) ? ss_binade(I) : 0;
-        }
-    }
-    // ---- walk 2: records of the crossings, in index order
-    if (ncross > 0 && base + ncross <= kSsMaxCross) {
-        SsMap cur{in.c0, in.c1, (in.f & 1) != 0};
-        float P = A;
-        int Eb = ss_binade(A);
-        int r = base;
+    if (lane == 0) in = pre;
+    const int base = in.n;
+    // records in crossing order: the first crossing of a chunk closes the
+    // segment open at its start
+    if (ncross > 0) {
+        // the first crossing closes the segment open at the chunk start
+        // (its binade: no crossing before it in this chunk)
+        const SsMap m0 = ss_compose(SsMap{in.c0, in.c1, (in.f & 1) != 0}, SsMap{rec[0].x, rec[0].y, rec[0].z != 0});
+        rec[0] = make_int4(m0.c0, m0.c1, m0.nz ? ss_binade(A) : 0, rec[0].w);
 #pragma unroll
-        for (int k = 0; k < kSsMaxPer; k++) {
-            if (k < c) {
-                const float Pa = k + 1 < c ? P + v[k] : I;
-                const int Ea = ss_binade(Pa);
-                if (Ea == Eb) {
-                    cur = ss_compose(cur, ss_step(v[k], Eb));
-                } else {
-                    sh.rc0[r] = cur.c0;
-                    sh.rc1[r] = cur.c1;
-                    sh.rE[r] = cur.nz ? Eb : 0;
-                    sh.rt[r] = v[k];
-                    r++;
-                    cur = ss_identity();
-                }
-                P = Pa;
-                Eb = Ea;
-            }
-        }
+        for (int q = 0; q < kSsMaxRec; q++)
+            if (q < ncross && base + q < kSsMaxCross) sh.rec[base + q] = rec[q];
+    }
+    if (tid == kSsThreads - 1) {
+        sh.m = any_over ? kSsMaxCross + 1 : cnt;
+        if (cnt < kSsMaxCross) sh.rec[cnt] = make_int4(x.c0, x.c1, (x.f & 1) ? ss_binade(I) : 0, 0);
     }
     lds_barrier();
-    // ---- replay on wave 0: record r in lane r, segment maps and crossing
-    // adds applied in order (a uniform loop over readlanes)
+    // ---- replay on wave 0 from thread 0's exact chunk sum: record r in lane
+    // r; per record s = s + u C(parity) (when the segment holds a nonzero
+    // term), then the crossing add; the binade checks ride beside the chain
     if (w == 0) {
         const int mm = sh.m;
-        bool ok = mm <= kSsMaxCross;
+        int ok = mm < kSsMaxCross;
+        // within binade E consecutive grid values have consecutive bit
+        // patterns (E = 1 spans the subnormals too), so s + u C is bits + C
+        // and the parity of s / u is the last bit; the final record's term
+        // is +0, which leaves s as it is.  The chain state is kept in vector
+        // registers (the empty asm marks it lane-varying): scalar registers
+        // would cost a vector-to-scalar move per record.
+        int sb = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs));
         if (ok) {
-            const int rl = lane <= mm ? lane : 0;
-            const int lc0 = sh.rc0[rl], lc1 = sh.rc1[rl], lE = sh.rE[rl];
-            const float lt = sh.rt[rl];
-            float s = 0.0f;
+            asm volatile("" : "+v"(sb), "+v"(ok));
+#pragma unroll 4
             for (int r = 0; r <= mm; r++) {
-                const int E = __builtin_amdgcn_readlane(lE, r);
-                const SsMap sm{__builtin_amdgcn_readlane(lc0, r), __builtin_amdgcn_readlane(lc1, r), E != 0};
-                ok = ss_apply(s, sm, E) && ok;
-                if (r < mm) s = s + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lt), r));
+                const int4 R = sh.rec[r];  // same address on every lane: an LDS broadcast
+                const int E = R.z;
+                const int nb = sb + ((sb & 1) ? R.y : R.x);  // 0 units for a segment of zeros
+                const bool good = E == 0 || (E < 255 && ss_binade(__builtin_bit_cast(float, sb)) == E &&
+                                             ss_binade(__builtin_bit_cast(float, nb)) == E);
+                ok &= good ? 1 : 0;
+                sb = __builtin_bit_cast(int, __builtin_bit_cast(float, nb) + __builtin_bit_cast(float, R.w));
             }
-            if (lane == 0) sh.result = s;
         }
-        if (lane == 0) sh.ok = ok;
+        if (lane == 0) {
+            sh.result = __builtin_bit_cast(float, sb);
+            sh.ok = ok;
+        }
     }
     lds_barrier();
     if (!sh.ok) {
@@ -315,6 +316,16 @@ __device__ float block_seq_sum_nonneg(const float* t, int n, SsShared& sh, bool*
     const float res = sh.result;
     lds_barrier();  // sh reusable after return
     return res;
+}
+
+
+// Dispatch on the terms per thread (compile-time chunk lengths for the
+// model widths: 2048 -> 8, 2304 -> 9).
+__device__ __forceinline__ float block_seq_sum_nonneg(const float* t, int n, SsShared& sh, bool* fast = nullptr)
+{
+    if (n == 8 * kSsThreads) return block_seq_sum_impl<8>(t, n, sh, fast);
+    if (n == 9 * kSsThreads) return block_seq_sum_impl<9>(t, n, sh, fast);
+    return block_seq_sum_impl<0>(t, n, sh, fast);
 }
 
 #endif  // __HIPCC__
