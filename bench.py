@@ -12,9 +12,18 @@ n - 1, device argmax, token fed back on the device).
 
 Prints one JSON line.  `value` is decode tokens/s over exactly K timed steps
 (warmup steps run first, on the same sequence).  `roofline` is for the
-quantized matvec kernel: algorithmic bytes per launch (weights once +
-activation row + fp32 outputs) over the launch's average duration, both
-measured with HIP events on the model stream during the timed steps.
+kernel that takes the most time in a decode step (the fused gate|up matvec
+for the Q4/Q8 workloads): algorithmic bytes per launch (weights once +
+its input rows + its output rows) over the launch's average duration, both
+measured with HIP events on the model stream during a second pass over the
+same timed steps with every kernel launched directly; `per_kernel` gives
+the same figures for each matvec role.  `traffic` is the measured HBM bytes
+per launch of that kernel, from the committed rocprofv3 counter summary
+(profiles/traffic.json), when one exists for the workload.
+
+    python bench.py --copy-calibration MIB   (one plain copy of MIB MiB: the
+                                              reference dispatch for the
+                                              profiler's byte counters)
 """
 import argparse
 import ctypes as C
@@ -31,6 +40,12 @@ from nc_pkg import nc  # noqa: E402
 
 METRIC = "decode tok/s (1 GPU) + Q4/Q8 matvec HBM GB/s as % of MI355X peak"
 HBM_PEAK_GBS = 8000.0
+# kernel names (as the profiler lists them) of the fused decode matvecs
+FUSED_KERNEL = {"qkv": "k_dmv (qkv, residual add + rms_norm prologue)",
+                "o": "k_dmv (o)",
+                "gate_up": "k_dmv_glu (gate|up, residual add + rms_norm prologue, SwiGLU epilogue)",
+                "down": "k_dmv (down)",
+                "lm_head": "k_dmv (lm head, residual add + final norm prologue, greedy-token epilogue)"}
 
 
 def workload_config(name):
@@ -83,6 +98,35 @@ def cpu_baseline(w, prompt, budget_s=12.0):
                       f"({dt:.1f} s), same weights and prompt, OpenMP threads = {threads}"}
 
 
+def copy_calibration(mib):
+    """One plain device copy of `mib` MiB (after a warmup copy): its counter
+    readings under rocprofv3 --pmc scale the matvec kernels' FETCH_SIZE /
+    WRITE_SIZE to bytes."""
+    nc.init(0)
+    n = mib << 20
+    a, b = nc.DeviceBuffer(n), nc.DeviceBuffer(n)
+    L = nc.lib()
+    nc.check(L.nc_copy_d2d(C.c_void_p(b.ptr), C.c_void_p(a.ptr), n, None))
+    nc.check(L.nc_synchronize())
+    t0 = time.perf_counter()
+    nc.check(L.nc_copy_d2d(C.c_void_p(b.ptr), C.c_void_p(a.ptr), n, None))
+    nc.check(L.nc_synchronize())
+    dt = time.perf_counter() - t0
+    print(json.dumps({"copy_bytes": n, "copy_ms": round(dt * 1e3, 4)}), flush=True)
+
+
+def traffic_for(workload, kernel_role):
+    """HBM bytes per launch of the role's kernel from the committed counter
+    summary, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    e = t.get(workload, {}).get(kernel_role)
+    return None if e is None else e.get("bytes_per_launch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,7 +136,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel directly instead of replaying "
                     "the captured decode-step graph (for profilers that do not follow graph launches)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); decode of these models runs as one "
               "independent stream per GPU, so N GPUs serve N streams at the 1-GPU rate.", file=sys.stderr)
@@ -133,13 +181,26 @@ def main():
     model.decode(args.steps)
     nc.check(L.nc_synchronize())
     dt_direct = time.perf_counter() - t1
-    prof = model.profile_end()
+    model.profile_end()
+    ms, nbytes, kind = model.profile_launches(launches_per_step * args.steps)
     model.close()
 
+    per_kernel = []
+    for k in sorted(set(kind.tolist())):
+        sel = kind == k
+        role = nc.PROF_ROLES[k & 7]
+        fused = bool(k & nc.PROF_FUSED)
+        avg_ms = float(ms[sel].mean())
+        avg_b = float(nbytes[sel].mean())
+        per_kernel.append({"role": role, "kernel": FUSED_KERNEL[role] if fused else "k_matvec_q",
+                           "launches": int(sel.sum()), "total_ms": round(float(ms[sel].sum()), 4),
+                           "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(avg_b),
+                           "achieved_gbs": round(avg_b / (avg_ms * 1e-3) / 1e9, 1)})
+    dom = max(per_kernel, key=lambda e: e["total_ms"])
+    traffic = traffic_for(args.workload, dom["role"])
+
     tok_s = args.steps / dt
-    avg_ms = prof["total_ms"] / max(prof["launches"], 1)
-    avg_bytes = prof["total_bytes"] / max(prof["launches"], 1)
-    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+    achieved = dom["achieved_gbs"]
     line = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -160,11 +221,11 @@ def main():
                    "timed_positions": [w["prompt"] + args.warmup, w["prompt"] + args.warmup + args.steps]},
         "prefill_tok_s": round(w["prompt"] / prefill_s, 1),
         "direct_launch_tok_s": round(args.steps / dt_direct, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_matvec_q (every matvec launch of the timed steps, replayed with direct launches)",
-                     "avg_launch_us": round(avg_ms * 1e3, 3), "avg_launch_bytes": round(avg_bytes),
-                     "launches": prof["launches"]},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": dom["kernel"], "avg_launch_us": dom["avg_launch_us"],
+                     "bytes_per_launch": dom["bytes_per_launch"], "launches": dom["launches"]},
+        "per_kernel": per_kernel,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, prompt)

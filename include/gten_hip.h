@@ -59,6 +59,10 @@ int nc_malloc(void** ptr, size_t bytes);
 int nc_free(void* ptr);
 int nc_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int nc_memcpy_d2h(void* dst, const void* src, size_t bytes);
+/* Device-to-device copy by a plain streaming kernel (bytes a multiple of
+ * 16, 16-byte aligned pointers); also the reference point that scales HBM
+ * byte counters of the profiler. */
+int nc_copy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int nc_memset_d(void* dst, int value, size_t bytes);
 int nc_synchronize(void);
 
@@ -213,6 +217,17 @@ int nc_model_decode(void* model, int n_steps, int32_t* out);
 int nc_model_profile_begin(void* model, int max_launches);
 int nc_model_profile_end(void* model, int* launches, double* total_ms, double* total_bytes, double* min_ms,
                          double* max_ms);
+/* The same launches one by one (after profile_end): duration, algorithmic
+ * bytes and role (NC_PROF_*, plus NC_PROF_FUSED for the fused single-row
+ * decode kernels, whose bytes also count their prologue inputs and
+ * residual / SwiGLU rows); *n_out <= cap launches written. */
+#define NC_PROF_QKV 0
+#define NC_PROF_O 1
+#define NC_PROF_GATE_UP 2
+#define NC_PROF_DOWN 3
+#define NC_PROF_LM_HEAD 4
+#define NC_PROF_FUSED 8
+int nc_model_profile_launches(void* model, int cap, float* ms, double* bytes, int* kind, int* n_out);
 
 #ifdef __cplusplus
 }

@@ -136,6 +136,8 @@ def lib():
         "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
         "nc_model_profile_begin": (I, [VP, I]),
         "nc_model_profile_end": (I, [VP, C.POINTER(I)] + [C.POINTER(C.c_double)] * 4),
+        "nc_model_profile_launches": (I, [VP, I, VP, VP, VP, C.POINTER(I)]),
+        "nc_copy_d2d": (I, [VP, VP, C.c_size_t, VP]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -156,6 +158,11 @@ def init(device=0):
 
 def _ptr(a):
     return a.ctypes.data_as(C.c_void_p)
+
+
+# Launch roles of nc_model_profile_launches (NC_PROF_* in gten_hip.h).
+PROF_ROLES = {0: "qkv", 1: "o", 2: "gate_up", 3: "down", 4: "lm_head"}
+PROF_FUSED = 8
 
 
 class DeviceBuffer:
@@ -246,6 +253,17 @@ class Model:
         check(lib().nc_model_profile_end(self.h, C.byref(n), *[C.byref(v) for v in vals]), "profile_end")
         total_ms, total_bytes, min_ms, max_ms = (v.value for v in vals)
         return dict(launches=n.value, total_ms=total_ms, total_bytes=total_bytes, min_ms=min_ms, max_ms=max_ms)
+
+    def profile_launches(self, cap):
+        """Per-launch (ms, algorithmic bytes, role) of the profiled launches."""
+        import numpy as np
+        ms = np.zeros(cap, np.float32)
+        by = np.zeros(cap, np.float64)
+        kind = np.zeros(cap, np.int32)
+        n = C.c_int()
+        check(lib().nc_model_profile_launches(self.h, cap, _ptr(ms), _ptr(by), _ptr(kind), C.byref(n)),
+              "profile_launches")
+        return ms[: n.value], by[: n.value], kind[: n.value]
 
     def close(self):
         if self.h:

@@ -94,6 +94,7 @@ public:
         bool on = false;
         std::vector<hipEvent_t> ev;
         std::vector<double> bytes;
+        std::vector<int> kind;  // NC_PROF_* role, + NC_PROF_FUSED for the fused kernels
         size_t used = 0;
     } prof;
 
@@ -115,7 +116,7 @@ public:
         return wb + rows * (xb + 4.0 * N);
     }
 
-    int mv(const uint8_t* x, int x_pitch, int rows, const nc_tensor* w, float* out, int out_pitch)
+    int mv(const uint8_t* x, int x_pitch, int rows, const nc_tensor* w, float* out, int out_pitch, int role)
     {
         const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
         int s = timed ? matvec_raw(x, adt, x_pitch, rows, w, out, out_pitch, st, prof.ev[prof.used],
@@ -125,6 +126,7 @@ public:
         if (timed) {
             prof.used += 2;
             prof.bytes.push_back(matvec_bytes(w, rows));
+            prof.kind.push_back(role);
         }
         return NC_OK;
     }
@@ -140,6 +142,7 @@ public:
         }
         prof.used = 0;
         prof.bytes.clear();
+        prof.kind.clear();
         prof.on = true;
         return NC_OK;
     }
@@ -164,6 +167,21 @@ public:
         *total_bytes = by;
         *min_ms = prof.used ? mn : 0;
         *max_ms = mx;
+        return NC_OK;
+    }
+
+    int profile_launches(int cap, float* ms, double* bytes, int* kind, int* n_out)
+    {
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "profile_launches");
+        const int n = std::min(cap, (int)(prof.used / 2));
+        for (int i = 0; i < n; i++) {
+            if ((e = hipEventElapsedTime(&ms[i], prof.ev[2 * i], prof.ev[2 * i + 1])) != hipSuccess)
+                return hip_fail(e, "hipEventElapsedTime");
+            bytes[i] = prof.bytes[i];
+            kind[i] = prof.kind[i];
+        }
+        *n_out = n;
         return NC_OK;
     }
 
@@ -518,21 +536,21 @@ public:
             Layer& y = L[l];
             const int pq = pitch(y.qd), pkv = pitch(y.kvd), pf = pitch(y.f);
             const int nqkv = y.qd + 2 * y.kvd;
-            if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv))) return s;
+            if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv, NC_PROF_QKV))) return s;
             if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, sp, R,
                                      q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
                 return s;
             if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, sp, n, st, dpos,
                                  cfg.max_ctx)))
                 return s;
-            if ((s = mv(attn, pq, R, &y.o, o_raw, d))) return s;
+            if ((s = mv(attn, pq, R, &y.o, o_raw, d, NC_PROF_O))) return s;
             // h = x + attn (MiniCPM: attn scaled first), then the MLP norm
             if ((s = norm_launch(norm_kind(), adt, true, xin + off, pd, o_raw, d, bs, y.res1 + off, pd, y.mlp_norm,
                                  y.mlp_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
                 return s;
-            if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f))) return s;
+            if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f, NC_PROF_GATE_UP))) return s;
             if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
-            if ((s = mv(m_act, pf, R, &y.down, down_raw, d))) return s;
+            if ((s = mv(m_act, pf, R, &y.down, down_raw, d, NC_PROF_DOWN))) return s;
             // out = h + mlp, then the next layer's attention norm (or the final norm)
             const bool last = l + 1 == cfg.n_layers;
             const uint16_t* nw = last ? norm_w : L[l + 1].attn_norm;
@@ -545,7 +563,7 @@ public:
         }
         // lm head on the last row only, fp32 out (gten/modules.cpp:48-59,111-122)
         const nc_tensor* head = tied() ? &emb : &lm;
-        return mv(xn + (size_t)(R - 1) * pd, pd, 1, head, logits, cfg.n_vocab);
+        return mv(xn + (size_t)(R - 1) * pd, pd, 1, head, logits, cfg.n_vocab, NC_PROF_LM_HEAD);
     }
 
     bool fused_supported() const
@@ -575,7 +593,7 @@ public:
         return b;
     }
 
-    int dmv(DmvArgs a, const nc_tensor* w, int pro, int epi)
+    int dmv(DmvArgs a, const nc_tensor* w, int pro, int epi, int role)
     {
         a.wq = (const uint32_t*)w->data;
         a.wd = (const uint16_t*)w->deltas;
@@ -588,6 +606,7 @@ public:
         if (timed) {
             prof.used += 2;
             prof.bytes.push_back(fused_bytes(w, pro, epi));
+            prof.kind.push_back(role | NC_PROF_FUSED);
         }
         return NC_OK;
     }
@@ -625,12 +644,12 @@ public:
             if (l == 0) {
                 a.x = x0;
                 a.x_pitch = pd;
-                if ((s = dmv(a, &y.qkv, PRO_RMS, EPI_RAW))) return s;
+                if ((s = dmv(a, &y.qkv, PRO_RMS, EPI_RAW, NC_PROF_QKV))) return s;
             } else {
                 a.res_in = L[l - 1].res1;
                 a.raw_in = down_raw;
                 a.res_out = L[l - 1].res2;
-                if ((s = dmv(a, &y.qkv, PRO_RES_RMS, EPI_RAW))) return s;
+                if ((s = dmv(a, &y.qkv, PRO_RES_RMS, EPI_RAW, NC_PROF_QKV))) return s;
             }
             if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, pos, 1,
                                      q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
@@ -641,18 +660,18 @@ public:
             a = base;
             a.x = attn;
             a.raw = o_raw;
-            if ((s = dmv(a, &y.o, PRO_X, EPI_RAW))) return s;
+            if ((s = dmv(a, &y.o, PRO_X, EPI_RAW, NC_PROF_O))) return s;
             a = base;
             a.res_in = l == 0 ? x0 : L[l - 1].res2;
             a.raw_in = o_raw;
             a.res_out = y.res1;
             a.norm_w = y.mlp_norm;
             a.m_out = m_act;
-            if ((s = dmv(a, &y.gu, PRO_RES_RMS, EPI_SWIGLU))) return s;
+            if ((s = dmv(a, &y.gu, PRO_RES_RMS, EPI_SWIGLU, NC_PROF_GATE_UP))) return s;
             a = base;
             a.x = m_act;
             a.raw = down_raw;
-            if ((s = dmv(a, &y.down, PRO_X, EPI_RAW))) return s;
+            if ((s = dmv(a, &y.down, PRO_X, EPI_RAW, NC_PROF_DOWN))) return s;
         }
         DmvArgs a = base;
         a.res_in = L[cfg.n_layers - 1].res1;
@@ -664,7 +683,7 @@ public:
         a.tokens = tokens;
         a.pos_out = dpos;
         a.amax = am_scratch;
-        return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_ARGMAX);
+        return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_ARGMAX, NC_PROF_LM_HEAD);
     }
 
     // One decode step as a HIP graph: forward at the device-held position,
@@ -861,6 +880,12 @@ int nc_model_profile_begin(void* model, int max_launches)
 {
     NC_CHECK_ARG(model, "model: null");
     return static_cast<Decoder*>(model)->profile_begin(max_launches);
+}
+
+int nc_model_profile_launches(void* model, int cap, float* ms, double* bytes, int* kind, int* n_out)
+{
+    NC_CHECK_ARG(model && cap >= 0 && ms && bytes && kind && n_out, "profile_launches: null argument");
+    return static_cast<Decoder*>(model)->profile_launches(cap, ms, bytes, kind, n_out);
 }
 
 int nc_model_profile_end(void* model, int* launches, double* total_ms, double* total_bytes, double* min_ms,

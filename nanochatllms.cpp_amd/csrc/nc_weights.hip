@@ -232,3 +232,23 @@ int nc_weight_quantize(const float* w, nc_tensor* out, void* stream)
 }
 
 }  // extern "C"
+
+// ============================================================ copy ==
+
+namespace nc {
+__global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+}
+}  // namespace nc
+
+extern "C" int nc_copy_d2d(void* dst, const void* src, size_t bytes, void* stream)
+{
+    NC_CHECK_ARG(dst && src && bytes % 16 == 0 && ((uintptr_t)dst | (uintptr_t)src) % 16 == 0,
+                 "copy_d2d: %zu bytes (16-byte multiples and alignment)", bytes);
+    if (!bytes) return NC_OK;
+    const size_t n = bytes / 16;
+    const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(nc::k_copy16, dim3(grid), dim3(256), 0, nc::stream_of(stream), (const uint4*)src, (uint4*)dst, n);
+    return nc::launch_status("k_copy16");
+}
