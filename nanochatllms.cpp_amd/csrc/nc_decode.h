@@ -13,8 +13,7 @@ namespace nc {
 //   PRO_RES_RMS h = Act(res_in[pos] + Act(raw_in [* bscale])) -- the
 //               residual add of the previous Linear's output -- stored to
 //               res_out[pos], then rms_norm(h) as PRO_RMS
-//   PRO_SWIGLU  Act(Act(silu(Act(g))) * Act(u)) of raw_in = [g | u]
-enum DmvPrologue { PRO_X = 0, PRO_RMS = 1, PRO_RES_RMS = 2, PRO_SWIGLU = 3 };
+enum DmvPrologue { PRO_X = 0, PRO_RMS = 1, PRO_RES_RMS = 2 };
 // Epilogue: EPI_RAW writes the fp32 dot products; EPI_ARGMAX also writes the
 // greedy token to tokens[pos + 1] (and *pos_out = pos + 1 when dpos is set);
 // EPI_SWIGLU takes fused gate|up weights [2f, K] and writes
@@ -31,7 +30,7 @@ struct DmvArgs {
     const int* dpos = nullptr;
     const uint8_t* x = nullptr;    // PRO_X: the row; PRO_RMS: [positions, K] Act rows
     int x_pitch = 0;
-    const float* raw_in = nullptr;      // PRO_RES_RMS: [K] fp32; PRO_SWIGLU: [2K] fp32
+    const float* raw_in = nullptr;      // PRO_RES_RMS: [K] fp32
     const uint8_t* res_in = nullptr;    // PRO_RES_RMS: [positions, K] Act rows
     uint8_t* res_out = nullptr;         // PRO_RES_RMS: [positions, K] Act rows (row pos written)
     int res_pitch = 0;
@@ -47,7 +46,9 @@ struct DmvArgs {
 
 constexpr int kDmvArgmaxWords = 320 + 4096;
 
-// Whether decode_matvec takes this weight dtype, shape and prologue.
+// Whether decode_matvec takes this weight dtype, shape, prologue and
+// epilogue (norm prologues need K % 256 == 0 and K <= 4096; the argmax and
+// SwiGLU epilogues come with a norm prologue).
 bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi);
 
 // One fused launch on `st`; with events, the dispatch records them at the

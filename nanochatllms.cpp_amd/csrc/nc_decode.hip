@@ -26,6 +26,7 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "nc_act.h"
 #include "nc_decode.h"
@@ -36,7 +37,7 @@ namespace nc {
 
 constexpr int kDmvThreads = 256;
 constexpr int kDmvMaxItems = 4;     // weight blocks per thread and row group
-constexpr int kDmvNormChunks = 2;   // PRO_RMS / PRO_RES_RMS: 8-value chunks per thread (K <= 4096)
+constexpr int kDmvNormChunks = 2;   // norm prologues: 8-value chunks per thread (NCH <= 2: K <= 4096)
 constexpr int kDmvMaxGrid = 4096;
 
 // Q8 round trip of 8 values of one block held by a lane quad:
@@ -113,7 +114,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx)
 // while the weights are in flight (LDS barriers do not wait for global
 // loads).  sq: K floats of LDS for the squares and the Act row.  Ends with
 // an LDS barrier.
-template <int PRO, class LoadW>
+template <int PRO, int NCH, class LoadW>
 __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t* xs, float* sq, SsShared& ssh,
                                              LoadW&& load_w)
 {
@@ -126,41 +127,13 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
         if (tid < nb) xr = load_x_block(A.x, nb, tid);
         load_w();
         if (tid < nb) stage_x_block(xr, xs + tid * 16);
-    } else if (PRO == PRO_SWIGLU) {
-        // m = Act(Act(silu(Act(g))) * Act(u)) chunk by chunk, into xq
-        float gv[8], uv[8];
-        int ch = tid;
-        const bool v0 = ch < nch;
-        load_f32_chunk(A.raw_in, v0 ? ch : 0, gv);
-        load_f32_chunk(A.raw_in + K, v0 ? ch : 0, uv);
-        load_w();
-        for (;;) {
-            const bool valid = ch < nch;
-            quad_roundtrip(gv);
-#pragma unroll
-            for (int i = 0; i < 8; i++) gv[i] = gv[i] / (1.0f + expf_ref(-gv[i]));
-            quad_roundtrip(gv);
-            quad_roundtrip(uv);
-            float mv[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) mv[i] = gv[i] * uv[i];
-            const Q8Chunk q = quad_quantize(mv);
-            if (valid) store_act_chunk(xq, K, ch, q);
-            ch += kDmvThreads;
-            if (ch - tid >= nch) break;  // uniform: the next round has no valid chunk
-            const int cc = ch < nch ? ch : 0;
-            load_f32_chunk(A.raw_in, cc, gv);
-            load_f32_chunk(A.raw_in + K, cc, uv);
-        }
-        lds_barrier();
-        if (tid < nb) stage_x_block(load_x_block(xq, nb, tid), xs + tid * 16);
     } else {
         // h: the stored row (PRO_RMS) or the residual sum (PRO_RES_RMS)
-        float h[kDmvNormChunks][8], gain[kDmvNormChunks][8];
-        float av[kDmvNormChunks][8], ov[kDmvNormChunks][8];
+        float h[NCH][8], gain[NCH][8];
+        float av[NCH][8], ov[NCH][8];
         const uint8_t* arow = (PRO == PRO_RMS ? A.x : A.res_in) + (size_t)pos * (PRO == PRO_RMS ? A.x_pitch : A.res_pitch);
 #pragma unroll
-        for (int j = 0; j < kDmvNormChunks; j++) {
+        for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
             const int cc = ch < nch ? ch : 0;
             load_act_chunk(arow, K, cc, av[j]);
@@ -172,7 +145,7 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
         }
         load_w();
 #pragma unroll
-        for (int j = 0; j < kDmvNormChunks; j++) {
+        for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
             const bool valid = ch < nch;
             if (j * kDmvThreads >= nch) break;  // uniform
@@ -207,7 +180,7 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
         const float denom = sqrtf(ss / (float)K) + 1e-6f;
         // the normalized row as stored (codes, then deltas) over sq's bytes
 #pragma unroll
-        for (int j = 0; j < kDmvNormChunks; j++) {
+        for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
             if (j * kDmvThreads >= nch) break;  // uniform
             float y[8];
@@ -227,7 +200,7 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
     lds_barrier();
 }
 
-template <int WT, int R, int PRO, int EPI>
+template <int WT, int R, int PRO, int EPI, int NCH>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
@@ -260,7 +233,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
         }
     };
     int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
-    dmv_prologue<PRO>(A, pos, xs, sq, ssh, [&] { load_group(g, wc, dc); });
+    dmv_prologue<PRO, NCH>(A, pos, xs, sq, ssh, [&] { load_group(g, wc, dc); });
 
     unsigned long long best = 0;  // EPI_ARGMAX: this workgroup's best key (thread 0)
     for (; g < A.ngroups; g += gridDim.x) {
@@ -376,78 +349,83 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
 // rows (f + 32b + r) -- all of their weights requested up front -- in two
 // halves through the fold, then m = Act(Act(silu(Act(g))) * Act(u)) for the
 // block (tinyllama/tinyllama.cpp:88-97).  No workgroup waits for another.
-constexpr int kGluMaxItems = 18;  // 64 rows x nb blocks / 256 threads, nb <= 72
+constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / 256 threads, NB <= 72
 
-template <int WT, int PRO>
+template <int WT, int PRO, int NCH, int NB>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
     constexpr int WV = WD / 4;
+    constexpr int TP = ((NB + 3) & ~3) + 4;
+    constexpr int IT = NB / 4;    // weight blocks per thread (64 rows)
+    constexpr int HALF = NB / 8;  // of them, the gate rows'
+    static_assert(NB % 8 == 0 && IT <= kGluMaxItems, "gate|up block shape");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
     __shared__ float s_out[64];
-    const int nb = A.nb;
-    const int tp = ((nb + 3) & ~3) + 4;
     uint32_t* xs = lds;
-    float* T = reinterpret_cast<float*>(xs + nb * 16);  // 32 rows x 4 lanes x tp
-    float* sq = T + 32 * 4 * tp;
+    float* T = reinterpret_cast<float*>(xs + NB * 16);  // 32 rows x 4 lanes x TP
+    float* sq = T + 32 * 4 * TP;
     const int tid = threadIdx.x;
     const int f = A.N / 2, nblk = f / 32;
-    const int its = nb / 4, half = nb / 8;  // items per thread, per half
     const int pos = A.dpos ? A.dpos[0] : A.pos;
 
-    uint4 w[kGluMaxItems][WV];
-    uint16_t dw[kGluMaxItems];
+    uint4 w[IT][WV];
+    uint16_t dw[IT];
     auto load_block = [&](int b) {
 #pragma unroll
-        for (int it = 0; it < kGluMaxItems; it++) {
-            if (it < its) {
-                const int j = tid + it * kDmvThreads;
-                const int r = j / nb, i = j - r * nb;
-                const int row = r < 32 ? 32 * b + r : f + 32 * b + (r - 32);
-                const size_t bi = (size_t)row * nb + i;
-                const uint4* src = reinterpret_cast<const uint4*>(A.wq + bi * WD);
+        for (int it = 0; it < IT; it++) {
+            const int j = tid + it * kDmvThreads;
+            const int r = j / NB, i = j - r * NB;
+            const int row = r < 32 ? 32 * b + r : f + 32 * b + (r - 32);
+            const size_t bi = (size_t)row * NB + i;
+            const uint4* src = reinterpret_cast<const uint4*>(A.wq + bi * WD);
 #pragma unroll
-                for (int v = 0; v < WV; v++) w[it][v] = src[v];
-                dw[it] = A.wd[bi];
-            }
+            for (int v = 0; v < WV; v++) w[it][v] = src[v];
+            dw[it] = A.wd[bi];
         }
     };
     int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks
-    dmv_prologue<PRO>(A, pos, xs, sq, ssh, [&] { load_block(b); });
+    DmvArgs P = A;
+    P.nb = NB;
+    dmv_prologue<PRO, NCH>(P, pos, xs, sq, ssh, [&] { load_block(b); });
 
-    for (; b < nblk; b += gridDim.x) {
-        if (b != (int)blockIdx.x) load_block(b);
-        for (int h = 0; h < 2; h++) {
+    // one half of the rows: terms of items [H*HALF, (H+1)*HALF), then the fold
+    auto half_pass = [&](auto hc) {
+        constexpr int H = decltype(hc)::value;
 #pragma unroll
-            for (int it = 0; it < kGluMaxItems; it++) {
-                if (it >= h * half && it < (h + 1) * half) {
-                    const int j = tid + it * kDmvThreads;
-                    const int r = j / nb, i = j - r * nb;
-                    float tv[4];
-                    q_block_terms<WT>(xs + i * 16, w[it], dw[it], tv);
-                    float* t = T + (r - 32 * h) * 4 * tp + i;
+        for (int it = H * HALF; it < (H + 1) * HALF; it++) {
+            const int j = tid + it * kDmvThreads;
+            const int r = j / NB, i = j - r * NB;
+            float tv[4];
+            q_block_terms<WT>(xs + i * 16, w[it], dw[it], tv);
+            float* t = T + (r - 32 * H) * 4 * TP + i;
 #pragma unroll
-                    for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
-                }
-            }
-            lds_barrier();
-            if (tid < 128) {
-                const float acc = seq_sum<16>(T + tid * tp, nb);
-                const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
-                if ((tid & 3) == 0) {
-                    s_out[32 * h + (tid >> 2)] = res;
-                    if (A.raw) A.raw[(h ? f : 0) + 32 * b + (tid >> 2)] = res;
-                }
-            }
-            lds_barrier();
+            for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
         }
+        lds_barrier();
+        if (tid < 128) {
+            const float acc = seq_sum<16>(T + tid * TP, NB);
+            const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
+            if ((tid & 3) == 0) {
+                s_out[32 * H + (tid >> 2)] = res;
+                if (A.raw) A.raw[(H ? f : 0) + 32 * b + (tid >> 2)] = res;
+            }
+        }
+        lds_barrier();
+    };
+    for (;;) {
+        half_pass(std::integral_constant<int, 0>{});
+        half_pass(std::integral_constant<int, 1>{});
         if (tid < 32) {
             const float gq = q8_roundtrip_lane(s_out[tid], true);
             const float gs = q8_roundtrip_lane(gq / (1.0f + expf_ref(-gq)), true);
             const float uq = q8_roundtrip_lane(s_out[32 + tid], true);
             act_store<Q8>(A.m_out, 32 * b + tid, f, gs * uq, true);
         }
+        b += gridDim.x;
+        if (b >= nblk) break;
+        load_block(b);
     }
 }
 
@@ -480,10 +458,10 @@ int dmv_rows(int nb, int N)
     return best;
 }
 
-template <int WT, int R, int PRO, int EPI>
+template <int WT, int R, int PRO, int EPI, int NCH>
 int dmv_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv<WT, R, PRO, EPI>;
+    auto kern = k_dmv<WT, R, PRO, EPI, NCH>;
     static int max_grid = 0;  // per instantiation: workgroups resident at once
     if (!max_grid) {
         int per_cu = 0;
@@ -500,10 +478,10 @@ int dmv_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
     return launch_status("k_dmv");
 }
 
-template <int WT, int PRO>
+template <int WT, int PRO, int NCH, int NB>
 int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv_glu<WT, PRO>;
+    auto kern = k_dmv_glu<WT, PRO, NCH, NB>;
     static int max_grid = 0;
     if (!max_grid) {
         int per_cu = 0;
@@ -519,14 +497,50 @@ int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
     return launch_status("k_dmv_glu");
 }
 
-template <int WT, int PRO, int EPI>
+template <int WT, int PRO, int EPI, int NCH>
 int dmv_r(const DmvArgs& A, size_t lds0, int R, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     const int tp = ((A.nb + 3) & ~3) + 4;
     const size_t lds = lds0 + (size_t)R * 4 * tp * 4;
-    if (R == 16) return dmv_go<WT, 16, PRO, EPI>(A, lds, st, ev0, ev1);
-    if (R == 8) return dmv_go<WT, 8, PRO, EPI>(A, lds, st, ev0, ev1);
-    return dmv_go<WT, 4, PRO, EPI>(A, lds, st, ev0, ev1);
+    if (R == 16) return dmv_go<WT, 16, PRO, EPI, NCH>(A, lds, st, ev0, ev1);
+    if (R == 8) return dmv_go<WT, 8, PRO, EPI, NCH>(A, lds, st, ev0, ev1);
+    return dmv_go<WT, 4, PRO, EPI, NCH>(A, lds, st, ev0, ev1);
+}
+
+template <int WT>
+int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    const int R = dmv_rows(A.nb, A.N);
+    const size_t K = (size_t)A.nb * 32;
+    const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
+    const bool two = K > (size_t)kDmvThreads * 8;  // norm prologue: two 8-value chunks per thread
+    // staged row (16 dwords per block), the fold terms, then the norm
+    // prologue's squares / Act row
+    const size_t lds0 = (size_t)A.nb * 64 + (norm ? K * 4 : 0);
+    if (epi == EPI_SWIGLU) {
+        const int tp = ((A.nb + 3) & ~3) + 4;
+        const size_t lds = lds0 + (size_t)32 * 4 * tp * 4;
+        // gate|up rows of 2048 (64 blocks) or 2304 (72 blocks) values
+        if (A.nb == 64) {
+            if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64>(A, lds, st, ev0, ev1);
+            return glu_go<WT, PRO_RES_RMS, 1, 64>(A, lds, st, ev0, ev1);
+        }
+        if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72>(A, lds, st, ev0, ev1);
+        return glu_go<WT, PRO_RES_RMS, 2, 72>(A, lds, st, ev0, ev1);
+    }
+    if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
+    if (epi == EPI_ARGMAX) {
+        if (pro == PRO_RMS)
+            return two ? dmv_r<WT, PRO_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
+                       : dmv_r<WT, PRO_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
+        return two ? dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
+                   : dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
+    }
+    if (pro == PRO_RMS)
+        return two ? dmv_r<WT, PRO_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
+                   : dmv_r<WT, PRO_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
+    return two ? dmv_r<WT, PRO_RES_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
+               : dmv_r<WT, PRO_RES_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
 }
 
 }  // namespace
@@ -534,12 +548,12 @@ int dmv_r(const DmvArgs& A, size_t lds0, int R, hipStream_t st, hipEvent_t ev0, 
 bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi)
 {
     if (wdtype != NC_Q4 && wdtype != NC_Q8) return false;
-    if (pro < PRO_X || pro > PRO_SWIGLU || epi < EPI_RAW || epi > EPI_SWIGLU) return false;
+    if (pro < PRO_X || pro > PRO_RES_RMS || epi < EPI_RAW || epi > EPI_SWIGLU) return false;
     if (K <= 0 || K % 32 || N <= 0 || !dmv_rows(K / 32, N)) return false;
     const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
     if (norm && (K % kSsThreads || K > kDmvThreads * 8 * kDmvNormChunks)) return false;
-    if (epi == EPI_SWIGLU && (N % 64 || (K / 32) % 8 || K / 32 > 4 * kGluMaxItems || pro == PRO_SWIGLU))
-        return false;
+    if (epi == EPI_ARGMAX && !norm) return false;
+    if (epi == EPI_SWIGLU && (N % 64 || (K != 2048 && K != 2304) || !norm)) return false;
     return true;
 }
 
@@ -548,38 +562,7 @@ int decode_matvec(const DmvArgs& A, int wdtype, int pro, int epi, hipStream_t st
     if (!decode_matvec_supported(wdtype, A.nb * 32, A.N, pro, epi))
         return fail(NC_ERR_ARG, "decode matvec: unsupported [%d x %d] dtype %d prologue %d epilogue %d", A.N,
                     A.nb * 32, wdtype, pro, epi);
-    const int R = dmv_rows(A.nb, A.N);
-    const size_t K = (size_t)A.nb * 32;
-    // staged row (16 dwords per block), then the fold terms, then the
-    // prologue's squares / Act row
-    const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
-    const size_t lds0 = (size_t)A.nb * 64 + (norm ? K * 4 : (pro == PRO_X ? 0 : K + (size_t)A.nb * 2 + 16));
-    if (epi == EPI_SWIGLU) {
-        const int tp = ((A.nb + 3) & ~3) + 4;
-        const size_t lds = lds0 + (size_t)32 * 4 * tp * 4;
-        if (wdtype == NC_Q4) {
-            if (pro == PRO_RMS) return glu_go<Q4, PRO_RMS>(A, lds, st, ev0, ev1);
-            if (pro == PRO_RES_RMS) return glu_go<Q4, PRO_RES_RMS>(A, lds, st, ev0, ev1);
-            return glu_go<Q4, PRO_X>(A, lds, st, ev0, ev1);
-        }
-        if (pro == PRO_RMS) return glu_go<Q8, PRO_RMS>(A, lds, st, ev0, ev1);
-        if (pro == PRO_RES_RMS) return glu_go<Q8, PRO_RES_RMS>(A, lds, st, ev0, ev1);
-        return glu_go<Q8, PRO_X>(A, lds, st, ev0, ev1);
-    }
-#define DMV_EPI(WTV, PROV)                                                             \
-    if (epi == EPI_RAW) return dmv_r<WTV, PROV, EPI_RAW>(A, lds0, R, st, ev0, ev1);    \
-    return dmv_r<WTV, PROV, EPI_ARGMAX>(A, lds0, R, st, ev0, ev1);
-#define DMV_PRO(WTV)                                      \
-    switch (pro) {                                        \
-    case PRO_X: { DMV_EPI(WTV, PRO_X) }                   \
-    case PRO_RMS: { DMV_EPI(WTV, PRO_RMS) }               \
-    case PRO_RES_RMS: { DMV_EPI(WTV, PRO_RES_RMS) }       \
-    default: { DMV_EPI(WTV, PRO_SWIGLU) }                 \
-    }
-    if (wdtype == NC_Q4) { DMV_PRO(Q4) }
-    DMV_PRO(Q8)
-#undef DMV_PRO
-#undef DMV_EPI
+    return wdtype == NC_Q4 ? dmv_dispatch<Q4>(A, pro, epi, st, ev0, ev1) : dmv_dispatch<Q8>(A, pro, epi, st, ev0, ev1);
 }
 
 }  // namespace nc

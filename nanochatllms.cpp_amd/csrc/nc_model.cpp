@@ -589,7 +589,6 @@ public:
         if (pro == PRO_X) b += row;
         if (pro == PRO_RMS) b += row + 2.0 * K;
         if (pro == PRO_RES_RMS) b += 2.0 * row + 4.0 * K + 2.0 * K;
-        if (pro == PRO_SWIGLU) b += 8.0 * K;
         return b;
     }
 
