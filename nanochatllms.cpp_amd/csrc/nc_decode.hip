@@ -126,7 +126,7 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
         XRaw xr{};
         if (tid < nb) xr = load_x_block(A.x, nb, tid);
         load_w();
-        if (tid < nb) stage_x_block(xr, xs + tid * 16);
+        if (tid < nb) stage_x_block(xr, xs + tid * kStage);
     } else {
         // h: the stored row (PRO_RMS) or the residual sum (PRO_RES_RMS)
         float h[NCH][8], gain[NCH][8];
@@ -195,7 +195,7 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
             if (ch < nch) store_act_chunk(xq, K, ch, q);
         }
         lds_barrier();
-        if (tid < nb) stage_x_block(load_x_block(xq, nb, tid), xs + tid * 16);
+        if (tid < nb) stage_x_block(load_x_block(xq, nb, tid), xs + tid * kStage);
     }
     lds_barrier();
 }
@@ -210,8 +210,8 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     __shared__ unsigned long long s_key[R];
     const int nb = A.nb;
     const int tp = ((nb + 3) & ~3) + 4;
-    uint32_t* xs = lds;                                 // staged row: nb * 16 dwords
-    float* T = reinterpret_cast<float*>(xs + nb * 16);  // fold terms: R * 4 * tp
+    uint32_t* xs = lds;                                     // staged row: nb * kStage dwords
+    float* T = reinterpret_cast<float*>(xs + nb * kStage);  // fold terms: R * 4 * tp
     float* sq = T + R * 4 * tp;                         // prologue scratch
     const int tid = threadIdx.x;
     const int nitems = R * nb;
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             if (j >= nitems) continue;
             const int r = j / nb, i = j - r * nb;
             float tv[4];
-            q_block_terms<WT>(xs + i * 16, wc[it], dc[it], tv);
+            q_block_terms<WT>(xs + i * kStage, wc[it], dc[it], tv);
             float* t = T + r * 4 * tp + i;
 #pragma unroll
             for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     __shared__ SsShared ssh;
     __shared__ float s_out[64];
     uint32_t* xs = lds;
-    float* T = reinterpret_cast<float*>(xs + NB * 16);  // 32 rows x 4 lanes x TP
+    float* T = reinterpret_cast<float*>(xs + NB * kStage);  // 32 rows x 4 lanes x TP
     float* sq = T + 32 * 4 * TP;
     const int tid = threadIdx.x;
     const int f = A.N / 2, nblk = f / 32;
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
             const int j = tid + it * kDmvThreads;
             const int r = j / NB, i = j - r * NB;
             float tv[4];
-            q_block_terms<WT>(xs + i * 16, w[it], dw[it], tv);
+            q_block_terms<WT>(xs + i * kStage, w[it], dw[it], tv);
             float* t = T + (r - 32 * H) * 4 * TP + i;
 #pragma unroll
             for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
@@ -514,9 +514,9 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
     const size_t K = (size_t)A.nb * 32;
     const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
     const bool two = K > (size_t)kDmvThreads * 8;  // norm prologue: two 8-value chunks per thread
-    // staged row (16 dwords per block), the fold terms, then the norm
+    // staged row (kStage dwords per block), the fold terms, then the norm
     // prologue's squares / Act row
-    const size_t lds0 = (size_t)A.nb * 64 + (norm ? K * 4 : 0);
+    const size_t lds0 = (size_t)A.nb * kStage * 4 + (norm ? K * 4 : 0);
     if (epi == EPI_SWIGLU) {
         const int tp = ((A.nb + 3) & ~3) + 4;
         const size_t lds = lds0 + (size_t)32 * 4 * tp * 4;

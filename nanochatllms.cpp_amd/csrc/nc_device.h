@@ -105,12 +105,16 @@ __device__ __forceinline__ float quad_max(float v)
     return fmaxf(v, dpp_f<kDppQuadXor2>(v));
 }
 
-// Reduction of a value across the 32 lanes of a half-wave (xor butterfly).
+// Maximum of a non-negative value across the 32 lanes of a half-wave:
+// quad_perm (xor 1, xor 2), row_half_mirror and row_mirror DPP moves pair
+// ever larger groups inside a 16-lane row, then a ds_swizzle exchanges the
+// two rows (xor 16).  Lanes of the half-wave that are inactive read as 0.
 __device__ __forceinline__ float half_wave_max(float v)
 {
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
-    return v;
+    v = quad_max(v);
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror: lane i <-> 7 - i
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror: lane i <-> 15 - i
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
 }
 
 // q8_quantize_block (gten/quants.cpp:16-30) for one 32-value block held one

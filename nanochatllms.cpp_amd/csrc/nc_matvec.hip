@@ -46,7 +46,7 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restri
     extern __shared__ __align__(16) uint32_t lds[];
     uint32_t* xs = lds;
     const int tp = ((nb + 3) & ~3) + 4;
-    float* T = reinterpret_cast<float*>(lds + nb * 16);
+    float* T = reinterpret_cast<float*>(lds + nb * kStage);
     const int tid = threadIdx.x;
     const int row0 = blockIdx.x * R;
     const int nitems = R * nb;
@@ -74,13 +74,13 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restri
     }
     for (int p = 0; p < n_xrows; p++) {
         const uint8_t* xr = x + (size_t)p * x_pitch;
-        if (tid < nb) stage_x_block(p == 0 ? x0 : load_x_block(xr, nb, tid), xs + tid * 16);
+        if (tid < nb) stage_x_block(p == 0 ? x0 : load_x_block(xr, nb, tid), xs + tid * kStage);
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < kMvMaxItems; it++) {
             if (tix[it] < 0) continue;
             float tv[4];
-            q_block_terms<WT>(xs + bix[it] * 16, w[it], dw16[it], tv);
+            q_block_terms<WT>(xs + bix[it] * kStage, w[it], dw16[it], tv);
             float* t = T + tix[it];
 #pragma unroll
             for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
@@ -165,7 +165,7 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
         constexpr int R = 4;
         if (R * nb > kMvThreads * kMvMaxItems) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);
         const int tp = ((nb + 3) & ~3) + 4;
-        const size_t lds = (size_t)nb * 64 + (size_t)R * 4 * tp * 4;
+        const size_t lds = (size_t)nb * kStage * 4 + (size_t)R * 4 * tp * 4;
         const dim3 grid((N + R - 1) / R);
         if (w->dtype == NC_Q4)
             NC_MV_LAUNCH((k_matvec_q<Q4, R>), grid, lds, x, x_pitch, n_rows, (const uint32_t*)w->data,

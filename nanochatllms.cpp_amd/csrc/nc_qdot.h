@@ -10,6 +10,11 @@
 
 namespace nc {
 
+// Dwords between staged blocks in LDS: 16 used, padded to 20 so that the
+// 16-byte reads of consecutive blocks by consecutive lanes fall in distinct
+// banks (a 64-byte stride would put every fourth lane on the same banks).
+constexpr int kStage = 20;
+
 __device__ __forceinline__ uint32_t pick_pair(uint32_t lo, uint32_t hi, int odd)
 {
     // bytes (2*odd, 2*odd+1) of lo followed by the same bytes of hi
