@@ -52,6 +52,24 @@ __device__ __forceinline__ float act_roundtrip(float v, bool valid)
     return v;
 }
 
+// (x_j, x_{j+d/2}) -> (x_j cos - x_{j+d/2} sin, x_j sin + x_{j+d/2} cos) on
+// the first d_r dims of a 64-wide head held one value per lane.
+__device__ __forceinline__ float rope_lane(float x, int lane, int d_half, const float2* cs)
+{
+    const int d_r = 2 * d_half;
+    const int partner = lane < d_half ? lane + d_half : (lane < d_r ? lane - d_half : lane);
+    const float xp = __shfl(x, partner);
+    if (lane < d_half) {
+        const float2 t = cs[lane];
+        return x * t.x - xp * t.y;
+    }
+    if (lane < d_r) {
+        const float2 t = cs[lane - d_half];
+        return xp * t.y + x * t.x;
+    }
+    return x;
+}
+
 // Code of element e (0..31) in a lane-permuted weight block (see
 // nc_layout.h): dword index and byte position of the element.
 __device__ __forceinline__ int wblock_byte_pos(int e) { return (e & 1) + (((e & 15) >> 3) << 1); }

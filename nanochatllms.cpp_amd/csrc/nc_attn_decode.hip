@@ -1,0 +1,313 @@
+// nc_attn_decode.hip -- single-row decode attention with the q/k/v post-
+// processing fused in (Q8 activations).
+//
+// One workgroup per query head h (group g = h / (hq / hkv)) does what
+// k_qkv_post + k_attn do for the decode row, with the same arithmetic:
+//   q_h, k_g, v_g from the fused qkv matvec output: requantized as Linear
+//     outputs; OpenELM's per-head QK RMSNorm (requantized); RoPE of q and k
+//     (requantized when stored) -- gten/modules.cpp:242-267, openelm.cpp:33-60;
+//   the group's first head appends k_g and v_g to the caches at the position
+//     (the others read that position from shared memory, so no workgroup
+//     waits for another);
+//   scores, softmax (max, expf, sequential sum, divide, requantize per 32
+//     positions) and P.V as qkv_attn (gten/ops.cpp:1017-1220): the Q8 dot's
+//     four lane sums per block, P.V as eight fp32 lanes (position mod 8)
+//     summed left to right, then the n mod 8 tail.
+// The K and V rows of the earlier positions are requested first, into
+// registers, so their latency overlaps the q/k/v work.
+#include <type_traits>
+
+#include "nc_act.h"
+#include "nc_kernels.h"
+
+namespace nc {
+
+// f(0), f(1), ..., f(N - 1) with compile-time indices (register arrays stay
+// in registers even where a plain loop would not be unrolled).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+constexpr int kAdThreads = 256;
+constexpr int kAdMaxK = 3;   // K rows per thread held in registers (positions < 768)
+constexpr int kAdMaxV = 10;  // 16-byte V loads per thread held in registers (positions < 640)
+constexpr int kAdVB = 80;    // LDS bytes per staged V position: 64 codes, 2 fp16 deltas, pad
+
+__device__ __forceinline__ uint32_t ad_pick(uint32_t lo, uint32_t hi, int odd)
+{
+    return odd ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
+}
+
+// The Q8 dot of two 64-value heads as vec_dot_product_q8 (gten/ops.cpp:
+// 292-384) computes it: per 32-block four int32 lane sums, fp32 terms
+// folded block by block, (a0 + a1) + (a2 + a3).  Codes as 4 uint4 per head.
+__device__ __forceinline__ float head_dot_q8(const uint4 (&a)[4], const float (&da)[2], const uint4 (&b)[4],
+                                             const float (&db)[2])
+{
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int blk = 0; blk < 2; blk++) {
+        const uint32_t A[8] = {a[2 * blk].x, a[2 * blk].y, a[2 * blk].z, a[2 * blk].w,
+                               a[2 * blk + 1].x, a[2 * blk + 1].y, a[2 * blk + 1].z, a[2 * blk + 1].w};
+        const uint32_t B[8] = {b[2 * blk].x, b[2 * blk].y, b[2 * blk].z, b[2 * blk].w,
+                               b[2 * blk + 1].x, b[2 * blk + 1].y, b[2 * blk + 1].z, b[2 * blk + 1].w};
+        const float dd = da[blk] * db[blk];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            // elements {2k, 2k+1, 2k+8, 2k+9} and the same + 16: lane k of the AVX dot
+            const uint32_t xa = ad_pick(A[k >> 1], A[2 + (k >> 1)], k & 1);
+            const uint32_t xb = ad_pick(A[4 + (k >> 1)], A[6 + (k >> 1)], k & 1);
+            const uint32_t ya = ad_pick(B[k >> 1], B[2 + (k >> 1)], k & 1);
+            const uint32_t yb = ad_pick(B[4 + (k >> 1)], B[6 + (k >> 1)], k & 1);
+            int L = __builtin_amdgcn_sdot4((int)xa, (int)ya, 0, false);
+            L = __builtin_amdgcn_sdot4((int)xb, (int)yb, L, false);
+            acc[k] = acc[k] + (float)L * dd;
+        }
+    }
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+// Wavefront maximum: DPP within 16-lane rows, then the four row results.
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, dpp_f<kDppQuadXor1, 0xf, false>(v, v));
+    v = fmaxf(v, dpp_f<kDppQuadXor2, 0xf, false>(v, v));
+    v = fmaxf(v, dpp_f<0x141, 0xf, false>(v, v));
+    v = fmaxf(v, dpp_f<0x140, 0xf, false>(v, v));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+template <bool QKNORM>
+__global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict__ raw, int hq, int hkv,
+                                                         const uint16_t* __restrict__ qn_w,
+                                                         const uint16_t* __restrict__ kn_w,
+                                                         const float2* __restrict__ table, int d_half, int pos_host,
+                                                         const int* __restrict__ dpos, uint8_t* __restrict__ kc,
+                                                         uint8_t* __restrict__ vc, int kv_pitch,
+                                                         uint8_t* __restrict__ out, float scale)
+{
+    extern __shared__ __align__(16) float sm[];
+    __shared__ __align__(16) uint8_t s_q[kAdVB], s_k[kAdVB];
+    __shared__ __align__(16) float s_nrm[2][64];
+    __shared__ float red[8];
+    const int pos = dpos ? dpos[0] : pos_host;
+    const int n = pos + 1;
+    const int npad = (n + 3) & ~3;
+    float* S = sm;                                           // scores / probabilities [npad]
+    float* acc = S + npad;                                   // [8 lanes][64 columns]
+    uint8_t* Vs = reinterpret_cast<uint8_t*>(acc + 512);    // [n][kAdVB]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int h = blockIdx.x;
+    const int gs = hq / hkv, g = h / gs;
+    const int kvd = act_delta_offset(hkv * 64);
+    const uint8_t* kslice = kc + g * 64;
+    const uint8_t* vslice = vc + g * 64;
+
+    // ---- K rows (positions < pos) into registers, V slices too
+    uint4 kr[kAdMaxK][4];
+    uint32_t kd[kAdMaxK];
+    static_for<0, kAdMaxK>([&](auto I) {
+        const int c = tid + I * kAdThreads;
+        const int cc = c < pos ? c : 0;
+        const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)cc * kv_pitch);
+#pragma unroll
+        for (int v = 0; v < 4; v++) kr[I][v] = p[v];
+        kd[I] = reinterpret_cast<const uint32_t*>(kc + (size_t)cc * kv_pitch + kvd)[g];
+    });
+    const int vtotal = pos * 4;  // 16-byte parts of the earlier positions' V slices
+    uint32_t vr[kAdMaxV][4];  // plain words: an array of the uint4 union type stays in scratch memory
+    uint32_t vd[kAdMaxV];
+    static_for<0, kAdMaxV>([&](auto I) {
+        const int idx = tid + I * kAdThreads;
+        const int c = idx < vtotal ? idx >> 2 : 0, part = idx & 3;
+        const uint4 t4 = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[part];
+        vr[I][0] = t4.x;
+        vr[I][1] = t4.y;
+        vr[I][2] = t4.z;
+        vr[I][3] = t4.w;
+        vd[I] = reinterpret_cast<const uint32_t*>(vc + (size_t)c * kv_pitch + kvd)[g];
+    });
+
+    // ---- q_h (wave 0), k_g (wave 1), v_g (wave 2) of the new position
+    if (w < 3) {
+        const int col = w == 0 ? h * 64 : (w == 1 ? hq * 64 + g * 64 : hq * 64 + hkv * 64 + g * 64);
+        float x = q8_roundtrip_lane(raw[col + lane], true);  // the Linear output as stored
+        if (w < 2) {
+            if (QKNORM) {
+                // RMSNorm3D over the head (rms_norm_vec_f32, gten/ops.cpp:830-903)
+                float* buf = s_nrm[w];
+                buf[lane] = x * x;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+                const float rms = sqrtf(seq_sum(buf, 64) / 64.0f);
+                x = q8_roundtrip_lane(x / (rms + 1e-6f) * h2f((w == 0 ? qn_w : kn_w)[lane]), true);
+            }
+            x = rope_lane(x, lane, d_half, table + (size_t)pos * d_half);
+        }
+        uint16_t d16;
+        const int8_t code = q8_quant_lane(x, true, &d16);
+        uint8_t* st = w == 0 ? s_q : (w == 1 ? s_k : Vs + (size_t)pos * kAdVB);
+        st[lane] = (uint8_t)code;
+        if ((lane & 31) == 0) reinterpret_cast<uint16_t*>(st + 64)[lane >> 5] = d16;
+        if (w > 0 && h % gs == 0) {
+            // the group's first head appends the new K / V row to the cache
+            uint8_t* row = (w == 1 ? kc : vc) + (size_t)pos * kv_pitch;
+            row[g * 64 + lane] = (uint8_t)code;
+            if ((lane & 31) == 0) reinterpret_cast<uint16_t*>(row + kvd)[g * 2 + (lane >> 5)] = d16;
+        }
+    }
+    lds_barrier();
+
+    // ---- scores of positions c <= pos (thread = position)
+    {
+        uint4 qv[4];
+        float dq[2];
+#pragma unroll
+        for (int v = 0; v < 4; v++) qv[v] = reinterpret_cast<const uint4*>(s_q)[v];
+        dq[0] = h2f(reinterpret_cast<const uint16_t*>(s_q + 64)[0]);
+        dq[1] = h2f(reinterpret_cast<const uint16_t*>(s_q + 64)[1]);
+        static_for<0, kAdMaxK>([&](auto I) {
+            const int c = tid + I * kAdThreads;
+            if (c < pos) {
+                const float dk[2] = {h2f((uint16_t)(kd[I] & 0xFFFFu)), h2f((uint16_t)(kd[I] >> 16))};
+                S[c] = head_dot_q8(qv, dq, kr[I], dk) * scale;
+            }
+        });
+        for (int c = tid + kAdMaxK * kAdThreads; c < pos; c += kAdThreads) {
+            uint4 kk[4];
+            const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)c * kv_pitch);
+#pragma unroll
+            for (int v = 0; v < 4; v++) kk[v] = p[v];
+            const uint32_t kdd = reinterpret_cast<const uint32_t*>(kc + (size_t)c * kv_pitch + kvd)[g];
+            const float dk[2] = {h2f((uint16_t)(kdd & 0xFFFFu)), h2f((uint16_t)(kdd >> 16))};
+            S[c] = head_dot_q8(qv, dq, kk, dk) * scale;
+        }
+        if (tid == (pos & (kAdThreads - 1))) {
+            uint4 kk[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) kk[v] = reinterpret_cast<const uint4*>(s_k)[v];
+            const float dk[2] = {h2f(reinterpret_cast<const uint16_t*>(s_k + 64)[0]),
+                                 h2f(reinterpret_cast<const uint16_t*>(s_k + 64)[1])};
+            S[pos] = head_dot_q8(qv, dq, kk, dk) * scale;
+        }
+    }
+    // V slices of the earlier positions into shared memory
+    static_for<0, kAdMaxV>([&](auto I) {
+        const int idx = tid + I * kAdThreads;
+        if (idx < vtotal) {
+            const int c = idx >> 2, part = idx & 3;
+            reinterpret_cast<uint4*>(Vs + (size_t)c * kAdVB)[part] = make_uint4(vr[I][0], vr[I][1], vr[I][2], vr[I][3]);
+            if (part == 0) reinterpret_cast<uint32_t*>(Vs + (size_t)c * kAdVB + 64)[0] = vd[I];
+        }
+    });
+    for (int idx = tid + kAdMaxV * kAdThreads; idx < vtotal; idx += kAdThreads) {
+        const int c = idx >> 2, part = idx & 3;
+        reinterpret_cast<uint4*>(Vs + (size_t)c * kAdVB)[part] =
+                reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[part];
+        if (part == 0)
+            reinterpret_cast<uint32_t*>(Vs + (size_t)c * kAdVB + 64)[0] =
+                    reinterpret_cast<const uint32_t*>(vc + (size_t)c * kv_pitch + kvd)[g];
+    }
+    lds_barrier();
+
+    // ---- softmax: max (order-free), expf, sequential sum, divide, requantize
+    float mx = -INFINITY;
+    for (int c = tid; c < n; c += kAdThreads) mx = fmaxf(mx, S[c]);
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    lds_barrier();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int c = tid; c < n; c += kAdThreads) S[c] = expf_ref(S[c] - mx);
+    lds_barrier();
+    if (w == 0) {
+        const float sum = seq_sum(S, n);
+        if (lane == 0) red[4] = sum;
+    }
+    lds_barrier();
+    const float sum = red[4];
+    for (int c0 = 0; c0 < n; c0 += kAdThreads) {
+        const int c = c0 + tid;
+        const bool valid = c < n;
+        const float p = valid ? S[c] / sum : 0.0f;
+        const float pr = q8_roundtrip_lane(p, valid);  // P stored as Act: 32-position blocks
+        if (valid) S[c] = pr;
+    }
+    lds_barrier();
+
+    // ---- P.V: thread = (column j, lanes l and l + 4), both chains in step
+    {
+        const int j = lane, l = w;
+        const int n8 = n & ~7;
+        auto vval = [&](int c) -> float {
+            const uint8_t* vrow = Vs + (size_t)c * kAdVB;
+            return (float)reinterpret_cast<const int8_t*>(vrow)[j] * h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[j >> 5]);
+        };
+        float a0 = 0.0f, a1 = 0.0f;
+        int c = 0;
+        for (; c + 32 <= n8; c += 32) {
+            // four positions of each chain: loads first, then the adds in order
+            float p0[4], v0[4], p1[4], v1[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                p0[u] = S[c + 8 * u + l];
+                v0[u] = vval(c + 8 * u + l);
+                p1[u] = S[c + 8 * u + l + 4];
+                v1[u] = vval(c + 8 * u + l + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                a0 = p0[u] * v0[u] + a0;
+                a1 = p1[u] * v1[u] + a1;
+            }
+        }
+        for (; c < n8; c += 8) {
+            a0 = S[c + l] * vval(c + l) + a0;
+            a1 = S[c + l + 4] * vval(c + l + 4) + a1;
+        }
+        acc[l * 64 + j] = a0;
+        acc[(l + 4) * 64 + j] = a1;
+    }
+    lds_barrier();
+    if (w == 0) {
+        const int j = lane;
+        float s = acc[j];
+#pragma unroll
+        for (int l = 1; l < 8; l++) s = s + acc[l * 64 + j];
+        for (int c = n & ~7; c < n; c++) {
+            const uint8_t* vrow = Vs + (size_t)c * kAdVB;
+            s = s + S[c] * ((float)reinterpret_cast<const int8_t*>(vrow)[j] *
+                            h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[j >> 5]));
+        }
+        act_store<Q8>(out, h * 64 + j, act_delta_offset(hq * 64), s, true);
+    }
+}
+
+int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
+                       const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st)
+{
+    if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "attention: %d query heads over %d kv heads", hq, hkv);
+    if (max_ctx > kAdMaxK * kAdThreads) return fail(NC_ERR_ARG, "attention: context %d too long", max_ctx);
+    const size_t lds = ((size_t)((max_ctx + 3) & ~3) + 512) * 4 + (size_t)max_ctx * kAdVB;
+    if (lds > 60 * 1024) return fail(NC_ERR_ARG, "attention: context %d too long", max_ctx);
+    const float scale = 1.0f / sqrtf(64.0f);
+    if (qn_w)
+        hipLaunchKernelGGL(k_attn_dec<true>, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w,
+                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale);
+    else
+        hipLaunchKernelGGL(k_attn_dec<false>, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w,
+                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale);
+    return launch_status("k_attn_dec");
+}
+
+}  // namespace nc

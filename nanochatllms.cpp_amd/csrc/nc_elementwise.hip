@@ -126,24 +126,6 @@ __global__ __launch_bounds__(1024) void k_norm(const uint8_t* __restrict__ a, in
 
 // ------------------------------------------------------------------- rope --
 
-// (x_j, x_{j+d/2}) -> (x_j cos - x_{j+d/2} sin, x_j sin + x_{j+d/2} cos) on
-// the first d_r dims of a 64-wide head held one value per lane.
-__device__ __forceinline__ float rope_lane(float x, int lane, int d_half, const float2* cs)
-{
-    const int d_r = 2 * d_half;
-    const int partner = lane < d_half ? lane + d_half : (lane < d_r ? lane - d_half : lane);
-    const float xp = __shfl(x, partner);
-    if (lane < d_half) {
-        const float2 t = cs[lane];
-        return x * t.x - xp * t.y;
-    }
-    if (lane < d_r) {
-        const float2 t = cs[lane - d_half];
-        return xp * t.y + x * t.x;
-    }
-    return x;
-}
-
 // rotary_emb (gten/ops.cpp:775-821) on stored activation rows: one
 // wavefront per 64-wide head; row r has position start + blockIdx.y.
 template <int ADT>

@@ -61,4 +61,12 @@ int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k
                 uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st,
                 const int* dpos = nullptr, int max_ctx = 0);
 
+// Decode attention with the q/k/v post-processing fused in (Q8 activations,
+// no qkv bias): raw = the qkv matvec's fp32 row [q | k | v]; the new k / v
+// rows are appended to the caches at the position (*dpos when set, else
+// pos); out = the attention output Act row.
+int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
+                       const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st);
+
 }  // namespace nc

@@ -650,12 +650,18 @@ public:
                 a.res_out = L[l - 1].res2;
                 if ((s = dmv(a, &y.qkv, PRO_RES_RMS, EPI_RAW, NC_PROF_QKV))) return s;
             }
-            if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, pos, 1,
-                                     q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
-                return s;
-            if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, pos, pos + 1, st, dpos,
-                                 cfg.max_ctx)))
-                return s;
+            if (!y.bq) {
+                if ((s = attn_decode_launch(qkv_raw, y.hq, y.hkv, y.qn, y.kn, rope, d_half, pos, dpos, y.kc, y.vc, pkv,
+                                            attn, cfg.max_ctx, st)))
+                    return s;
+            } else {
+                if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half,
+                                         pos, 1, q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
+                    return s;
+                if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, pos, pos + 1, st,
+                                     dpos, cfg.max_ctx)))
+                    return s;
+            }
             a = base;
             a.x = attn;
             a.raw = o_raw;
