@@ -280,23 +280,36 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
         int ok = mm < kSsMaxCross;
         // within binade E consecutive grid values have consecutive bit
         // patterns (E = 1 spans the subnormals too), so s + u C is bits + C
-        // and the parity of s / u is the last bit; the final record's term
-        // is +0, which leaves s as it is.  The chain state is kept in vector
-        // registers (the empty asm marks it lane-varying): scalar registers
-        // would cost a vector-to-scalar move per record.
+        // and the parity of s / u is the last bit; records past the last are
+        // the identity with a +0 term, which leaves s as it is.  Lane r
+        // holds record r; the chain reads them with readlane, in vector
+        // registers (the empty asm marks the state lane-varying, so it does
+        // not bounce through scalar registers).
         int sb = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs));
         if (ok) {
-            asm volatile("" : "+v"(sb), "+v"(ok));
-#pragma unroll 4
-            for (int r = 0; r <= mm; r++) {
-                const int4 R = sh.rec[r];  // same address on every lane: an LDS broadcast
-                const int E = R.z;
-                const int nb = sb + ((sb & 1) ? R.y : R.x);  // 0 units for a segment of zeros
-                const bool good = E == 0 || (E < 255 && ss_binade(__builtin_bit_cast(float, sb)) == E &&
-                                             ss_binade(__builtin_bit_cast(float, nb)) == E);
-                ok &= good ? 1 : 0;
-                sb = __builtin_bit_cast(int, __builtin_bit_cast(float, nb) + __builtin_bit_cast(float, R.w));
+            const int4 R = lane <= mm ? sh.rec[lane] : make_int4(0, 0, 0, 0);
+            int okl = R.z == 0 || R.z < 255;
+            asm volatile("" : "+v"(sb));
+            int sbl = 0, nbl = 0;  // the chain's value entering / leaving record `lane` (for the checks)
+            for (int r0 = 0; r0 <= mm; r0 += 4) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    // past the last record: lane 63, which holds the identity
+                    // (mm < kSsMaxCross = 63); readlane indices stay below 64
+                    const int r = min(r0 + k, kWave - 1);
+                    const int C0 = __builtin_amdgcn_readlane(R.x, r), C1 = __builtin_amdgcn_readlane(R.y, r);
+                    const float tr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(R.w, r));
+                    const int nb = sb + ((sb & 1) ? C1 : C0);
+                    sbl = lane == r ? sb : sbl;
+                    nbl = lane == r ? nb : nbl;
+                    sb = __builtin_bit_cast(int, __builtin_bit_cast(float, nb) + tr);
+                }
             }
+            // record `lane`'s segment must start and end inside its binade
+            if (lane <= mm && R.z != 0)
+                okl = okl && ss_binade(__builtin_bit_cast(float, sbl)) == R.z &&
+                      ss_binade(__builtin_bit_cast(float, nbl)) == R.z;
+            ok = __builtin_amdgcn_ballot_w64(!okl) == 0;
         }
         if (lane == 0) {
             sh.result = __builtin_bit_cast(float, sb);
