@@ -99,15 +99,19 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     __shared__ __align__(16) uint8_t s_q[kAdVB], s_k[kAdVB];
     __shared__ __align__(16) float s_nrm[2][64];
     __shared__ float red[8];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int h = blockIdx.x;
+    const int gs = hq / hkv, g = h / gs;
+    // this wave's raw q / k / v value does not depend on the position: it is
+    // requested before the position is known
+    const int col = w == 0 ? h * 64 : (w == 1 ? hq * 64 + g * 64 : hq * 64 + hkv * 64 + g * 64);
+    const float raw_x = w < 3 ? raw[col + lane] : 0.0f;
     const int pos = dpos ? dpos[0] : pos_host;
     const int n = pos + 1;
     const int npad = (n + 3) & ~3;
     float* S = sm;                                           // scores / probabilities [npad]
     float* acc = S + npad;                                   // [8 lanes][64 columns]
     uint8_t* Vs = reinterpret_cast<uint8_t*>(acc + 512);    // [n][kAdVB]
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int h = blockIdx.x;
-    const int gs = hq / hkv, g = h / gs;
     const int kvd = act_delta_offset(hkv * 64);
     const uint8_t* kslice = kc + g * 64;
     const uint8_t* vslice = vc + g * 64;
@@ -139,8 +143,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
 
     // ---- q_h (wave 0), k_g (wave 1), v_g (wave 2) of the new position
     if (w < 3) {
-        const int col = w == 0 ? h * 64 : (w == 1 ? hq * 64 + g * 64 : hq * 64 + hkv * 64 + g * 64);
-        float x = q8_roundtrip_lane(raw[col + lane], true);  // the Linear output as stored
+        float x = q8_roundtrip_lane(raw_x, true);  // the Linear output as stored
         if (w < 2) {
             if (QKNORM) {
                 // RMSNorm3D over the head (rms_norm_vec_f32, gten/ops.cpp:830-903)
@@ -254,18 +257,18 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         };
         float a0 = 0.0f, a1 = 0.0f;
         int c = 0;
-        for (; c + 32 <= n8; c += 32) {
-            // four positions of each chain: loads first, then the adds in order
-            float p0[4], v0[4], p1[4], v1[4];
+        for (; c + 64 <= n8; c += 64) {
+            // eight positions of each chain: loads first, then the adds in order
+            float p0[8], v0[8], p1[8], v1[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 8; u++) {
                 p0[u] = S[c + 8 * u + l];
                 v0[u] = vval(c + 8 * u + l);
                 p1[u] = S[c + 8 * u + l + 4];
                 v1[u] = vval(c + 8 * u + l + 4);
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 8; u++) {
                 a0 = p0[u] * v0[u] + a0;
                 a1 = p1[u] * v1[u] + a1;
             }
