@@ -144,6 +144,93 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_f16(const uint8_t* __rest
     }
 }
 
+// F16, one activation row (decode): a 64-thread workgroup owns 8 rows, thread
+// (row, lane j) folds lane j's chain over the 64-column groups in order
+// exactly as k_matvec_f16 does, but keeps two batches of kF16Batch weight
+// runs in flight (the next batch is requested before the current one is
+// folded), so the fold is not serialised behind one load per group.
+constexpr int kF16Batch = 8;
+
+__global__ __launch_bounds__(64) void k_matvec_f16_row(const uint8_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                      float* __restrict__ out, int N, int K)
+{
+    extern __shared__ __align__(16) float xsf[];  // [K/64][8 lanes][8]
+    const int tid = threadIdx.x;
+    const int j = tid & 7;
+    const int row = blockIdx.x * 8 + (tid >> 3);
+    const int G = K / 64;
+    const int npad = (N + 7) & ~7;
+    const int rowc = row < N ? row : N - 1;  // rows past N read a valid row and store nothing
+    const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;  // group 0
+    const size_t gstride = (size_t)npad * 8;                                         // uint4s per group
+    // two weight batches in flight, used in turn: batch A holds groups
+    // [g0, g0 + B), batch B the next B groups; each is refilled right after
+    // it is folded (no register copies, which would wait for the loads)
+    uint4 wa[kF16Batch], wb[kF16Batch];
+    auto load = [&](uint4(&dst)[kF16Batch], int gbase) {
+#pragma unroll
+        for (int b = 0; b < kF16Batch; b++) {
+            const int g = gbase + b;
+            dst[b] = wrow[(size_t)(g < G ? g : 0) * gstride];
+        }
+    };
+    // the activation row first (8 halves per load, K <= 8192), then the
+    // weights, so staging the row waits for the row only
+    constexpr int kXMax = 8192 / 8 / 64;
+    uint4 xv8[kXMax];
+#pragma unroll
+    for (int i = 0; i < kXMax; i++) {
+        const int c = tid + i * 64;  // 8-value chunk
+        xv8[i] = c * 8 < K ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0, 0, 0, 0);
+    }
+    load(wa, 0);
+    load(wb, kF16Batch);
+#pragma unroll
+    for (int i = 0; i < kXMax; i++) {
+        const int c = tid + i * 64;
+        if (c * 8 < K) {
+            const uint32_t q[4] = {xv8[i].x, xv8[i].y, xv8[i].z, xv8[i].w};
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int e = c * 8 + t;
+                const int g = e >> 6, m = (e >> 3) & 7, jj = e & 7;
+                xsf[(g * 8 + jj) * 8 + m] = h2f((uint16_t)(t & 1 ? q[t >> 1] >> 16 : q[t >> 1] & 0xFFFFu));
+            }
+        }
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    auto fold = [&](const uint4(&wv4)[kF16Batch], int gbase) {
+#pragma unroll
+        for (int b = 0; b < kF16Batch; b++) {
+            const int g = gbase + b;
+            if (g < G) {
+                const float4 xa = *reinterpret_cast<const float4*>(xsf + (g * 8 + j) * 8);
+                const float4 xb = *reinterpret_cast<const float4*>(xsf + (g * 8 + j) * 8 + 4);
+                const uint32_t wv[4] = {wv4[b].x, wv4[b].y, wv4[b].z, wv4[b].w};
+                const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                for (int m = 0; m < 8; m++) {
+                    const uint16_t h = (uint16_t)(m & 1 ? wv[m >> 1] >> 16 : wv[m >> 1] & 0xFFFFu);
+                    acc = xv[m] * h2f(h) + acc;
+                }
+            }
+        }
+    };
+    for (int g0 = 0; g0 < G; g0 += 2 * kF16Batch) {
+        fold(wa, g0);
+        if (g0 + 2 * kF16Batch < G) load(wa, g0 + 2 * kF16Batch);
+        fold(wb, g0 + kF16Batch);
+        if (g0 + 3 * kF16Batch < G) load(wb, g0 + 3 * kF16Batch);
+    }
+    // lanes 0..7 of the row summed left to right
+    const int base = tid & ~7;
+    float s = __shfl(acc, base);
+#pragma unroll
+    for (int l = 1; l < 8; l++) s = s + __shfl(acc, base + l);
+    if (j == 0 && row < N) out[row] = s;
+}
+
 // out[r, c] = dot(x[r], w[c]) for x rows [0, n_rows) (pointers already at
 // the first row), fp32 out with `out_pitch` floats per row.
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
@@ -180,6 +267,15 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
         if (K % 64) return fail(NC_ERR_ARG, "matmul: F16 path needs K %% 64 == 0, K=%d", K);
         const size_t lds = (size_t)K * 4;
         if (lds > 64 * 1024) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);
+        if (n_rows == 1 && K <= 8192) {
+            if (ev_start)
+                hipExtLaunchKernelGGL(k_matvec_f16_row, dim3((N + 7) / 8), dim3(64), lds, st, ev_start, ev_stop, 0, x,
+                                      (const uint16_t*)w->data, out, N, K);
+            else
+                hipLaunchKernelGGL(k_matvec_f16_row, dim3((N + 7) / 8), dim3(64), lds, st, x, (const uint16_t*)w->data,
+                                   out, N, K);
+            return launch_status("k_matvec_f16_row");
+        }
         const dim3 grid((N + 31) / 32);
         NC_MV_LAUNCH(k_matvec_f16, grid, lds, x, x_pitch, n_rows, (const uint16_t*)w->data, out, out_pitch, N, K);
         return launch_status("k_matvec_f16");
