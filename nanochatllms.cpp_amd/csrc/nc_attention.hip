@@ -136,7 +136,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const uint8_t* __restrict
 #pragma unroll
                 for (int m = 0; m < 8; m++)
 #pragma unroll
-                    for (int j = 0; j < 8; j++) a8[j] = qv[8 * m + j] * h2f(kh[8 * m + j]) + a8[j];
+                    for (int j = 0; j < 8; j++) a8[j] = __builtin_fmaf(qv[8 * m + j], h2f(kh[8 * m + j]), a8[j]);
                 s = a8[0] + a8[1] + a8[2] + a8[3] + a8[4] + a8[5] + a8[6] + a8[7];
                 s = s * scale;
             }

@@ -25,7 +25,7 @@ struct DmvArgs {
     const uint32_t* wq = nullptr;  // weight codes, lane-permuted blocks
     const uint16_t* wd = nullptr;  // weight deltas
     int N = 0, nb = 0;             // weight rows, 32-value blocks per row (K = 32 nb)
-    int ngroups = 0;               // set by the launcher
+    int rows = 0, ngroups = 0;     // rows per group and groups: set by the launcher
     int pos = 0;                   // the row's position, or *dpos when dpos is set
     const int* dpos = nullptr;
     const uint8_t* x = nullptr;    // PRO_X: the row; PRO_RMS: [positions, K] Act rows

@@ -36,7 +36,7 @@
 namespace nc {
 
 constexpr int kDmvThreads = 256;
-constexpr int kDmvMaxItems = 4;     // weight blocks per thread and row group
+constexpr int kDmvMaxItems = 12;    // weight blocks per thread and row group
 constexpr int kDmvNormChunks = 2;   // norm prologues: 8-value chunks per thread (NCH <= 2: K <= 4096)
 constexpr int kDmvMaxGrid = 4096;
 
@@ -125,7 +125,11 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
     if (PRO == PRO_X) {
         XRaw xr{};
         if (tid < nb) xr = load_x_block(A.x, nb, tid);
+        // scheduling fences keep the row's loads first and every weight
+        // load issued before anything waits on the row
+        __builtin_amdgcn_sched_barrier(0);
         load_w();
+        __builtin_amdgcn_sched_barrier(0);
         if (tid < nb) stage_x_block(xr, xs + tid * kStage);
     } else {
         // h: the stored row (PRO_RMS) or the residual sum (PRO_RES_RMS)
@@ -143,7 +147,9 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
 #pragma unroll
             for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
         }
+        __builtin_amdgcn_sched_barrier(0);
         load_w();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
@@ -200,15 +206,15 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
     lds_barrier();
 }
 
-template <int WT, int R, int PRO, int EPI, int NCH>
+template <int WT, int IT, int PRO, int EPI, int NCH>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
     constexpr int WV = WD / 4;
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
-    __shared__ unsigned long long s_key[R];
-    const int nb = A.nb;
+    __shared__ unsigned long long s_key[4];
+    const int nb = A.nb, R = A.rows;
     const int tp = ((nb + 3) & ~3) + 4;
     uint32_t* xs = lds;                                     // staged row: nb * kStage dwords
     float* T = reinterpret_cast<float*>(xs + nb * kStage);  // fold terms: R * 4 * tp
@@ -217,32 +223,36 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     const int nitems = R * nb;
     const int pos = A.dpos ? A.dpos[0] : A.pos;
 
-    uint4 wc[kDmvMaxItems][WV];
-    uint16_t dc[kDmvMaxItems];
-    auto load_group = [&](int g, uint4(&w)[kDmvMaxItems][WV], uint16_t(&dw)[kDmvMaxItems]) {
+    // IT: weight blocks per thread (R rows x nb blocks <= IT x 256)
+    uint4 wc[IT][WV];
+    uint16_t dc[IT];
+    auto load_group = [&](int g, uint4(&w)[IT][WV], uint16_t(&dw)[IT]) {
 #pragma unroll
-        for (int it = 0; it < kDmvMaxItems; it++) {
+        for (int it = 0; it < IT; it++) {
+            // every slot loads (items past the group and rows past N: block
+            // 0), so the waits for these loads are exact counts
             const int j = tid + it * kDmvThreads;
             const int r = j / nb, i = j - r * nb;
-            const bool ok = j < nitems && g * R + r < A.N;
-            const size_t b = ok ? (size_t)(g * R + r) * nb + i : 0;
+            const size_t b = j < nitems && g * R + r < A.N ? (size_t)(g * R + r) * nb + i : 0;
             const uint4* src = reinterpret_cast<const uint4*>(A.wq + b * WD);
 #pragma unroll
             for (int v = 0; v < WV; v++) w[it][v] = src[v];
             dw[it] = A.wd[b];
         }
     };
+    const int G = gridDim.x;
     int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
     dmv_prologue<PRO, NCH>(A, pos, xs, sq, ssh, [&] { load_group(g, wc, dc); });
 
-    unsigned long long best = 0;  // EPI_ARGMAX: this workgroup's best key (thread 0)
-    for (; g < A.ngroups; g += gridDim.x) {
-        const int gn = g + gridDim.x;
-        uint4 wn[kDmvMaxItems][WV];
-        uint16_t dn[kDmvMaxItems];
+    // EPI_ARGMAX: each row's lane-0 thread keeps the best key of its rows
+    unsigned long long best = 0;
+    for (; g < A.ngroups; g += G) {
+        const int gn = g + G;
+        uint4 wn[IT][WV];
+        uint16_t dn[IT];
         if (gn < A.ngroups) load_group(gn, wn, dn);
 #pragma unroll
-        for (int it = 0; it < kDmvMaxItems; it++) {
+        for (int it = 0; it < IT; it++) {
             const int j = tid + it * kDmvThreads;
             if (j >= nitems) continue;
             const int r = j / nb, i = j - r * nb;
@@ -253,10 +263,9 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
         }
         lds_barrier();
-        if (tid < kWave) {
+        if (tid < 4 * R) {
             // thread 4r + k folds lane k of row r in block order
-            float acc = 0.0f;
-            if (tid < 4 * R) acc = seq_sum<16>(T + tid * tp, nb);
+            const float acc = seq_sum<16>(T + tid * tp, nb);
             // lanes 4r..4r+3 hold row r's four lane sums; lane 4r reads
             // the other three with quad_perm [1,0,3,2], [2,3,0,1], [3,2,1,0]
             const float a1 = dpp_f<kDppQuadXor1>(acc);
@@ -264,16 +273,17 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             const float a3 = dpp_f<0x1B>(acc);
             const float res = (acc + a1) + (a2 + a3);
             const int row = g * R + (tid >> 2);
-            const bool mine = tid < 4 * R && (tid & 3) == 0 && row < A.N;
-            if (mine) A.raw[row] = res;
-            if (EPI == EPI_ARGMAX && (tid & 3) == 0 && tid < 4 * R)
-                s_key[tid >> 2] = mine ? argmax_key(res, row) : 0ull;
+            if ((tid & 3) == 0 && row < A.N) {
+                A.raw[row] = res;
+                if (EPI == EPI_ARGMAX) {
+                    const unsigned long long key = argmax_key(res, row);
+                    best = key > best ? key : best;
+                }
+            }
         }
         lds_barrier();
-        if (EPI == EPI_ARGMAX && tid == 0)
-            for (int r = 0; r < R; r++) best = s_key[r] > best ? s_key[r] : best;
 #pragma unroll
-        for (int it = 0; it < kDmvMaxItems; it++) {
+        for (int it = 0; it < IT; it++) {
 #pragma unroll
             for (int v = 0; v < WV; v++) wc[it][v] = wn[it][v];
             dc[it] = dn[it];
@@ -292,7 +302,19 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
         unsigned long long* sub = A.amax + 64;
         unsigned long long* cnt = A.amax + 192;
         unsigned long long* slot = A.amax + 320;
-        const int G = gridDim.x, grp = blockIdx.x >> 5;
+        const int fold_waves = (4 * R + kWave - 1) / kWave;
+        if (tid < fold_waves * kWave) {
+#pragma unroll
+            for (int o = 4; o < kWave; o <<= 1) {
+                const unsigned long long other = __shfl_xor(best, o);
+                best = other > best ? other : best;
+            }
+            if ((tid & (kWave - 1)) == 0) s_key[tid / kWave] = best;
+        }
+        lds_barrier();
+        if (tid == 0)
+            for (int w = 1; w < fold_waves; w++) best = s_key[w] > best ? s_key[w] : best;
+        const int grp = blockIdx.x >> 5;
         const int ngrp = (G + 31) >> 5;
         if (tid < kWave) {
             unsigned long long done = 0;
@@ -445,23 +467,39 @@ int device_cus()
     return cus;
 }
 
-// Rows per group: the most rows whose blocks fit kDmvMaxItems per thread,
-// but no fewer than two groups per CU while a smaller group allows it.
-int dmv_rows(int nb, int N)
+constexpr int kDmvDirectItems = 4;  // streaming launches: weight blocks per thread and group, at most
+
+// Row groups of a launch.  Norm prologues, where every workgroup computes
+// the row's sum of squares (chains of dependent steps that workgroups
+// sharing a CU slow down for each other), spread N over the CUs in one pass
+// when they can: one group per workgroup, one workgroup per CU, the fewest
+// rows per group that do it within kDmvMaxItems blocks per thread.  Every
+// other launch streams: the most rows that fit kDmvDirectItems blocks per
+// thread while there are at least two groups per CU, as many workgroups as
+// the GPU holds at once.
+struct DmvShape {
+    int rows;
+    bool spread;
+};
+
+DmvShape dmv_shape(int nb, int N, bool norm)
 {
+    if (norm)
+        for (int r : {4, 8, 16, 32})
+            if (r * nb <= kDmvThreads * kDmvMaxItems && (N + r - 1) / r <= device_cus()) return {r, true};
     int best = 0;
     for (int r : {4, 8, 16}) {
-        if (r * nb > kDmvThreads * kDmvMaxItems) break;
+        if (r * nb > kDmvThreads * kDmvDirectItems) break;
         if (best && (N + r - 1) / r < 2 * device_cus()) break;
         best = r;
     }
-    return best;
+    return {best, false};
 }
 
-template <int WT, int R, int PRO, int EPI, int NCH>
-int dmv_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+template <int WT, int IT, int PRO, int EPI, int NCH>
+int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv<WT, R, PRO, EPI, NCH>;
+    auto kern = k_dmv<WT, IT, PRO, EPI, NCH>;
     static int max_grid = 0;  // per instantiation: workgroups resident at once
     if (!max_grid) {
         int per_cu = 0;
@@ -469,8 +507,9 @@ int dmv_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
         if (e != hipSuccess) return hip_fail(e, "decode matvec: occupancy");
         max_grid = std::min(kDmvMaxGrid, std::max(1, per_cu) * device_cus());
     }
-    A.ngroups = (A.N + R - 1) / R;
-    const dim3 grid(std::min(A.ngroups, max_grid));
+    A.ngroups = (A.N + A.rows - 1) / A.rows;
+    // spread: ngroups <= CUs, one workgroup each
+    const dim3 grid(spread ? A.ngroups : std::min(A.ngroups, max_grid));
     if (ev0)
         hipExtLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, ev0, ev1, 0, A);
     else
@@ -497,22 +536,27 @@ int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
     return launch_status("k_dmv_glu");
 }
 
+// Launch with the items per thread the group needs (1, 2, 4, 8 or 12).
 template <int WT, int PRO, int EPI, int NCH>
-int dmv_r(const DmvArgs& A, size_t lds0, int R, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+int dmv_r(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     const int tp = ((A.nb + 3) & ~3) + 4;
-    const size_t lds = lds0 + (size_t)R * 4 * tp * 4;
-    if (R == 16) return dmv_go<WT, 16, PRO, EPI, NCH>(A, lds, st, ev0, ev1);
-    if (R == 8) return dmv_go<WT, 8, PRO, EPI, NCH>(A, lds, st, ev0, ev1);
-    return dmv_go<WT, 4, PRO, EPI, NCH>(A, lds, st, ev0, ev1);
+    const size_t lds = lds0 + (size_t)sh.rows * 4 * tp * 4;
+    A.rows = sh.rows;
+    const int items = (sh.rows * A.nb + kDmvThreads - 1) / kDmvThreads;
+    if (items <= 1) return dmv_go<WT, 1, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 2) return dmv_go<WT, 2, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 4) return dmv_go<WT, 4, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 8) return dmv_go<WT, 8, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    return dmv_go<WT, 12, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
 }
 
 template <int WT>
 int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    const int R = dmv_rows(A.nb, A.N);
     const size_t K = (size_t)A.nb * 32;
     const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
+    const DmvShape R = dmv_shape(A.nb, A.N, norm);
     const bool two = K > (size_t)kDmvThreads * 8;  // norm prologue: two 8-value chunks per thread
     // staged row (kStage dwords per block), the fold terms, then the norm
     // prologue's squares / Act row
@@ -549,8 +593,8 @@ bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi)
 {
     if (wdtype != NC_Q4 && wdtype != NC_Q8) return false;
     if (pro < PRO_X || pro > PRO_RES_RMS || epi < EPI_RAW || epi > EPI_SWIGLU) return false;
-    if (K <= 0 || K % 32 || N <= 0 || !dmv_rows(K / 32, N)) return false;
     const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
+    if (K <= 0 || K % 32 || N <= 0 || !dmv_shape(K / 32, N, norm).rows) return false;
     if (norm && (K % kSsThreads || K > kDmvThreads * 8 * kDmvNormChunks)) return false;
     if (epi == EPI_ARGMAX && !norm) return false;
     if (epi == EPI_SWIGLU && (N % 64 || (K != 2048 && K != 2304) || !norm)) return false;

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_f16(const uint8_t* __rest
 #pragma unroll
                 for (int m = 0; m < 8; m++) {
                     const uint16_t h = (uint16_t)(m & 1 ? wv[m >> 1] >> 16 : wv[m >> 1] & 0xFFFFu);
-                    acc = xv[m] * h2f(h) + acc;
+                    acc = __builtin_fmaf(xv[m], h2f(h), acc);  // exact product: same as mul then add
                 }
             }
         }
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_f16(const uint8_t* __rest
 // exactly as k_matvec_f16 does, but keeps two batches of kF16Batch weight
 // runs in flight (the next batch is requested before the current one is
 // folded), so the fold is not serialised behind one load per group.
-constexpr int kF16Batch = 8;
+constexpr int kF16Batch = 16;
 
 __global__ __launch_bounds__(64) void k_matvec_f16_row(const uint8_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                       float* __restrict__ out, int N, int K)
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(64) void k_matvec_f16_row(const uint8_t* __restrict
 #pragma unroll
                 for (int m = 0; m < 8; m++) {
                     const uint16_t h = (uint16_t)(m & 1 ? wv[m >> 1] >> 16 : wv[m >> 1] & 0xFFFFu);
-                    acc = xv[m] * h2f(h) + acc;
+                    acc = __builtin_fmaf(xv[m], h2f(h), acc);  // exact product: same as mul then add
                 }
             }
         }
