@@ -93,7 +93,8 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
                                                          const float2* __restrict__ table, int d_half, int pos_host,
                                                          const int* __restrict__ dpos, uint8_t* __restrict__ kc,
                                                          uint8_t* __restrict__ vc, int kv_pitch,
-                                                         uint8_t* __restrict__ out, float scale)
+                                                         uint8_t* __restrict__ out, float scale,
+                                                         const float2* __restrict__ rope_cur, int kv_rows)
 {
     extern __shared__ __align__(16) float sm[];
     __shared__ __align__(16) uint8_t s_q[kAdVB], s_k[kAdVB];
@@ -106,11 +107,12 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     // requested before the position is known
     const int col = w == 0 ? h * 64 : (w == 1 ? hq * 64 + g * 64 : hq * 64 + hkv * 64 + g * 64);
     const float raw_x = w < 3 ? raw[col + lane] : 0.0f;
-    const int pos = dpos ? dpos[0] : pos_host;
+    const int pos = dpos ? load_pos(dpos) : pos_host;
     const int n = pos + 1;
-    const int npad = (n + 3) & ~3;
-    float* S = sm;                                           // scores / probabilities [npad]
-    float* acc = S + npad;                                   // [8 lanes][64 columns]
+    // the shared-memory layout is sized by the cache rows, not by the position
+    const int spad = (kv_rows + 3) & ~3;
+    float* S = sm;                                           // scores / probabilities [spad]
+    float* acc = S + spad;                                   // [8 lanes][64 columns]
     uint8_t* Vs = reinterpret_cast<uint8_t*>(acc + 512);    // [n][kAdVB]
     const int kvd = act_delta_offset(hkv * 64);
     const uint8_t* kslice = kc + g * 64;
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
                 const float rms = sqrtf(seq_sum(buf, 64) / 64.0f);
                 x = q8_roundtrip_lane(x / (rms + 1e-6f) * h2f((w == 0 ? qn_w : kn_w)[lane]), true);
             }
-            x = rope_lane(x, lane, d_half, table + (size_t)pos * d_half);
+            x = rope_lane(x, lane, d_half, rope_cur ? rope_cur : table + (size_t)pos * d_half);
         }
         uint16_t d16;
         const int8_t code = q8_quant_lane(x, true, &d16);
@@ -297,7 +299,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
 
 int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
                        const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st)
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur)
 {
     if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "attention: %d query heads over %d kv heads", hq, hkv);
     if (max_ctx > kAdMaxK * kAdThreads) return fail(NC_ERR_ARG, "attention: context %d too long", max_ctx);
@@ -306,10 +308,12 @@ int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, 
     const float scale = 1.0f / sqrtf(64.0f);
     if (qn_w)
         hipLaunchKernelGGL(k_attn_dec<true>, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w,
-                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale);
+                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale,
+                           (const float2*)rope_cur, max_ctx);
     else
         hipLaunchKernelGGL(k_attn_dec<false>, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w,
-                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale);
+                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale,
+                           (const float2*)rope_cur, max_ctx);
     return launch_status("k_attn_dec");
 }
 

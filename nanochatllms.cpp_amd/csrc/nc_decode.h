@@ -13,6 +13,9 @@ namespace nc {
 //   PRO_RES_RMS h = Act(res_in[pos] + Act(raw_in [* bscale])) -- the
 //               residual add of the previous Linear's output -- stored to
 //               res_out[pos], then rms_norm(h) as PRO_RMS
+// PRO_RMS with x_pitch = 0 reads the row at x itself, and PRO_RES_RMS with
+// res_cur set reads the residual row there: rows at a fixed address, so the
+// first loads do not wait for the position.
 enum DmvPrologue { PRO_X = 0, PRO_RMS = 1, PRO_RES_RMS = 2 };
 // Epilogue: EPI_RAW writes the fp32 dot products; EPI_ARGMAX also writes the
 // greedy token to tokens[pos + 1] (and *pos_out = pos + 1 when dpos is set);
@@ -34,6 +37,8 @@ struct DmvArgs {
     const uint8_t* res_in = nullptr;    // PRO_RES_RMS: [positions, K] Act rows
     uint8_t* res_out = nullptr;         // PRO_RES_RMS: [positions, K] Act rows (row pos written)
     int res_pitch = 0;
+    const uint8_t* res_cur = nullptr;   // PRO_RES_RMS: the residual input row (else res_in at pos)
+    uint8_t* res_cur_out = nullptr;     // PRO_RES_RMS: the residual sum also stored here (a fixed row)
     float bscale = 1.0f;                // PRO_RES_RMS: scale of the branch output (1: none)
     const uint16_t* norm_w = nullptr;   // PRO_RMS / PRO_RES_RMS gain (fp16)
     float post_scale = 1.0f;            // scale of the normalized row (1: none)
@@ -42,6 +47,21 @@ struct DmvArgs {
     int32_t* tokens = nullptr;          // EPI_ARGMAX
     int* pos_out = nullptr;
     unsigned long long* amax = nullptr;  // EPI_ARGMAX scratch (kDmvArgmaxWords zeroed words, left zeroed)
+    // EPI_ARGMAX: the next step's inputs, prepared by the workgroup that
+    // finds the greedy token (when emb_codes is set): the token's embedding
+    // row (token_embed, then * emb_scale as MiniCPM) to emb_cur and, when
+    // pos + 1 < max_ctx, to row pos + 1 of emb_rows; RoPE row pos + 1 of
+    // rope_table to rope_cur.
+    const uint32_t* emb_codes = nullptr;
+    const uint16_t* emb_deltas = nullptr;
+    float emb_scale = 1.0f;
+    uint8_t* emb_cur = nullptr;
+    uint8_t* emb_rows = nullptr;
+    int emb_pitch = 0;
+    int max_ctx = 0;
+    const float* rope_table = nullptr;  // [max_ctx][rope_half] (cos, sin) pairs
+    float* rope_cur = nullptr;
+    int rope_half = 0;
 };
 
 constexpr int kDmvArgmaxWords = 320 + 4096;

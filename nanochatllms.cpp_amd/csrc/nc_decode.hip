@@ -115,8 +115,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx)
 // loads).  sq: K floats of LDS for the squares and the Act row.  Ends with
 // an LDS barrier.
 template <int PRO, int NCH, class LoadW>
-__device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t* xs, float* sq, SsShared& ssh,
-                                             LoadW&& load_w)
+__device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, LoadW&& load_w)
 {
     const int tid = threadIdx.x;
     const int nb = A.nb, K = nb * 32;
@@ -131,11 +130,24 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
         load_w();
         __builtin_amdgcn_sched_barrier(0);
         if (tid < nb) stage_x_block(xr, xs + tid * kStage);
+        lds_barrier();
+        return A.pos;  // not used after a PRO_X prologue
     } else {
         // h: the stored row (PRO_RMS) or the residual sum (PRO_RES_RMS)
         float h[NCH][8], gain[NCH][8];
         float av[NCH][8], ov[NCH][8];
-        const uint8_t* arow = (PRO == PRO_RMS ? A.x : A.res_in) + (size_t)pos * (PRO == PRO_RMS ? A.x_pitch : A.res_pitch);
+        // A row at a fixed address (x_pitch = 0, res_cur) is requested
+        // before the position: the position is then loaded after the row
+        // and before the weights, so waiting for it does not wait for them.
+        const bool fixed = PRO == PRO_RMS ? A.x_pitch == 0 : A.res_cur != nullptr;
+        int pos = A.pos;
+        const uint8_t* arow;
+        if (fixed) {
+            arow = PRO == PRO_RMS ? A.x : A.res_cur;
+        } else {
+            if (A.dpos) pos = load_pos(A.dpos);
+            arow = PRO == PRO_RMS ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
+        }
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
@@ -148,8 +160,12 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
             for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
         }
         __builtin_amdgcn_sched_barrier(0);
+        int posv = 0;
+        if (fixed && A.dpos) posv = load_pos(A.dpos);
+        __builtin_amdgcn_sched_barrier(0);
         load_w();
         __builtin_amdgcn_sched_barrier(0);
+        if (fixed && A.dpos) pos = posv;
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
@@ -166,7 +182,10 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
 #pragma unroll
                 for (int i = 0; i < 8; i++) s[i] = av[j][i] + ov[j][i];
                 const Q8Chunk q = quad_quantize(s);
-                if (valid && blockIdx.x == 0) store_act_chunk(A.res_out + (size_t)pos * A.res_pitch, K, ch, q);
+                if (valid && blockIdx.x == 0) {
+                    store_act_chunk(A.res_out + (size_t)pos * A.res_pitch, K, ch, q);
+                    if (A.res_cur_out) store_act_chunk(A.res_cur_out, K, ch, q);
+                }
                 const float d = h2f(q.d16);
 #pragma unroll
                 for (int i = 0; i < 8; i++) h[j][i] = (float)q.q[i] * d;
@@ -202,8 +221,83 @@ __device__ __forceinline__ void dmv_prologue(const DmvArgs& A, int pos, uint32_t
         }
         lds_barrier();
         if (tid < nb) stage_x_block(load_x_block(xq, nb, tid), xs + tid * kStage);
+        lds_barrier();
+        return pos;
     }
-    lds_barrier();
+}
+
+// The next step's inputs from the greedy token `tok` at position pos + 1:
+// token_embed (gten/ops.cpp:526-576: a Q8 row copied, a Q4 row dequantized
+// and requantized; MiniCPM then scales it, minicpm.cpp:57-58) into the
+// fixed row emb_cur (and row pos + 1 of emb_rows), and the RoPE row of
+// position pos + 1.  Called by all threads of one workgroup; a lane quad
+// holds one 32-value block, 8 values per lane.
+template <int WT, int NCH>
+__device__ __forceinline__ void next_step_inputs(const DmvArgs& A, int tok, int pos)
+{
+    constexpr int WD = WT == Q4 ? 4 : 8;
+    const int tid = threadIdx.x;
+    const int nb = A.nb, K = nb * 32, nch = K / 8;
+    const bool row_ok = pos + 1 < A.max_ctx;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        if (j * kDmvThreads >= nch) break;  // uniform
+        const int ch = tid + j * kDmvThreads;
+        const int cc = ch < nch ? ch : 0;
+        const size_t blk = (size_t)tok * nb + (cc >> 2);
+        const uint32_t* bw = A.emb_codes + blk * WD;
+        uint32_t w[WD];
+#pragma unroll
+        for (int v = 0; v < WD / 4; v++) {
+            const uint4 t4 = reinterpret_cast<const uint4*>(bw)[v];
+            w[4 * v] = t4.x;
+            w[4 * v + 1] = t4.y;
+            w[4 * v + 2] = t4.z;
+            w[4 * v + 3] = t4.w;
+        }
+        const uint16_t d16 = A.emb_deltas[blk];
+        const float dw = h2f(d16);
+        // element e = 8 (cc & 3) + i of the lane-permuted block: dword
+        // (i & 7) >> 1 (Q8: its upper half for e >= 16), byte (i & 1) +
+        // 2 (cc & 1); Q4: high nibble for e < 16
+        const int hi = (cc >> 1) & 1, sh8 = 16 * (cc & 1);
+        int code[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int k = (i & 7) >> 1;
+            const int shift = sh8 + 8 * (i & 1);
+            if (WT == Q8) {
+                const uint32_t dword = hi ? w[2 * k + 1] : w[2 * k];
+                code[i] = (int)(int8_t)((dword >> shift) & 0xFFu);
+            } else {
+                const uint32_t byte = (w[k] >> shift) & 0xFFu;
+                code[i] = (hi ? (int)(byte & 0x0Fu) : (int)(byte >> 4)) - 7;
+            }
+        }
+        Q8Chunk q;
+        if (WT == Q8 && A.emb_scale == 1.0f) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) q.q[i] = (int8_t)code[i];
+            q.d16 = d16;
+        } else {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = (float)code[i] * dw;
+            if (A.emb_scale != 1.0f) {
+                quad_roundtrip(v);
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = v[i] * A.emb_scale;
+            }
+            q = quad_quantize(v);
+        }
+        if (ch < nch) {
+            store_act_chunk(A.emb_cur, K, ch, q);
+            if (row_ok) store_act_chunk(A.emb_rows + (size_t)(pos + 1) * A.emb_pitch, K, ch, q);
+        }
+    }
+    if (row_ok && tid < A.rope_half)
+        reinterpret_cast<float2*>(A.rope_cur)[tid] =
+                reinterpret_cast<const float2*>(A.rope_table)[(size_t)(pos + 1) * A.rope_half + tid];
 }
 
 template <int WT, int IT, int PRO, int EPI, int NCH>
@@ -214,6 +308,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
     __shared__ unsigned long long s_key[4];
+    __shared__ int s_tok;
     const int nb = A.nb, R = A.rows;
     const int tp = ((nb + 3) & ~3) + 4;
     uint32_t* xs = lds;                                     // staged row: nb * kStage dwords
@@ -221,7 +316,6 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     float* sq = T + R * 4 * tp;                         // prologue scratch
     const int tid = threadIdx.x;
     const int nitems = R * nb;
-    const int pos = A.dpos ? A.dpos[0] : A.pos;
 
     // IT: weight blocks per thread (R rows x nb blocks <= IT x 256)
     uint4 wc[IT][WV];
@@ -242,7 +336,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     };
     const int G = gridDim.x;
     int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
-    dmv_prologue<PRO, NCH>(A, pos, xs, sq, ssh, [&] { load_group(g, wc, dc); });
+    const int pos = dmv_prologue<PRO, NCH>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
 
     // EPI_ARGMAX: each row's lane-0 thread keeps the best key of its rows
     unsigned long long best = 0;
@@ -311,6 +405,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             }
             if ((tid & (kWave - 1)) == 0) s_key[tid / kWave] = best;
         }
+        if (tid == 0) s_tok = -1;
         lds_barrier();
         if (tid == 0)
             for (int w = 1; w < fold_waves; w++) best = s_key[w] > best ? s_key[w] : best;
@@ -356,12 +451,20 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
                         b2 = other > b2 ? other : b2;
                     }
                     if (tid == 0) {
-                        A.tokens[pos + 1] = (int32_t)(0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull));
+                        const int tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull));
+                        A.tokens[pos + 1] = tok;
                         if (A.dpos) A.pos_out[0] = pos + 1;
                         __hip_atomic_store(top, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        s_tok = tok;
                     }
                 }
             }
+        }
+        if (A.emb_codes) {
+            // the workgroup that found the token prepares the next step
+            lds_barrier();
+            const int tok = s_tok;
+            if (tok >= 0) next_step_inputs<WT, NCH>(A, tok, pos);
         }
     }
 }
@@ -390,7 +493,6 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     float* sq = T + 32 * 4 * TP;
     const int tid = threadIdx.x;
     const int f = A.N / 2, nblk = f / 32;
-    const int pos = A.dpos ? A.dpos[0] : A.pos;
 
     uint4 w[IT][WV];
     uint16_t dw[IT];
@@ -410,7 +512,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks
     DmvArgs P = A;
     P.nb = NB;
-    dmv_prologue<PRO, NCH>(P, pos, xs, sq, ssh, [&] { load_block(b); });
+    dmv_prologue<PRO, NCH>(P, xs, sq, ssh, [&] { load_block(b); });
 
     // one half of the rows: terms of items [H*HALF, (H+1)*HALF), then the fold
     auto half_pass = [&](auto hc) {

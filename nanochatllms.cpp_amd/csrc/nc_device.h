@@ -69,6 +69,16 @@ NC_HD float expf_ref(float x)
     return (float)y;
 }
 
+// The device-held decode position, read with a vector load.  A scalar load
+// would be waited for together with the kernel-argument loads (scalar loads
+// complete out of order, so every wait on them is a wait for all), holding
+// back every later load; a vector load is waited for only where the
+// position is used.
+__device__ __forceinline__ int load_pos(const int* dpos)
+{
+    return __hip_atomic_load(dpos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
 // accesses, not for its global loads (which may stay in flight across it).
 __device__ __forceinline__ void lds_barrier()

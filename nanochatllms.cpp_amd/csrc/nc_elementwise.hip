@@ -238,7 +238,8 @@ __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ raw,
 template <int WDT, int ADT>
 __global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ codes, const uint16_t* __restrict__ deltas,
                                                int vocab, const int32_t* __restrict__ tokens, uint8_t* __restrict__ out,
-                                               int out_pitch, int d, float post_scale, const int* __restrict__ dpos)
+                                               int out_pitch, int d, float post_scale, const int* __restrict__ dpos,
+                                               uint8_t* __restrict__ out_cur)
 {
     const int e = blockIdx.x * 256 + threadIdx.x;
     const int r = dpos ? dpos[0] : (int)blockIdx.y;  // row of tokens / out
@@ -259,6 +260,10 @@ __global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ code
                 if (valid) {
                     reinterpret_cast<int8_t*>(orow)[e] = (int8_t)q;
                     if ((e & 31) == 0) reinterpret_cast<uint16_t*>(orow + dofs)[e >> 5] = deltas[blk];
+                    if (out_cur) {
+                        reinterpret_cast<int8_t*>(out_cur)[e] = (int8_t)q;
+                        if ((e & 31) == 0) reinterpret_cast<uint16_t*>(out_cur + dofs)[e >> 5] = deltas[blk];
+                    }
                 }
                 return;
             }
@@ -272,6 +277,7 @@ __global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ code
     }
     if (post_scale != 1.0f) v = act_roundtrip<ADT>(v, valid) * post_scale;
     act_store<ADT>(orow, e, dofs, v, valid);
+    if (out_cur) act_store<ADT>(out_cur, e, dofs, v, valid);
 }
 
 // ----------------------------------------------------------------- argmax --
@@ -433,7 +439,7 @@ int silu_mul_launch(int adt, const float* raw, int raw_pitch, int f, uint8_t* ou
 }
 
 int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, int out_pitch, int adt, int rows,
-                 float post_scale, hipStream_t st, const int* dpos)
+                 float post_scale, hipStream_t st, const int* dpos, uint8_t* out_cur)
 {
     if (rows <= 0) return NC_OK;
     const int d = table->cols;
@@ -442,13 +448,13 @@ int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, in
     const uint16_t* dl = (const uint16_t*)table->deltas;
     if (table->dtype == NC_Q4 && adt == NC_Q8)
         hipLaunchKernelGGL((k_embed<Q4, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale,
-                           dpos);
+                           dpos, out_cur);
     else if (table->dtype == NC_Q8 && adt == NC_Q8)
         hipLaunchKernelGGL((k_embed<Q8, Q8>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale,
-                           dpos);
+                           dpos, out_cur);
     else if (table->dtype == NC_F16 && adt == NC_F16)
         hipLaunchKernelGGL((k_embed<F16, F16>), grid, dim3(256), 0, st, c, dl, table->rows, tokens, out, out_pitch, d, post_scale,
-                           dpos);
+                           dpos, out_cur);
     else
         return fail(NC_ERR_ARG, "token_embed: table dtype %d with activation dtype %d", table->dtype, adt);
     return launch_status("k_embed");

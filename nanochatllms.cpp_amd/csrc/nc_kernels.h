@@ -37,9 +37,9 @@ int silu_mul_launch(int adt, const float* raw, int raw_pitch, int f, uint8_t* ou
                     hipStream_t st);
 
 // dpos != nullptr: embeds the single token tokens[*dpos] (tokens = the
-// sequence base).
+// sequence base).  out_cur (one row): the (single) row is also stored there.
 int embed_launch(const nc_tensor* table, const int32_t* tokens, uint8_t* out, int out_pitch, int adt, int rows,
-                 float post_scale, hipStream_t st, const int* dpos = nullptr);
+                 float post_scale, hipStream_t st, const int* dpos = nullptr, uint8_t* out_cur = nullptr);
 
 int argmax_launch(const float* x, int n, int32_t* out, hipStream_t st);
 
@@ -64,9 +64,11 @@ int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k
 // Decode attention with the q/k/v post-processing fused in (Q8 activations,
 // no qkv bias): raw = the qkv matvec's fp32 row [q | k | v]; the new k / v
 // rows are appended to the caches at the position (*dpos when set, else
-// pos); out = the attention output Act row.
+// pos); out = the attention output Act row.  rope_cur, when set, is the
+// position's RoPE (cos, sin) row at a fixed address (read instead of the
+// table row, so that load does not wait for the position).
 int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
                        const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st);
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur = nullptr);
 
 }  // namespace nc

@@ -77,6 +77,12 @@ public:
     float* rope = nullptr;
     int d_half = 0;
     uint8_t *x0 = nullptr, *xn = nullptr, *q_act = nullptr, *attn = nullptr, *m_act = nullptr;
+    // The fused decode step's rows at fixed addresses (read without waiting
+    // for the device-held position): the embedding of the step's token, the
+    // residual sums after attention and after the MLP, and the position's
+    // RoPE row.
+    uint8_t *cur_x0 = nullptr, *cur1 = nullptr, *cur2 = nullptr;
+    float* cur_rope = nullptr;
     float *qkv_raw = nullptr, *o_raw = nullptr, *gu_raw = nullptr, *down_raw = nullptr, *logits = nullptr;
     int32_t* tokens = nullptr;
     int n_cur = 0;        // tokens in the sequence processed so far
@@ -279,6 +285,8 @@ public:
             (s = alloc_t(&logits, (size_t)c->n_vocab * 4)) || (s = alloc_t(&tokens, (size_t)(mc + 1) * 4)))
             return s;
         if ((s = alloc_t(&am_scratch, (size_t)kDmvArgmaxWords * 8))) return s;
+        if ((s = alloc_t(&cur_x0, pitch(d))) || (s = alloc_t(&cur1, pitch(d))) || (s = alloc_t(&cur2, pitch(d))))
+            return s;
         fused = fused_supported();
         if (const char* f = std::getenv("NC_DECODE_FUSED")) fused = fused && std::atoi(f) != 0;
         // RoPE table from the host libm, the reference's expression
@@ -286,6 +294,7 @@ public:
         std::vector<float> tab((size_t)mc * std::max(d_half, 1) * 2);
         if ((s = nc_rope_table(mc, c->d_head, c->rope_pct, tab.data()))) return s;
         if ((s = alloc_t(&rope, tab.size() * 4))) return s;
+        if ((s = alloc_t(&cur_rope, (size_t)std::max(d_half, 1) * 8))) return s;
         hipError_t e = hipMemcpyAsync(rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, st);
         if (e == hipSuccess) e = hipStreamSynchronize(st);
         return e == hipSuccess ? NC_OK : hip_fail(e, "rope table upload");
@@ -625,8 +634,11 @@ public:
         const bool minicpm = cfg.arch == NC_ARCH_MINICPM;
         const float bs = branch_scale();
         int s;
-        if ((s = embed_launch(&emb, dpos ? tokens : tokens + pos, x0 + (dpos ? 0 : (size_t)pos * pd), pd, adt, 1,
-                              minicpm ? 12.0f : 1.0f, st, dpos)))
+        // Under graph replay (dpos) the previous step's lm head has stored
+        // this step's embedding row (cur_x0) and RoPE row (cur_rope); a
+        // direct step embeds its token first.
+        if (!dpos && (s = embed_launch(&emb, tokens + pos, x0 + (size_t)pos * pd, pd, adt, 1, minicpm ? 12.0f : 1.0f,
+                                       st, nullptr, cur_x0)))
             return s;
         DmvArgs base;
         base.pos = pos;
@@ -641,18 +653,20 @@ public:
             a.norm_w = y.attn_norm;
             a.raw = qkv_raw;
             if (l == 0) {
-                a.x = x0;
-                a.x_pitch = pd;
+                a.x = cur_x0;
+                a.x_pitch = 0;
                 if ((s = dmv(a, &y.qkv, PRO_RMS, EPI_RAW, NC_PROF_QKV))) return s;
             } else {
                 a.res_in = L[l - 1].res1;
+                a.res_cur = cur1;
                 a.raw_in = down_raw;
                 a.res_out = L[l - 1].res2;
+                a.res_cur_out = cur2;
                 if ((s = dmv(a, &y.qkv, PRO_RES_RMS, EPI_RAW, NC_PROF_QKV))) return s;
             }
             if (!y.bq) {
                 if ((s = attn_decode_launch(qkv_raw, y.hq, y.hkv, y.qn, y.kn, rope, d_half, pos, dpos, y.kc, y.vc, pkv,
-                                            attn, cfg.max_ctx, st)))
+                                            attn, cfg.max_ctx, st, dpos ? cur_rope : nullptr)))
                     return s;
             } else {
                 if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half,
@@ -668,8 +682,10 @@ public:
             if ((s = dmv(a, &y.o, PRO_X, EPI_RAW, NC_PROF_O))) return s;
             a = base;
             a.res_in = l == 0 ? x0 : L[l - 1].res2;
+            a.res_cur = l == 0 ? cur_x0 : cur2;
             a.raw_in = o_raw;
             a.res_out = y.res1;
+            a.res_cur_out = cur1;
             a.norm_w = y.mlp_norm;
             a.m_out = m_act;
             if ((s = dmv(a, &y.gu, PRO_RES_RMS, EPI_SWIGLU, NC_PROF_GATE_UP))) return s;
@@ -680,6 +696,7 @@ public:
         }
         DmvArgs a = base;
         a.res_in = L[cfg.n_layers - 1].res1;
+        a.res_cur = cur1;
         a.raw_in = down_raw;
         a.res_out = L[cfg.n_layers - 1].res2;
         a.norm_w = norm_w;
@@ -688,6 +705,19 @@ public:
         a.tokens = tokens;
         a.pos_out = dpos;
         a.amax = am_scratch;
+        if (dpos) {
+            // the next step's embedding and RoPE rows, from the greedy token
+            a.emb_codes = (const uint32_t*)emb.data;
+            a.emb_deltas = (const uint16_t*)emb.deltas;
+            a.emb_scale = minicpm ? 12.0f : 1.0f;
+            a.emb_cur = cur_x0;
+            a.emb_rows = x0;
+            a.emb_pitch = pd;
+            a.max_ctx = cfg.max_ctx;
+            a.rope_table = rope;
+            a.rope_cur = cur_rope;
+            a.rope_half = d_half;
+        }
         return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_ARGMAX, NC_PROF_LM_HEAD);
     }
 
@@ -767,6 +797,16 @@ public:
             const int pos = n_cur;
             hipError_t e = hipMemcpyAsync(step_pos, &pos, 4, hipMemcpyHostToDevice, st);
             if (e != hipSuccess) return hip_fail(e, "decode: position upload");
+            if (fused) {
+                // the first replayed step's inputs (later steps' come from the
+                // lm head before them): its token's embedding and RoPE row
+                if ((s = embed_launch(&emb, tokens + pos, x0 + (size_t)pos * pitch(d), pitch(d), adt, 1,
+                                      cfg.arch == NC_ARCH_MINICPM ? 12.0f : 1.0f, st, nullptr, cur_x0)))
+                    return s;
+                if (d_half > 0 && (e = hipMemcpyAsync(cur_rope, rope + (size_t)pos * d_half * 2, (size_t)d_half * 8,
+                                                      hipMemcpyDeviceToDevice, st)) != hipSuccess)
+                    return hip_fail(e, "decode: rope row");
+            }
             // the upload reads host memory asynchronously: wait before `pos` dies
             if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "decode: sync");
             for (int i = 0; i < n_steps; i++)
