@@ -1,0 +1,199 @@
+// nc_gemm.hip -- prefill matmul of Q8 activation rows with Q4 / Q8 weights
+// on the matrix cores, with the reference's arithmetic.
+//
+// matmul_2d_impl (gten/ops.cpp:579-614) computes each output as the
+// reference's block dot product (vec_dot_product_q8 / _q8_q4, ops.cpp:
+// 292-490): per 32-value block b, four int32 lane sums L_k(b) over the
+// elements {2k, 2k+1, 2k+8, 2k+9} and the same + 16, fp32 terms
+// float(L_k) * (d_x * d_w), four fp32 chains acc_k folded in block order,
+// and (acc_0 + acc_1) + (acc_2 + acc_3).
+//
+// The integer lane sums come from v_mfma_i32_16x16x32_i8 (K = 32 = one
+// block), with the activation operand expanded by lane: matrix row 4r + k
+// holds row r's lane-k codes in K group k and zeros in the other three
+// groups, the weight operand holds column n's lane-g codes in K group g (the
+// weights are stored lane-permuted, so a lane's eight codes are one dword
+// (Q4) or two (Q8)).  Result entry (4r + k, n) is then exactly L_k(r, n),
+// and the MFMA output layout puts the four lane sums of one (row, column)
+// in one thread: thread (n, r) owns its chains and folds them in block
+// order with plain fp32 multiplies and adds -- the reference's rounding
+// steps, one per block and lane.  Q4 codes enter raw (0..14): the
+// accumulator starts at -7 * (sum of the lane's activation codes), so the
+// MFMA yields sum (code - 7) * x, as the reference's decoded values give.
+//
+// Three quarters of each activation operand are zeros: the matrix cores do
+// four times the necessary integer work, which is cheap next to the
+// vector-unit fold (13 fp32 operations per output and block).
+#include <hip/hip_ext.h>
+
+#include "nc_kernels.h"
+#include "nc_qdot.h"
+
+namespace nc {
+
+constexpr int kGmThreads = 256;
+constexpr int kGmRows = 16;                // output rows per workgroup
+constexpr int kGmColsW = 32;               // output columns per wavefront (two 16-wide groups)
+constexpr int kGmCols = 4 * kGmColsW;      // per workgroup
+constexpr int kGmChunk = 4;                // activation blocks staged per step (double-buffered)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+template <int WT>
+__global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
+                                                      const uint32_t* __restrict__ wq,
+                                                      const uint16_t* __restrict__ wd, float* __restrict__ out,
+                                                      int out_pitch, int N, int nb)
+{
+    constexpr int WV = WT == Q4 ? 1 : 2;  // code dwords of one lane of a weight block
+    constexpr int WD = WT == Q4 ? 4 : 8;  // code dwords per weight block
+    // staged activation blocks (nc_qdot.h layout): [buffer][block][row]
+    __shared__ __align__(16) uint32_t xs[2][kGmChunk][kGmRows][kStage];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int lc = lane & 15, lg = lane >> 4;  // column within a 16-group; K group (AVX lane)
+    const int r0 = blockIdx.y * kGmRows;
+    const int c0 = blockIdx.x * kGmCols + wv * kGmColsW;
+    const int nch = (nb + kGmChunk - 1) / kGmChunk;
+
+    // staging: thread t < 64 stages (row t % 16, block t / 16) of each chunk;
+    // rows past the end repeat the last row (their outputs are not stored)
+    const int srow = tid & 15, sblk = (tid >> 4) & (kGmChunk - 1);
+    const uint8_t* xrow = x + (size_t)min(r0 + srow, n_rows - 1) * x_pitch;
+    auto stage_load = [&](int ch) { return load_x_block(xrow, nb, min(ch * kGmChunk + sblk, nb - 1)); };
+
+    // this thread's weight columns (columns past the end repeat the last)
+    size_t wrow[2];
+#pragma unroll
+    for (int n = 0; n < 2; n++) wrow[n] = (size_t)min(c0 + 16 * n + lc, N - 1) * nb;
+    auto w_load = [&](int ch, uint32_t (&w)[kGmChunk][2][WV], uint16_t (&d)[kGmChunk][2]) {
+#pragma unroll
+        for (int j = 0; j < kGmChunk; j++) {
+            const int b = min(ch * kGmChunk + j, nb - 1);
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                const uint32_t* blk = wq + (wrow[n] + b) * WD;
+#pragma unroll
+                for (int v = 0; v < WV; v++) w[j][n][v] = blk[WV * lg + v];
+                d[j][n] = wd[wrow[n] + b];
+            }
+        }
+    };
+
+    float acc[4][2][4];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc[m][n][k] = 0.0f;
+
+    uint32_t wc[kGmChunk][2][WV];
+    uint16_t dc[kGmChunk][2];
+    {
+        XRaw xr{};
+        if (tid < 64) xr = stage_load(0);
+        w_load(0, wc, dc);
+        if (tid < 64) stage_x_block(xr, xs[0][sblk][srow]);
+    }
+    lds_barrier();
+    for (int ch = 0; ch < nch; ch++) {
+        const int buf = ch & 1;
+        const bool more = ch + 1 < nch;
+        XRaw xn{};
+        uint32_t wn[kGmChunk][2][WV];
+        uint16_t dn[kGmChunk][2];
+        if (more) {
+            if (tid < 64) xn = stage_load(ch + 1);
+            w_load(ch + 1, wn, dn);
+        }
+#pragma unroll
+        for (int j = 0; j < kGmChunk; j++) {
+            if (ch * kGmChunk + j >= nb) break;  // uniform
+            // weight operands: column lc of group n, lane lg's eight codes
+            long B[2];
+            float dw[2];
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                if (WT == Q4) {
+                    const uint32_t P = wc[j][n][0];
+                    // high nibbles pair with codes {2k,2k+1,2k+8,2k+9}, low
+                    // nibbles with those + 16 (the staged xa_k, xb_k order)
+                    B[n] = (long)(uint64_t)(((P >> 4) & 0x0F0F0F0Fu) | ((uint64_t)(P & 0x0F0F0F0Fu) << 32));
+                } else {
+                    B[n] = (long)(uint64_t)(wc[j][n][0] | ((uint64_t)wc[j][n][1] << 32));
+                }
+                dw[n] = h2f(dc[j][n]);
+            }
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                // activation operand: matrix row lc = 4 r' + k of row group m
+                // holds row (4m + r')'s lane-k codes in K group k only
+                const uint32_t* sa = xs[buf][j][4 * m + (lc >> 2)];
+                long A = 0;
+                if (lg == (lc & 3)) {
+                    const uint2 v = *reinterpret_cast<const uint2*>(sa + 2 * lg);
+                    A = (long)(uint64_t)(v.x | ((uint64_t)v.y << 32));
+                }
+                // this thread's outputs: row 4m + lg, lane sums k = 0..3
+                const uint32_t* sr = xs[buf][j][4 * m + lg];
+                const uint4 cs = *reinterpret_cast<const uint4*>(sr + 8);
+                const v4i cinit = WT == Q4 ? v4i{(int)cs.x, (int)cs.y, (int)cs.z, (int)cs.w} : v4i{0, 0, 0, 0};
+                const float dx = __uint_as_float(sr[12]);
+#pragma unroll
+                for (int n = 0; n < 2; n++) {
+                    const v4i L = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B[n], cinit, 0, 0, 0);
+                    const float dd = dx * dw[n];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[m][n][k] = acc[m][n][k] + (float)L[k] * dd;
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < kGmChunk; j++)
+#pragma unroll
+                for (int n = 0; n < 2; n++) {
+#pragma unroll
+                    for (int v = 0; v < WV; v++) wc[j][n][v] = wn[j][n][v];
+                    dc[j][n] = dn[j][n];
+                }
+            if (tid < 64) stage_x_block(xn, xs[buf ^ 1][sblk][srow]);
+        }
+        lds_barrier();
+    }
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const int row = r0 + 4 * m + lg;
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const int col = c0 + 16 * n + lc;
+            if (row < n_rows && col < N)
+                out[(size_t)row * out_pitch + col] = (acc[m][n][0] + acc[m][n][1]) + (acc[m][n][2] + acc[m][n][3]);
+        }
+    }
+}
+
+int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
+               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop)
+{
+    if (w->dtype != NC_Q4 && w->dtype != NC_Q8) return fail(NC_ERR_ARG, "gemm: Q4/Q8 weights only");
+    if (w->cols % 32 || w->cols <= 0 || w->rows <= 0 || n_rows <= 0)
+        return fail(NC_ERR_ARG, "gemm: [%d x %d] weights, %d rows", w->rows, w->cols, n_rows);
+    const int N = w->rows, nb = w->cols / 32;
+    const dim3 grid((N + kGmCols - 1) / kGmCols, (n_rows + kGmRows - 1) / kGmRows);
+    auto go = [&](auto kern) {
+        if (ev_start)
+            hipExtLaunchKernelGGL(kern, grid, dim3(kGmThreads), 0, st, ev_start, ev_stop, 0, x, x_pitch, n_rows,
+                                  (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+        else
+            hipLaunchKernelGGL(kern, grid, dim3(kGmThreads), 0, st, x, x_pitch, n_rows, (const uint32_t*)w->data,
+                               (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+    };
+    if (w->dtype == NC_Q4)
+        go(k_gemm_q<Q4>);
+    else
+        go(k_gemm_q<Q8>);
+    return launch_status("k_gemm_q");
+}
+
+}  // namespace nc

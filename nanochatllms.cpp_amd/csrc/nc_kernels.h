@@ -18,6 +18,13 @@ int write_rows(const float* in, int in_pitch, uint8_t* out, int out_pitch, int d
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
                hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 
+// x rows times Q4/Q8 weight rows -> fp32 dots on the matrix cores (the
+// reference's block dot product, exact); used by matvec_raw for multi-row
+// (prefill) products.
+int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
+               hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+constexpr int kGemmMinRows = 8;  // matvec_raw takes the matrix-core path from this many rows
+
 // Norm over segments of d_norm values; with `add` the input is
 // a + requant(braw) (scaled by bscale and requantized when bscale != 1),
 // stored to h_out.  dpos != nullptr: a and h_out rows are taken at the

@@ -248,6 +248,7 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
     if (w->dtype == NC_Q4 || w->dtype == NC_Q8) {
         if (x_dtype != NC_Q8) return fail(NC_ERR_ARG, "matmul: Q%d weights need Q8 activations", w->dtype == NC_Q4 ? 4 : 8);
         if (K % 32) return fail(NC_ERR_ARG, "matmul: K=%d is not a multiple of 32", K);
+        if (n_rows >= kGemmMinRows) return gemm_q_raw(x, x_pitch, n_rows, w, out, out_pitch, st, ev_start, ev_stop);
         const int nb = K / 32;
         constexpr int R = 4;
         if (R * nb > kMvThreads * kMvMaxItems) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);
