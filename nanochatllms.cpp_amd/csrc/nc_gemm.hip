@@ -31,28 +31,30 @@
 
 namespace nc {
 
-constexpr int kGmThreads = 256;
 constexpr int kGmRows = 16;                // output rows per workgroup
-constexpr int kGmColsW = 32;               // output columns per wavefront (two 16-wide groups)
-constexpr int kGmCols = 4 * kGmColsW;      // per workgroup
 constexpr int kGmChunk = 4;                // activation blocks staged per step (double-buffered)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-template <int WT>
-__global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
+// NG 16-wide column groups per wavefront, NW wavefronts per workgroup (all
+// on the same 16 rows, side by side in columns); the first 64 threads stage
+// the activation blocks.
+template <int WT, int NG, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
                                                       const uint32_t* __restrict__ wq,
                                                       const uint16_t* __restrict__ wd, float* __restrict__ out,
                                                       int out_pitch, int N, int nb)
 {
     constexpr int WV = WT == Q4 ? 1 : 2;  // code dwords of one lane of a weight block
     constexpr int WD = WT == Q4 ? 4 : 8;  // code dwords per weight block
+    constexpr int kGmNg = NG;
+    constexpr int kGmCols = 16 * NG * NW;  // columns per workgroup
     // staged activation blocks (nc_qdot.h layout): [buffer][block][row]
     __shared__ __align__(16) uint32_t xs[2][kGmChunk][kGmRows][kStage];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int lc = lane & 15, lg = lane >> 4;  // column within a 16-group; K group (AVX lane)
     const int r0 = blockIdx.y * kGmRows;
-    const int c0 = blockIdx.x * kGmCols + wv * kGmColsW;
+    const int c0 = blockIdx.x * kGmCols + wv * 16 * NG;
     const int nch = (nb + kGmChunk - 1) / kGmChunk;
 
     // staging: thread t < 64 stages (row t % 16, block t / 16) of each chunk;
@@ -62,15 +64,15 @@ __global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict
     auto stage_load = [&](int ch) { return load_x_block(xrow, nb, min(ch * kGmChunk + sblk, nb - 1)); };
 
     // this thread's weight columns (columns past the end repeat the last)
-    size_t wrow[2];
+    size_t wrow[kGmNg];
 #pragma unroll
-    for (int n = 0; n < 2; n++) wrow[n] = (size_t)min(c0 + 16 * n + lc, N - 1) * nb;
-    auto w_load = [&](int ch, uint32_t (&w)[kGmChunk][2][WV], uint16_t (&d)[kGmChunk][2]) {
+    for (int n = 0; n < kGmNg; n++) wrow[n] = (size_t)min(c0 + 16 * n + lc, N - 1) * nb;
+    auto w_load = [&](int ch, uint32_t (&w)[kGmChunk][kGmNg][WV], uint16_t (&d)[kGmChunk][kGmNg]) {
 #pragma unroll
         for (int j = 0; j < kGmChunk; j++) {
             const int b = min(ch * kGmChunk + j, nb - 1);
 #pragma unroll
-            for (int n = 0; n < 2; n++) {
+            for (int n = 0; n < kGmNg; n++) {
                 const uint32_t* blk = wq + (wrow[n] + b) * WD;
 #pragma unroll
                 for (int v = 0; v < WV; v++) w[j][n][v] = blk[WV * lg + v];
@@ -79,16 +81,16 @@ __global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict
         }
     };
 
-    float acc[4][2][4];
+    float acc[4][kGmNg][4];
 #pragma unroll
     for (int m = 0; m < 4; m++)
 #pragma unroll
-        for (int n = 0; n < 2; n++)
+        for (int n = 0; n < kGmNg; n++)
 #pragma unroll
             for (int k = 0; k < 4; k++) acc[m][n][k] = 0.0f;
 
-    uint32_t wc[kGmChunk][2][WV];
-    uint16_t dc[kGmChunk][2];
+    uint32_t wc[kGmChunk][kGmNg][WV];
+    uint16_t dc[kGmChunk][kGmNg];
     {
         XRaw xr{};
         if (tid < 64) xr = stage_load(0);
@@ -100,8 +102,8 @@ __global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict
         const int buf = ch & 1;
         const bool more = ch + 1 < nch;
         XRaw xn{};
-        uint32_t wn[kGmChunk][2][WV];
-        uint16_t dn[kGmChunk][2];
+        uint32_t wn[kGmChunk][kGmNg][WV];
+        uint16_t dn[kGmChunk][kGmNg];
         if (more) {
             if (tid < 64) xn = stage_load(ch + 1);
             w_load(ch + 1, wn, dn);
@@ -110,10 +112,10 @@ __global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict
         for (int j = 0; j < kGmChunk; j++) {
             if (ch * kGmChunk + j >= nb) break;  // uniform
             // weight operands: column lc of group n, lane lg's eight codes
-            long B[2];
-            float dw[2];
+            long B[kGmNg];
+            float dw[kGmNg];
 #pragma unroll
-            for (int n = 0; n < 2; n++) {
+            for (int n = 0; n < kGmNg; n++) {
                 if (WT == Q4) {
                     const uint32_t P = wc[j][n][0];
                     // high nibbles pair with codes {2k,2k+1,2k+8,2k+9}, low
@@ -129,18 +131,16 @@ __global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict
                 // activation operand: matrix row lc = 4 r' + k of row group m
                 // holds row (4m + r')'s lane-k codes in K group k only
                 const uint32_t* sa = xs[buf][j][4 * m + (lc >> 2)];
-                long A = 0;
-                if (lg == (lc & 3)) {
-                    const uint2 v = *reinterpret_cast<const uint2*>(sa + 2 * lg);
-                    A = (long)(uint64_t)(v.x | ((uint64_t)v.y << 32));
-                }
+                const uint2 v = *reinterpret_cast<const uint2*>(sa + 2 * lg);
+                const bool own = lg == (lc & 3);
+                const long A = (long)(uint64_t)((own ? v.x : 0u) | ((uint64_t)(own ? v.y : 0u) << 32));
                 // this thread's outputs: row 4m + lg, lane sums k = 0..3
                 const uint32_t* sr = xs[buf][j][4 * m + lg];
                 const uint4 cs = *reinterpret_cast<const uint4*>(sr + 8);
                 const v4i cinit = WT == Q4 ? v4i{(int)cs.x, (int)cs.y, (int)cs.z, (int)cs.w} : v4i{0, 0, 0, 0};
                 const float dx = __uint_as_float(sr[12]);
 #pragma unroll
-                for (int n = 0; n < 2; n++) {
+                for (int n = 0; n < kGmNg; n++) {
                     const v4i L = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B[n], cinit, 0, 0, 0);
                     const float dd = dx * dw[n];
 #pragma unroll
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict
 #pragma unroll
             for (int j = 0; j < kGmChunk; j++)
 #pragma unroll
-                for (int n = 0; n < 2; n++) {
+                for (int n = 0; n < kGmNg; n++) {
 #pragma unroll
                     for (int v = 0; v < WV; v++) wc[j][n][v] = wn[j][n][v];
                     dc[j][n] = dn[j][n];
@@ -165,13 +165,20 @@ __global__ __launch_bounds__(kGmThreads) void k_gemm_q(const uint8_t* __restrict
     for (int m = 0; m < 4; m++) {
         const int row = r0 + 4 * m + lg;
 #pragma unroll
-        for (int n = 0; n < 2; n++) {
+        for (int n = 0; n < kGmNg; n++) {
             const int col = c0 + 16 * n + lc;
             if (row < n_rows && col < N)
                 out[(size_t)row * out_pitch + col] = (acc[m][n][0] + acc[m][n][1]) + (acc[m][n][2] + acc[m][n][3]);
         }
     }
 }
+
+// Workgroup shape (measured on MI355X, prefill of 64 and 512 rows): one
+// wavefront per workgroup (a workgroup of four on the same rows is slower:
+// it shares the staging but waits at every chunk's barrier), and two
+// 16-wide column groups per wavefront once the product has enough
+// wavefronts to fill the CUs several times over, else one.
+constexpr int kGmWideWaves = 4096;
 
 int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
                hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop)
@@ -180,19 +187,24 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
     if (w->cols % 32 || w->cols <= 0 || w->rows <= 0 || n_rows <= 0)
         return fail(NC_ERR_ARG, "gemm: [%d x %d] weights, %d rows", w->rows, w->cols, n_rows);
     const int N = w->rows, nb = w->cols / 32;
-    const dim3 grid((N + kGmCols - 1) / kGmCols, (n_rows + kGmRows - 1) / kGmRows);
-    auto go = [&](auto kern) {
+    const int rt = (n_rows + kGmRows - 1) / kGmRows;
+    const bool wide = (long long)rt * ((N + 31) / 32) >= kGmWideWaves;
+    auto go = [&](auto kern, int ng) {
+        const dim3 grid((N + 16 * ng - 1) / (16 * ng), rt);
         if (ev_start)
-            hipExtLaunchKernelGGL(kern, grid, dim3(kGmThreads), 0, st, ev_start, ev_stop, 0, x, x_pitch, n_rows,
+            hipExtLaunchKernelGGL(kern, grid, dim3(64), 0, st, ev_start, ev_stop, 0, x, x_pitch, n_rows,
                                   (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
         else
-            hipLaunchKernelGGL(kern, grid, dim3(kGmThreads), 0, st, x, x_pitch, n_rows, (const uint32_t*)w->data,
+            hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, x, x_pitch, n_rows, (const uint32_t*)w->data,
                                (const uint16_t*)w->deltas, out, out_pitch, N, nb);
     };
-    if (w->dtype == NC_Q4)
-        go(k_gemm_q<Q4>);
-    else
-        go(k_gemm_q<Q8>);
+    if (w->dtype == NC_Q4) {
+        if (wide) go(k_gemm_q<Q4, 2, 1>, 2);
+        else go(k_gemm_q<Q4, 1, 1>, 1);
+    } else {
+        if (wide) go(k_gemm_q<Q8, 2, 1>, 2);
+        else go(k_gemm_q<Q8, 1, 1>, 1);
+    }
     return launch_status("k_gemm_q");
 }
 
