@@ -218,6 +218,176 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const uint8_t* __restrict
     }
 }
 
+// Prefill: kArRows consecutive query rows of one head per workgroup, with
+// the same arithmetic as k_attn.  The V slice and every K row are read once
+// for all of them, and each row stops at its own position: past it the
+// reference's probabilities are exact zeros (expf(-inf) = 0, requantized to
+// 0), so they add nothing to the sequential softmax sum, to the absmax of
+// their 32-position blocks, or to the P.V lane chains (each starts at +0,
+// and adding +/-0 leaves a running sum unchanged, its sign included).
+constexpr int kArRows = 8;
+
+template <int ADT>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_rows(const uint8_t* __restrict__ q, int q_pitch,
+                                                            const uint8_t* __restrict__ kc, int k_pitch,
+                                                            const uint8_t* __restrict__ vc, int v_pitch,
+                                                            uint8_t* __restrict__ out, int out_pitch, int hq, int hkv,
+                                                            int start, int n_ctx, int rows, float scale)
+{
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float outs[kArRows][64];
+    constexpr int VB = v_stage_bytes<ADT>();
+    constexpr int VPARTS = ADT == Q8 ? 4 : 8;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int h = blockIdx.x, qr0 = blockIdx.y * kArRows;
+    const int nr = min(kArRows, rows - qr0);
+    const int m = start + qr0 + nr;  // positions attended by any of the rows
+    const int mpad = (m + 3) & ~3;
+    float* S = sm;                                                  // [kArRows][mpad]
+    uint8_t* Vs = reinterpret_cast<uint8_t*>(S + kArRows * mpad);   // [m][VB]
+    const int g = h / (hq / hkv);
+    const int qcols = hq * 64, kvcols = hkv * 64;
+    const int qd = act_delta_offset(qcols), kvd = act_delta_offset(kvcols);
+
+    // ---- V head slice of positions [0, m)
+    for (int idx = tid; idx < m * VPARTS; idx += kAttnThreads) {
+        const int c = idx / VPARTS, part = idx % VPARTS;
+        const uint8_t* vrow = vc + (size_t)c * v_pitch;
+        reinterpret_cast<uint4*>(Vs + (size_t)c * VB)[part] =
+                reinterpret_cast<const uint4*>(vrow + g * (ADT == Q8 ? 64 : 128))[part];
+        if (ADT == Q8 && part == 0)
+            reinterpret_cast<uint32_t*>(Vs + (size_t)c * VB + 64)[0] = reinterpret_cast<const uint32_t*>(vrow + kvd)[g];
+    }
+
+    // ---- scores: thread = (row i, positions c0 + 32 k); the eight rows
+    // sharing a position read its K row together
+    {
+        const int i = tid & (kArRows - 1);
+        const int ic = min(i, nr - 1);
+        const int row = start + qr0 + i;  // absolute position of the query
+        const uint8_t* qrow = q + (size_t)(qr0 + ic) * q_pitch;
+        if (ADT == Q8) {
+            uint32_t qa[2][4], qb[2][4];
+            float dq[2];
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                lane_dwords(qrow + h * 64 + b * 32, qa[b], qb[b]);
+                dq[b] = h2f(reinterpret_cast<const uint16_t*>(qrow + qd)[h * 2 + b]);
+            }
+            for (int c = tid / kArRows; c < m; c += kAttnThreads / kArRows) {
+                if (i < nr && c <= row) {
+                    const uint8_t* krow = kc + (size_t)c * k_pitch;
+                    float a4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int b = 0; b < 2; b++) {
+                        uint32_t ka[4], kb[4];
+                        lane_dwords(krow + g * 64 + b * 32, ka, kb);
+                        const float dd = dq[b] * h2f(reinterpret_cast<const uint16_t*>(krow + kvd)[g * 2 + b]);
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            int L = __builtin_amdgcn_sdot4((int)qa[b][k], (int)ka[k], 0, false);
+                            L = __builtin_amdgcn_sdot4((int)qb[b][k], (int)kb[k], L, false);
+                            a4[k] = a4[k] + (float)L * dd;
+                        }
+                    }
+                    S[i * mpad + c] = ((a4[0] + a4[1]) + (a4[2] + a4[3])) * scale;
+                }
+            }
+        } else {
+            float qv[64];
+            const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + h * 64;
+#pragma unroll
+            for (int e = 0; e < 64; e++) qv[e] = h2f(qh[e]);
+            for (int c = tid / kArRows; c < m; c += kAttnThreads / kArRows) {
+                if (i < nr && c <= row) {
+                    const uint16_t* kh = reinterpret_cast<const uint16_t*>(kc + (size_t)c * k_pitch) + g * 64;
+                    float a8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                    for (int mm = 0; mm < 8; mm++)
+#pragma unroll
+                        for (int j = 0; j < 8; j++) a8[j] = __builtin_fmaf(qv[8 * mm + j], h2f(kh[8 * mm + j]), a8[j]);
+                    const float sc = a8[0] + a8[1] + a8[2] + a8[3] + a8[4] + a8[5] + a8[6] + a8[7];
+                    S[i * mpad + c] = sc * scale;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- softmax of row i on wave i % 4: max, expf, sequential sum over
+    // [0, row], divide, requantize in 32-position blocks
+    for (int i = w; i < nr; i += kAttnThreads / kWave) {
+        const int n = start + qr0 + i + 1;  // positions of this row
+        float* Si = S + i * mpad;
+        float mx = -INFINITY;
+        for (int c = lane; c < n; c += kWave) mx = fmaxf(mx, Si[c]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        for (int c = lane; c < n; c += kWave) Si[c] = expf_ref(Si[c] - mx);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        const float sum = seq_sum(Si, n);
+        for (int c0 = 0; c0 < n; c0 += kWave) {
+            const int c = c0 + lane;
+            const bool valid = c < n;
+            const float p = valid ? Si[c] / sum : 0.0f;
+            const float pr = act_roundtrip<ADT>(p, valid);
+            if (valid) Si[c] = pr;
+        }
+    }
+    __syncthreads();
+
+    // ---- P.V: thread = (column j, lanes 2 lp and 2 lp + 1) for every row;
+    // row i's lane chains cover positions < min(n_i, n8), n8 = the call's
+    // n_ctx rounded down to 8 (the reference's 8-lane part), then the lane
+    // sums left to right across the quad and the tail positions in order
+    {
+        const int j = tid >> 2, lp = tid & 3;
+        const int n8 = (n_ctx / 8) * 8;
+        auto vval = [&](int c) -> float {
+            const uint8_t* vr = Vs + (size_t)c * VB;
+            if (ADT == Q8)
+                return (float)reinterpret_cast<const int8_t*>(vr)[j] * h2f(reinterpret_cast<const uint16_t*>(vr + 64)[j >> 5]);
+            return h2f(reinterpret_cast<const uint16_t*>(vr)[j]);
+        };
+        float a[kArRows][2];
+#pragma unroll
+        for (int i = 0; i < kArRows; i++) a[i][0] = a[i][1] = 0.0f;
+        const int lim_max = min(m, n8);
+        for (int c8 = 0; c8 < lim_max; c8 += 8) {
+            const int c = c8 + 2 * lp;
+            const float v0 = vval(min(c, m - 1)), v1 = vval(min(c + 1, m - 1));
+#pragma unroll
+            for (int i = 0; i < kArRows; i++) {
+                const int lim = min(start + qr0 + i + 1, n8);
+                const float* Si = S + i * mpad;
+                if (c < lim) a[i][0] = Si[c] * v0 + a[i][0];
+                if (c + 1 < lim) a[i][1] = Si[c + 1] * v1 + a[i][1];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kArRows; i++) {
+            // left-to-right lane sum through the quad: lp 0 holds lanes 0, 1,
+            // lp 1 lanes 2, 3, ...
+            float t = a[i][0] + a[i][1];
+#pragma unroll
+            for (int k = 1; k < 4; k++) {
+                const float tin = dpp_f<0x90, 0xf, false>(t, t);  // quad_perm [0, 0, 1, 2]: lane lp reads lp - 1
+                if (lp == k) t = (tin + a[i][0]) + a[i][1];
+            }
+            if (lp == 3 && i < nr) {
+                const int n = start + qr0 + i + 1;
+                for (int c = n8; c < n; c++) t = t + S[i * mpad + c] * vval(c);
+                outs[i][j] = t;
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = w; i < nr; i += kAttnThreads / kWave)
+        act_store<ADT>(out + (size_t)(qr0 + i) * out_pitch, h * 64 + lane, qd, outs[i][lane], true);
+}
+
 int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k_pitch, const uint8_t* vc, int v_pitch,
                 uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st, const int* dpos,
                 int max_ctx)
@@ -232,6 +402,23 @@ int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k
     const int vb = adt == NC_Q8 ? v_stage_bytes<Q8>() : v_stage_bytes<F16>();
     const size_t lds = ((size_t)((lds_ctx + 3) & ~3) + 64 + 512) * 4 + (size_t)lds_ctx * vb;
     if (lds > 64 * 1024) return fail(NC_ERR_ARG, "qkv_attn: context %d too long", lds_ctx);
+    // prefill: several query rows per workgroup when their shared memory fits
+    if (!dpos && rows > 1) {
+        const int m = n_ctx;  // the last group attends at most n_ctx positions
+        const size_t lds_r = (size_t)kArRows * ((m + 3) & ~3) * 4 + (size_t)m * vb;
+        if (lds_r <= 64 * 1024) {
+            const dim3 grid_r(hq, (rows + kArRows - 1) / kArRows);
+            if (adt == NC_Q8)
+                hipLaunchKernelGGL((k_attn_rows<Q8>), grid_r, dim3(kAttnThreads), lds_r, st, q, q_pitch, kc, k_pitch, vc,
+                                   v_pitch, out, out_pitch, hq, hkv, start, n_ctx, rows, scale);
+            else if (adt == NC_F16)
+                hipLaunchKernelGGL((k_attn_rows<F16>), grid_r, dim3(kAttnThreads), lds_r, st, q, q_pitch, kc, k_pitch, vc,
+                                   v_pitch, out, out_pitch, hq, hkv, start, n_ctx, rows, scale);
+            else
+                return fail(NC_ERR_ARG, "qkv_attn: activation dtype %d", adt);
+            return launch_status("k_attn_rows");
+        }
+    }
     const dim3 grid(hq, rows);
     if (adt == NC_Q8)
         hipLaunchKernelGGL((k_attn<Q8>), grid, dim3(kAttnThreads), lds, st, q, q_pitch, kc, k_pitch, vc, v_pitch, out, out_pitch,
