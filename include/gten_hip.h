@@ -192,6 +192,13 @@ int nc_model_init_synthetic(void* model, uint64_t seed);
 /* One weight from its reference payload bytes (read_into_weight,
  * src/gten/utils.cpp:29-48). */
 int nc_model_set_weight(void* model, int layer, int slot, const void* ref_bytes, size_t n_bytes);
+/* Model::load_from_ckpt (src/tinyllama/tinyllama.cpp:131-187 and its
+ * siblings; records read as gten::read_layer_header / read_into_weight,
+ * src/gten/utils.cpp:29-61): every weight from a .gten checkpoint file, in
+ * the model's file order.  A wrong magic number, a payload size that does
+ * not match the tensor, or a truncated file is an error (the reference
+ * asserts). */
+int nc_model_load_gten(void* model, const char* path);
 /* The stored weight back in the reference's payload bytes. */
 int nc_model_get_weight(void* model, int layer, int slot, void* ref_bytes, size_t n_bytes);
 /* Model::logits(tokens, start_pos): processes rows [start_pos, n_tokens) and

@@ -132,6 +132,7 @@ def lib():
         "nc_model_create": (I, [C.POINTER(ModelConfig), C.POINTER(VP)]), "nc_model_free": (I, [VP]),
         "nc_model_init_synthetic": (I, [VP, U64]), "nc_model_set_weight": (I, [VP, I, I, VP, SZ]),
         "nc_model_get_weight": (I, [VP, I, I, VP, SZ]), "nc_model_logits": (I, [VP, VP, I, I, VP]),
+        "nc_model_load_gten": (I, [VP, C.c_char_p]),
         "nc_model_layer_out": (I, [VP, I, I, VP]), "nc_model_generate": (I, [VP, VP, I, I, VP, C.POINTER(I)]),
         "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
         "nc_model_profile_begin": (I, [VP, I]),
@@ -204,6 +205,10 @@ class Model:
 
     def init_synthetic(self, seed):
         check(lib().nc_model_init_synthetic(self.h, seed), "init_synthetic")
+
+    def load_gten(self, path):
+        """Model::load_from_ckpt: every weight from a .gten checkpoint file."""
+        check(lib().nc_model_load_gten(self.h, os.fsencode(path)), "load_gten")
 
     def set_weight(self, layer, slot, ref_bytes):
         check(lib().nc_model_set_weight(self.h, layer, slot, _ptr(ref_bytes), ref_bytes.nbytes), "set_weight")

@@ -19,8 +19,11 @@
 // Decode keeps the token stream on the device: argmax writes the next token
 // where the next step's embedding reads it, so steps need no host round trip.
 #include <cmath>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
+#include <string>
 #include <memory>
 #include <vector>
 
@@ -63,6 +66,10 @@ __global__ void k_f16_rows(const float* __restrict__ w, int rows, int cols, int 
 }
 
 }  // namespace
+
+// .gten checkpoint magic number (the converters' GTEN_MAGIC_NUMBER,
+// tinyllama/tinyllama_to_gten.py:7; checked in load_from_ckpt).
+constexpr int64_t kGtenMagic = 0x454c49464e455447;
 
 class Decoder {
 public:
@@ -445,6 +452,98 @@ public:
             e = hipMemcpy((uint16_t*)o.mat->deltas + (size_t)o.row_off * (o.cols / 32), deltas.data(), db,
                           hipMemcpyHostToDevice);
         return e == hipSuccess ? NC_OK : hip_fail(e, "set_weight");
+    }
+
+    // ------------------------------------------------------- checkpoint --
+
+    // The tensors of a .gten checkpoint in file order, as each model's
+    // load_from_ckpt reads them (tinyllama/tinyllama.cpp:131-187,
+    // zephyr/zephyr.cpp:79-150, minicpm/minicpm.cpp:113-166,
+    // openelm/openelm.cpp:201-262).
+    std::vector<std::pair<int, int>> gten_order() const
+    {
+        std::vector<std::pair<int, int>> o;
+        const int a = cfg.arch;
+        o.push_back({-1, NC_TID_EMB});
+        for (int l = 0; l < cfg.n_layers; l++) {
+            if (a == NC_ARCH_ZEPHYR) {
+                for (int s : {NC_W_Q, NC_W_Q_BIAS, NC_W_K, NC_W_K_BIAS, NC_W_V, NC_W_V_BIAS, NC_W_O, NC_W_GATE, NC_W_UP,
+                              NC_W_DOWN, NC_W_ATTN_NORM, NC_W_ATTN_NORM_B, NC_W_MLP_NORM, NC_W_MLP_NORM_B})
+                    o.push_back({l, s});
+            } else {
+                for (int s : {NC_W_Q, NC_W_K, NC_W_V, NC_W_O, NC_W_GATE, NC_W_UP, NC_W_DOWN}) o.push_back({l, s});
+                if (a == NC_ARCH_OPENELM) {
+                    o.push_back({l, NC_W_Q_NORM});
+                    o.push_back({l, NC_W_K_NORM});
+                }
+                o.push_back({l, NC_W_ATTN_NORM});
+                o.push_back({l, NC_W_MLP_NORM});
+            }
+        }
+        o.push_back({-1, NC_TID_NORM});
+        if (a == NC_ARCH_ZEPHYR) o.push_back({-1, NC_TID_NORM_B});
+        if (!tied()) o.push_back({-1, NC_TID_LM});
+        return o;
+    }
+
+    // Payload bytes of one tensor in the reference's storage
+    // (Tensor::nbytes: Q8 / Q4 blocks of 34 / 18 bytes, or fp16 values).
+    int ref_bytes(int layer, int slot, size_t* n)
+    {
+        Loc o;
+        int s = locate(layer, slot, &o);
+        if (s) return s;
+        if (o.vec) {
+            *n = (size_t)o.n * 2;
+        } else {
+            const int dt = o.mat->dtype;
+            *n = dt == NC_F16 ? (size_t)o.rows * o.cols * 2 : (size_t)o.rows * (o.cols / 32) * (dt == NC_Q8 ? 34 : 18);
+        }
+        return NC_OK;
+    }
+
+    // load_from_ckpt: the magic number, then per tensor in file order a
+    // layer header and a weight record (read_layer_header /
+    // read_into_weight, gten/utils.cpp:29-61) -- name size, name, payload
+    // size, payload -- with the reference's checks (magic, payload size,
+    // plus a truncated file) as errors.  Records before a failing one have
+    // already replaced their weights.
+    int load_gten(const char* path)
+    {
+        std::ifstream f(path, std::ios::binary);
+        if (!f) return fail(NC_ERR_ARG, "load_gten: cannot open `%s`", path);
+        int64_t magic = 0;
+        f.read(reinterpret_cast<char*>(&magic), sizeof(magic));
+        if (!f || magic != kGtenMagic)
+            return fail(NC_ERR_ARG, "Magic number in the binary does not match the expected one.");
+        std::vector<char> payload;
+        auto read_name = [&](std::string* name) {
+            int32_t n = 0;
+            f.read(reinterpret_cast<char*>(&n), sizeof(n));
+            if (!f || n < 0 || n > (1 << 20)) return false;
+            name->resize(n);
+            f.read(name->data(), n);
+            return (bool)f;
+        };
+        for (const auto& [layer, slot] : gten_order()) {
+            std::string layer_name, weight_name;
+            if (!read_name(&layer_name) || !read_name(&weight_name))
+                return fail(NC_ERR_ARG, "load_gten: `%s` ends before tensor (%d, %#x)", path, layer, slot);
+            int32_t size = 0;
+            f.read(reinterpret_cast<char*>(&size), sizeof(size));
+            if (!f) return fail(NC_ERR_ARG, "load_gten: `%s` ends before tensor (%d, %#x)", path, layer, slot);
+            size_t want;
+            int s = ref_bytes(layer, slot, &want);
+            if (s) return s;
+            if (size < 0 || (size_t)size != want)
+                return fail(NC_ERR_ARG, "Weight `%s` data size: %d does not match the expected size: %zu.",
+                            weight_name.c_str(), size, want);
+            payload.resize(want);
+            f.read(payload.data(), (std::streamsize)want);
+            if (!f) return fail(NC_ERR_ARG, "load_gten: `%s` ends inside weight `%s`", path, weight_name.c_str());
+            if ((s = set_weight(layer, slot, payload.data(), want))) return s;
+        }
+        return NC_OK;
     }
 
     // Inverse of set_weight: the stored weight in the reference's bytes.
@@ -885,6 +984,12 @@ int nc_model_set_weight(void* model, int layer, int slot, const void* ref_bytes,
 {
     NC_CHECK_ARG(model && ref_bytes, "model: null");
     return static_cast<Decoder*>(model)->set_weight(layer, slot, ref_bytes, n_bytes);
+}
+
+int nc_model_load_gten(void* model, const char* path)
+{
+    NC_CHECK_ARG(model && path, "load_gten: null argument");
+    return static_cast<Decoder*>(model)->load_gten(path);
 }
 
 int nc_model_get_weight(void* model, int layer, int slot, void* ref_bytes, size_t n_bytes)

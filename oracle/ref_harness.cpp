@@ -19,6 +19,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <fstream>
 #include <memory>
 #include <vector>
 
@@ -407,6 +408,75 @@ int ref_generate_greedy(void* p, const int32_t* prompt, int n_prompt, int n_gen,
         toks.push_back(idx);
     }
     return produced;
+}
+
+// Model::load_from_ckpt with the reference's record readers
+// (gten::read_layer_header / read_into_weight, gten/utils.cpp:29-61) over
+// this harness's modules, in each model's file order
+// (tinyllama/tinyllama.cpp:131-187, zephyr/zephyr.cpp:79-150,
+// minicpm/minicpm.cpp:113-166, openelm/openelm.cpp:201-262).  Returns 0, or
+// -1 for a file that does not open or has the wrong magic number (the
+// reference asserts on those; a wrong payload size still exits the process
+// inside read_into_weight, so callers pass well-formed files only).
+int ref_model_load_gten(void* p, const char* path)
+{
+    auto* m = static_cast<RefModel*>(p);
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return -1;
+    int64_t magic = 0;
+    f.read(reinterpret_cast<char*>(&magic), sizeof(magic));
+    if (magic != 0x454c49464e455447) return -1;
+    const ModuleDtype dt = m->dtype;
+    const ModuleDtype norm_dt = {kFloat16, dt.adtype};
+    auto rec = [&](Tensor& t, const ModuleDtype& d) {
+        read_layer_header(f);
+        read_into_weight(f, t, d);
+    };
+    rec(m->emb ? m->emb->m_weight : m->tied->m_weight, dt);
+    const or_config* c = &m->cfg;
+    for (int l = 0; l < c->n_layers; l++) {
+        if (c->arch == OR_ARCH_LLAMA) {
+            auto& b = m->llama[l];
+            for (Linear* x : {&b.m_self_attn.m_query, &b.m_self_attn.m_key, &b.m_self_attn.m_value,
+                              &b.m_self_attn.m_qkv_proj, &b.m_mlp_gate_proj, &b.m_mlp_up_proj, &b.m_mlp_down_proj})
+                rec(x->m_weight, dt);
+            rec(b.m_attn_norm.m_weight, norm_dt);
+            rec(b.m_mlp_norm.m_weight, norm_dt);
+        } else if (c->arch == OR_ARCH_ZEPHYR) {
+            auto& b = m->zephyr[l];
+            for (Linear* x : {&b.m_self_attn.m_query, &b.m_self_attn.m_key, &b.m_self_attn.m_value}) {
+                rec(x->m_weight, dt);
+                rec(x->m_bias, norm_dt);
+            }
+            for (Linear* x : {&b.m_self_attn.m_qkv_proj, &b.m_mlp_gate_proj, &b.m_mlp_up_proj, &b.m_mlp_down_proj})
+                rec(x->m_weight, dt);
+            rec(b.m_attn_norm.m_weight, norm_dt);
+            rec(b.m_attn_norm.m_bias, norm_dt);
+            rec(b.m_mlp_norm.m_weight, norm_dt);
+            rec(b.m_mlp_norm.m_bias, norm_dt);
+        } else if (c->arch == OR_ARCH_MINICPM) {
+            auto& b = m->minicpm[l];
+            for (Linear* x : {&b.m_self_attn.m_query, &b.m_self_attn.m_key, &b.m_self_attn.m_value,
+                              &b.m_self_attn.m_qkv_proj, &b.m_mlp_gate_proj, &b.m_mlp_up_proj, &b.m_mlp_down_proj})
+                rec(x->m_weight, dt);
+            rec(b.m_input_norm.m_weight, norm_dt);
+            rec(b.m_post_attn_norm.m_weight, norm_dt);
+        } else {
+            auto& b = *m->elm[l];
+            for (Linear* x : {&b.q, &b.k, &b.v, &b.o, &b.gate, &b.up, &b.down}) rec(x->m_weight, dt);
+            rec(b.q_norm.m_weight, norm_dt);
+            rec(b.k_norm.m_weight, norm_dt);
+            rec(b.attn_norm.m_weight, norm_dt);
+            rec(b.mlp_norm.m_weight, norm_dt);
+        }
+    }
+    if (m->rms) rec(m->rms->m_weight, norm_dt);
+    if (m->ln) {
+        rec(m->ln->m_weight, norm_dt);
+        rec(m->ln->m_bias, norm_dt);
+    }
+    if (m->lm) rec(m->lm->m_weight, dt);
+    return f ? 0 : -1;
 }
 
 }  // extern "C"

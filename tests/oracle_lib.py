@@ -134,6 +134,7 @@ class Reference(_Lib):
         b = lambda n, r, a: _bind(self.lib, n, r, a)
         self.token_embed_ = b("ref_token_embed", None, [_VP, _I, _VP, _VP, _I, _I, _I, _I, _I])
         self.model_create_ = b("ref_model_create", _VP, [C.POINTER(Config), _U64])
+        self.model_load_gten = b("ref_model_load_gten", _I, [_VP, C.c_char_p])
 
     def token_embed(self, table, wdt, tokens, out, adt, d, vocab, start, n_ctx):
         self.token_embed_(table, wdt, tokens, out, adt, d, vocab, start, n_ctx)
