@@ -19,6 +19,18 @@ SMALL = {
     "small-openelm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=1000, n_embd=256, n_layers=3,
                              n_heads=[2, 2, 3], n_kv_heads=[1, 1, 1], n_ffn=[256, 512, 768], eos=-1,
                              rope_pct=1.0, prompt=16, gen=32, seed=1239),
+    # the model x dtype combinations the full-size workloads do not cover
+    "small-zephyr-q8": dict(arch=nc.ZEPHYR, wdtype=nc.Q8, n_vocab=1000, n_embd=256, n_layers=2, n_heads=4,
+                            n_kv_heads=4, n_ffn=512, eos=999, rope_pct=0.25, prompt=16, gen=32, seed=1240),
+    "small-zephyr-q4": dict(arch=nc.ZEPHYR, wdtype=nc.Q4, n_vocab=1000, n_embd=256, n_layers=2, n_heads=4,
+                            n_kv_heads=4, n_ffn=512, eos=999, rope_pct=0.25, prompt=16, gen=32, seed=1241),
+    "small-minicpm-f16": dict(arch=nc.MINICPM, wdtype=nc.F16, n_vocab=1000, n_embd=256, n_layers=2, n_heads=4,
+                              n_kv_heads=4, n_ffn=512, eos=2, rope_pct=1.0, prompt=16, gen=32, seed=1242),
+    "small-minicpm-q8": dict(arch=nc.MINICPM, wdtype=nc.Q8, n_vocab=1000, n_embd=256, n_layers=2, n_heads=4,
+                             n_kv_heads=4, n_ffn=512, eos=2, rope_pct=1.0, prompt=16, gen=32, seed=1243),
+    "small-openelm-f16": dict(arch=nc.OPENELM, wdtype=nc.F16, n_vocab=1000, n_embd=256, n_layers=3,
+                              n_heads=[2, 2, 3], n_kv_heads=[1, 1, 1], n_ffn=[256, 512, 768], eos=-1,
+                              rope_pct=1.0, prompt=16, gen=32, seed=1244),
 }
 
 
