@@ -155,6 +155,26 @@ size_t or_model_act_row_bytes(or_model* m);
 /* greedy_sample (gten/sampler.cpp:11-60) without the tokenizer: returns the
  * number of generated tokens (stops at eos), tokens appended into out. */
 int or_generate_greedy(or_model* m, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out);
+/* topk_sample (gten/sampler.cpp:63-143) with std::mt19937(seed) in place of
+ * the random_device-seeded generator: n_gen steps, stopping before EOS. */
+int or_generate_topk(or_model* m, const int32_t* prompt, int n_prompt, int n_gen, float temp, int top_k,
+                     uint32_t seed, int32_t* out);
+
+/* ---- top-k / temperature sampling (oracle_sample.c) ---------------------- */
+/* std::mt19937 state: 624 words, then the index of the next word. */
+void or_mt_seed(uint32_t seed, uint32_t* st);
+uint32_t or_mt_next(uint32_t* st);
+double or_mt_canonical(uint32_t* st);
+/* One sampling step of topk_sample (gten/sampler.cpp:90-127) on a logits
+ * row, drawing from the generator st; probs_out (n doubles, may be NULL)
+ * receives the normalized weights std::discrete_distribution holds.
+ * Requires 1 <= min(top_k, 1000) <= n and temp > 0. */
+int or_topk_sample(const float* logits, int n, float temp, int top_k, uint32_t* st, double* probs_out);
+/* glibc exp (std::exp on double) and checks of another exp against it. */
+double or_exp(double x);
+void or_exp_probe_inputs(uint64_t seed, int64_t start, int64_t n, double* x);
+int64_t or_check_exp_fn(double (*fn)(double), uint64_t seed, int64_t count, double* first_x);
+int64_t or_exp_mismatches(const double* x, const double* y, int64_t n, int64_t* first);
 
 #ifdef __cplusplus
 }

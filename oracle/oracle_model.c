@@ -269,6 +269,29 @@ const void* or_model_layer_out(or_model* m, int layer, int row)
 
 size_t or_model_act_row_bytes(or_model* m) { return or_row_bytes(m->adt, m->cfg.n_embd); }
 
+/* topk_sample's loop (gten/sampler.cpp:84-134) with a seeded generator. */
+int or_generate_topk(or_model* m, const int32_t* prompt, int n_prompt, int n_gen, float temp, int top_k,
+                     uint32_t seed, int32_t* out)
+{
+    uint32_t st[625];
+    or_mt_seed(seed, st);
+    const int total = n_prompt + n_gen;
+    int32_t* toks = (int32_t*)malloc((size_t)total * 4);
+    float* lg = (float*)malloc((size_t)m->cfg.n_vocab * 4);
+    memcpy(toks, prompt, (size_t)n_prompt * 4);
+    int n = n_prompt, produced = 0;
+    for (int i = 0; i < n_gen; i++) {
+        or_model_logits(m, toks, n, i == 0 ? 0 : n - 1, lg);
+        const int t = or_topk_sample(lg, m->cfg.n_vocab, temp, top_k, st, NULL);
+        if (t == m->cfg.eos) break;
+        out[produced++] = t;
+        toks[n++] = t;
+    }
+    free(toks);
+    free(lg);
+    return produced;
+}
+
 int or_generate_greedy(or_model* m, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out)
 {
     const int total = n_prompt + n_gen;

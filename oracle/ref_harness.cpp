@@ -16,11 +16,14 @@
 // gten/modules.cpp:247-249), which makes Q8 models abort in qkv_attn
 // (gten/ops.cpp:1216); the OpenELM block is therefore composed here from the
 // reference's modules and ops with that buffer typed in the activation dtype.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <fstream>
 #include <memory>
+#include <random>
+#include <utility>
 #include <vector>
 
 #include "gten/gten.h"
@@ -477,6 +480,61 @@ int ref_model_load_gten(void* p, const char* path)
     }
     if (m->lm) rec(m->lm->m_weight, dt);
     return f ? 0 : -1;
+}
+
+// topk_sample's per-step sampling (gten/sampler.cpp:90-127) with the
+// standard library calls the reference makes -- std::partial_sort, std::exp,
+// std::discrete_distribution<int> -- over a std::mt19937 the caller seeds
+// (the reference seeds it from std::random_device, sampler.cpp:70-71).
+void* ref_rng_create(uint32_t seed) { return new std::mt19937(seed); }
+void ref_rng_free(void* g) { delete static_cast<std::mt19937*>(g); }
+uint32_t ref_rng_next(void* g) { return (uint32_t)(*static_cast<std::mt19937*>(g))(); }
+
+int ref_topk_sample(void* g, const float* logits, int n, float temp, int top_k, double* probs_out)
+{
+    auto& gen = *static_cast<std::mt19937*>(g);
+    top_k = std::min(top_k, 1000);
+    temp = std::min(temp, 2.0f);
+    std::vector<std::pair<double, int>> lp;
+    lp.reserve(n);
+    for (int j = 0; j < n; ++j) lp.emplace_back((double)logits[j] / temp, j);
+    std::partial_sort(lp.begin(), lp.begin() + top_k, lp.end(),
+                      [](const std::pair<double, int>& a, const std::pair<double, int>& b) { return a.first > b.first; });
+    lp.resize(top_k);
+    double sum_exp = 0;
+    for (auto& e : lp) {
+        e.first = std::exp(e.first);
+        sum_exp += e.first;
+    }
+    for (auto& e : lp) e.first = e.first / sum_exp;
+    std::vector<double> w(n, 0.0);
+    for (const auto& e : lp) w[e.second] = e.first;
+    std::discrete_distribution<int> dist(w.begin(), w.end());
+    if (probs_out) {
+        const std::vector<double> pr = n >= 2 ? dist.probabilities() : std::vector<double>(n, 0.0);
+        std::copy(pr.begin(), pr.end(), probs_out);
+    }
+    return dist(gen);
+}
+
+// topk_sample's loop (sampler.cpp:84-134) over this harness's model.
+int ref_generate_topk(void* p, const int32_t* prompt, int n_prompt, int n_gen, float temp, int top_k, uint32_t seed,
+                      int32_t* out)
+{
+    auto* m = static_cast<RefModel*>(p);
+    std::mt19937 gen(seed);
+    std::vector<int32_t> toks(prompt, prompt + n_prompt);
+    std::vector<float> lg(m->cfg.n_vocab);
+    int produced = 0;
+    for (int i = 0; i < n_gen; i++) {
+        const int n = (int)toks.size();
+        ref_model_logits(p, toks.data(), n, i == 0 ? 0 : n - 1, lg.data());
+        const int t = ref_topk_sample(&gen, lg.data(), m->cfg.n_vocab, temp, top_k, nullptr);
+        if (t == m->cfg.eos) break;
+        out[produced++] = t;
+        toks.push_back(t);
+    }
+    return produced;
 }
 
 }  // extern "C"

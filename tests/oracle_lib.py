@@ -114,6 +114,16 @@ class Oracle(_Lib):
         self.weight_shape_ = b("or_weight_shape", _I, [C.POINTER(Config), _I, _I, C.POINTER(_I), C.POINTER(_I),
                                                         C.POINTER(_I)])
 
+        self.mt_seed = b("or_mt_seed", None, [C.c_uint32, _VP])
+        self.mt_next = b("or_mt_next", C.c_uint32, [_VP])
+        self.mt_canonical = b("or_mt_canonical", C.c_double, [_VP])
+        self.topk_sample = b("or_topk_sample", _I, [_VP, _I, _F, _I, _VP, _VP])
+        self.exp = b("or_exp", C.c_double, [C.c_double])
+        self.exp_probe_inputs = b("or_exp_probe_inputs", None, [_U64, C.c_int64, C.c_int64, _VP])
+        self.check_exp_fn = b("or_check_exp_fn", C.c_int64, [_VP, _U64, C.c_int64, C.POINTER(C.c_double)])
+        self.exp_mismatches = b("or_exp_mismatches", C.c_int64, [_VP, _VP, C.c_int64, C.POINTER(C.c_int64)])
+        self.generate_topk = b("or_generate_topk", _I, [_VP, _VP, _I, _I, _F, _I, C.c_uint32, _VP])
+
     def token_embed(self, table, wdt, tokens, out, adt, d, vocab, start, n_ctx):
         self.token_embed_(table, wdt, tokens, out, adt, d, start, n_ctx)
 
@@ -135,6 +145,11 @@ class Reference(_Lib):
         self.token_embed_ = b("ref_token_embed", None, [_VP, _I, _VP, _VP, _I, _I, _I, _I, _I])
         self.model_create_ = b("ref_model_create", _VP, [C.POINTER(Config), _U64])
         self.model_load_gten = b("ref_model_load_gten", _I, [_VP, C.c_char_p])
+        self.rng_create = b("ref_rng_create", _VP, [C.c_uint32])
+        self.rng_free = b("ref_rng_free", None, [_VP])
+        self.rng_next = b("ref_rng_next", C.c_uint32, [_VP])
+        self.topk_sample = b("ref_topk_sample", _I, [_VP, _VP, _I, _F, _I, _VP])
+        self.generate_topk = b("ref_generate_topk", _I, [_VP, _VP, _I, _I, _F, _I, C.c_uint32, _VP])
 
     def token_embed(self, table, wdt, tokens, out, adt, d, vocab, start, n_ctx):
         self.token_embed_(table, wdt, tokens, out, adt, d, vocab, start, n_ctx)
