@@ -137,6 +137,24 @@ float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int* fast);
 /* Greedy pick of greedy_sample (src/gten/sampler.cpp:33-41): first index of
  * the maximum. */
 int nc_argmax(const float* x, int n, int32_t* out, void* stream);
+/* std::mt19937(seed) as a 625-word state (624 words, then the index of the
+ * next word), written to host memory `state`; the reference seeds its
+ * generator from std::random_device (src/gten/sampler.cpp:70-71). */
+int nc_rng_seed(uint32_t seed, uint32_t* state);
+/* One sampling step of topk_sample (src/gten/sampler.cpp:90-127) on the
+ * device: logits[n_vocab] (device), top_k and temp clamped to 1000 and 2.0
+ * as sampler.cpp:66-67 does, the mt19937 state rng_state (device, 625
+ * words) advanced by the draw, the token to *token (device).  probs (device,
+ * n_vocab doubles, may be NULL) receives the normalized weights the
+ * discrete distribution holds.  Errors: top_k < 1 or above n_vocab,
+ * temp <= 0 or NaN, n_vocab < 2. */
+int nc_sample_topk(const float* logits, int n_vocab, float temp, int top_k, uint32_t* rng_state, int32_t* token,
+                   double* probs, void* stream);
+/* std::exp on double as the sampler uses it (src/gten/sampler.cpp:112-113,
+ * the host glibc's exp): y[i] = exp(x[i]) on the device. */
+int nc_exp(const double* x, double* y, int64_t n, void* stream);
+/* The same function evaluated on the host CPU (no GPU needed). */
+double nc_exp_host(double x);
 
 /* ---- models: gten::Model::logits (src/gten/abc.h:25) and greedy_sample ------ */
 #define NC_ARCH_LLAMA 0   /* src/tinyllama */
@@ -210,6 +228,13 @@ int nc_model_layer_out(void* model, int layer, int row, void* ref_bytes);
  * the prompt, then up to n_gen greedy steps with device-side argmax; stops
  * at eos.  *n_out = tokens produced. */
 int nc_model_generate(void* model, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out, int* n_out);
+/* topk_sample (src/gten/sampler.cpp:63-143) without the tokenizer and with
+ * std::mt19937(seed) in place of the random_device-seeded generator: prefill
+ * the prompt, then n_gen sampled tokens (logits, sampling and the next
+ * step's inputs on the device, no host round trip); stops at eos.
+ * *n_out = tokens produced. */
+int nc_model_generate_topk(void* model, const int32_t* prompt, int n_prompt, int n_gen, float temp, int top_k,
+                           uint32_t seed, int32_t* out, int* n_out);
 /* Split form for timing: nc_model_prefill runs the start_pos = 0 call and
  * leaves the greedy token on the device; nc_model_decode runs n_steps more
  * calls (no host round trip between steps) and appends the tokens. */

@@ -133,6 +133,11 @@ def lib():
         "nc_model_init_synthetic": (I, [VP, U64]), "nc_model_set_weight": (I, [VP, I, I, VP, SZ]),
         "nc_model_get_weight": (I, [VP, I, I, VP, SZ]), "nc_model_logits": (I, [VP, VP, I, I, VP]),
         "nc_model_load_gten": (I, [VP, C.c_char_p]),
+        "nc_model_generate_topk": (I, [VP, VP, I, I, C.c_float, I, C.c_uint32, VP, C.POINTER(I)]),
+        "nc_rng_seed": (I, [C.c_uint32, VP]),
+        "nc_sample_topk": (I, [VP, I, C.c_float, I, VP, VP, VP, VP]),
+        "nc_exp": (I, [VP, VP, C.c_int64, VP]),
+        "nc_exp_host": (C.c_double, [C.c_double]),
         "nc_model_layer_out": (I, [VP, I, I, VP]), "nc_model_generate": (I, [VP, VP, I, I, VP, C.POINTER(I)]),
         "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
         "nc_model_profile_begin": (I, [VP, I]),
@@ -239,6 +244,16 @@ class Model:
         out = np.zeros(n_gen, np.int32)
         n = C.c_int()
         check(lib().nc_model_generate(self.h, _ptr(p), len(p), n_gen, _ptr(out), C.byref(n)), "generate")
+        return out[: n.value]
+
+    def generate_topk(self, prompt, n_gen, temp, top_k, seed):
+        """topk_sample with std::mt19937(seed): up to n_gen sampled tokens."""
+        import numpy as np
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, np.int32)
+        n = C.c_int()
+        check(lib().nc_model_generate_topk(self.h, _ptr(p), len(p), n_gen, temp, top_k, seed, _ptr(out), C.byref(n)),
+              "generate_topk")
         return out[: n.value]
 
     def prefill(self, prompt):

@@ -76,4 +76,9 @@ bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi);
 int decode_matvec(const DmvArgs& a, int wdtype, int pro, int epi, hipStream_t st, hipEvent_t ev0 = nullptr,
                   hipEvent_t ev1 = nullptr);
 
+// After a token was written to tokens[*pos_out] by another kernel: that
+// token's embedding and RoPE rows, as the argmax epilogue prepares them (the
+// emb_* and rope_* fields, nb of the embedding rows, tokens, pos_out).
+int next_inputs_launch(const DmvArgs& a, int wdtype, hipStream_t st);
+
 }  // namespace nc

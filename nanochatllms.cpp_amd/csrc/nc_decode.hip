@@ -711,4 +711,28 @@ int decode_matvec(const DmvArgs& A, int wdtype, int pro, int epi, hipStream_t st
     return wdtype == NC_Q4 ? dmv_dispatch<Q4>(A, pro, epi, st, ev0, ev1) : dmv_dispatch<Q8>(A, pro, epi, st, ev0, ev1);
 }
 
+// The next step's inputs for a token another kernel chose: the position is
+// read from A.pos_out (already advanced to the token's position p), the
+// token from A.tokens[p]; the embedding and RoPE rows are those the argmax
+// epilogue prepares for position p.
+template <int WT, int NCH>
+__global__ __launch_bounds__(kDmvThreads) void k_next_inputs(DmvArgs A)
+{
+    const int p = load_pos(A.pos_out);
+    next_step_inputs<WT, NCH>(A, A.tokens[p], p - 1);
+}
+
+int next_inputs_launch(const DmvArgs& A, int wdtype, hipStream_t st)
+{
+    const int K = A.nb * 32;
+    if ((wdtype != NC_Q4 && wdtype != NC_Q8) || K % 32 || K > 2 * kDmvThreads * 8 || !A.pos_out || !A.tokens ||
+        !A.emb_codes)
+        return fail(NC_ERR_ARG, "next inputs: unsupported (dtype %d, %d values)", wdtype, K);
+    const bool two = K > kDmvThreads * 8;
+    auto kern = wdtype == NC_Q4 ? (two ? k_next_inputs<Q4, 2> : k_next_inputs<Q4, 1>)
+                                : (two ? k_next_inputs<Q8, 2> : k_next_inputs<Q8, 1>);
+    hipLaunchKernelGGL(kern, dim3(1), dim3(kDmvThreads), 0, st, A);
+    return launch_status("k_next_inputs");
+}
+
 }  // namespace nc

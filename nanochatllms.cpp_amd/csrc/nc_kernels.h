@@ -56,6 +56,14 @@ int argmax_launch(const float* x, int n, int32_t* out, hipStream_t st);
 int argmax_advance_launch(const float* x, int n, int32_t* tokens, int* dpos, unsigned long long* scratch,
                           hipStream_t st);
 
+// One top-k / temperature sampling step (gten/sampler.cpp:90-127) of the
+// logits row x[n] with the mt19937 state rng (625 words, updated): the token
+// goes to tokens[pos + 1], pos being *dpos (then advanced by one) when dpos
+// is given.  probs (optional): the n normalized weights.
+int sample_topk_launch(const float* logits, int n, float temp, int top_k, uint32_t* rng, int32_t* tokens, int* dpos,
+                       int pos, double* probs, hipStream_t st);
+void mt_seed_host(uint32_t seed, uint32_t* state);
+
 int ew_launch(int op, int adt, const uint8_t* a, int a_pitch, const uint8_t* b, int b_pitch, const uint16_t* bias,
               float s, uint8_t* out, int out_pitch, int cols, int rows, hipStream_t st);
 

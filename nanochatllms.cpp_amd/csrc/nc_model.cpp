@@ -100,6 +100,13 @@ public:
     // the op-by-op path.
     bool fused = false;
     unsigned long long* am_scratch = nullptr;  // zeroed argmax scratch of the greedy step
+    // Top-k sampling: the lm head writes logits only (sample_head), and the
+    // sampler draws from the device-held mt19937 state rng (625 words).
+    bool sample_head = false;
+    uint32_t* rng = nullptr;
+    hipGraphExec_t sample_graph = nullptr;
+    float sample_temp = 0.0f;
+    int sample_k = 0;
 
     // Matvec launch timing: a start/end event pair recorded on the model's
     // stream around every matvec launch while profiling is on.
@@ -114,6 +121,7 @@ public:
     ~Decoder()
     {
         if (step_graph) (void)hipGraphExecDestroy(step_graph);
+        if (sample_graph) (void)hipGraphExecDestroy(sample_graph);
         for (hipEvent_t e : prof.ev) (void)hipEventDestroy(e);
         for (void* p : allocs) (void)hipFree(p);
     }
@@ -801,23 +809,33 @@ public:
         a.norm_w = norm_w;
         a.post_scale = minicpm ? 1.0f / 9 : 1.0f;  // minicpm.cpp:104-105
         a.raw = logits;
+        // a sampling step: logits only, the sampler picks the token
+        if (sample_head) return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_RAW, NC_PROF_LM_HEAD);
         a.tokens = tokens;
         a.pos_out = dpos;
         a.amax = am_scratch;
-        if (dpos) {
-            // the next step's embedding and RoPE rows, from the greedy token
-            a.emb_codes = (const uint32_t*)emb.data;
-            a.emb_deltas = (const uint16_t*)emb.deltas;
-            a.emb_scale = minicpm ? 12.0f : 1.0f;
-            a.emb_cur = cur_x0;
-            a.emb_rows = x0;
-            a.emb_pitch = pd;
-            a.max_ctx = cfg.max_ctx;
-            a.rope_table = rope;
-            a.rope_cur = cur_rope;
-            a.rope_half = d_half;
-        }
+        // the next step's embedding and RoPE rows, from the greedy token
+        if (dpos) next_input_fields(&a, dpos);
         return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_ARGMAX, NC_PROF_LM_HEAD);
+    }
+
+    // The fields of the next step's embedding and RoPE rows (the greedy
+    // lm head's epilogue, or k_next_inputs after a sampler).
+    void next_input_fields(DmvArgs* a, int* dpos)
+    {
+        a->nb = d / 32;
+        a->tokens = tokens;
+        a->pos_out = dpos;
+        a->emb_codes = (const uint32_t*)emb.data;
+        a->emb_deltas = (const uint16_t*)emb.deltas;
+        a->emb_scale = cfg.arch == NC_ARCH_MINICPM ? 12.0f : 1.0f;
+        a->emb_cur = cur_x0;
+        a->emb_rows = x0;
+        a->emb_pitch = pitch(d);
+        a->max_ctx = cfg.max_ctx;
+        a->rope_table = rope;
+        a->rope_cur = cur_rope;
+        a->rope_half = d_half;
     }
 
     // One decode step as a HIP graph: forward at the device-held position,
@@ -917,6 +935,99 @@ public:
             const int n = n_cur + 1;
             if ((s = forward(n - 1, n))) return s;
             if (!fused && (s = argmax_launch(logits, cfg.n_vocab, tokens + n, st))) return s;
+            n_cur = n;
+        }
+        return NC_OK;
+    }
+
+    // One sampling step after the logits of position pos: the sampler writes
+    // tokens[pos + 1] (pos from the device when dpos is given, which it then
+    // advances) and, for the fused step, the next step's input rows.
+    int sample_after(float temp, int k, int* dpos, int pos)
+    {
+        int s = sample_topk_launch(logits, cfg.n_vocab, temp, k, rng, tokens, dpos, pos, nullptr, st);
+        if (s || !fused || !dpos) return s;
+        DmvArgs a;
+        next_input_fields(&a, dpos);
+        return next_inputs_launch(a, cfg.wdtype, st);
+    }
+
+    // A decode step that samples instead of taking the greedy token, as a
+    // HIP graph (temp and k are baked in).
+    int capture_sample_graph(float temp, int k)
+    {
+        if (sample_graph) {
+            (void)hipGraphExecDestroy(sample_graph);
+            sample_graph = nullptr;
+        }
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "capture: sync");
+        if ((e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+            return hip_fail(e, "hipStreamBeginCapture");
+        const bool was_on = prof.on;
+        prof.on = false;
+        sample_head = true;
+        int s = forward(0, 0, step_pos);
+        sample_head = false;
+        if (!s) s = sample_after(temp, k, step_pos, 0);
+        prof.on = was_on;
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(st, &g);
+        if (s) {
+            if (g) (void)hipGraphDestroy(g);
+            return s;
+        }
+        if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+        e = hipGraphInstantiate(&sample_graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+        sample_temp = temp;
+        sample_k = k;
+        return NC_OK;
+    }
+
+    // topk_sample (gten/sampler.cpp:63-143) with std::mt19937(seed): the
+    // prompt's logits, then n_gen sampled tokens, each step's logits on the
+    // device.  top_k and temp are clamped as the reference clamps them.
+    int generate_topk(const int32_t* prompt, int np, int n_gen, float temp, int top_k, uint32_t seed)
+    {
+        const int k = 1000 < top_k ? 1000 : top_k;
+        const float t = 2.0f < temp ? 2.0f : temp;
+        NC_CHECK_ARG(prompt && np > 0 && n_gen > 0 && np + n_gen - 1 <= cfg.max_ctx,
+                     "generate_topk: %d prompt + %d tokens, max_ctx %d", np, n_gen, cfg.max_ctx);
+        NC_CHECK_ARG(k >= 1 && k <= cfg.n_vocab && t > 0.0f, "generate_topk: top_k %d, temperature %g", top_k,
+                     (double)temp);
+        int s;
+        if (!rng && (s = alloc_t(&rng, 625 * 4))) return s;
+        if (!step_pos && (s = alloc_t(&step_pos, 16))) return s;
+        uint32_t st0[625];
+        mt_seed_host(seed, st0);
+        hipError_t e = hipMemcpyAsync(rng, st0, sizeof(st0), hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(tokens, prompt, (size_t)np * 4, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return hip_fail(e, "generate_topk: upload");
+        if ((s = forward(0, np))) return s;
+        n_cur = np;
+        n_prompt = np;
+        const bool graph = use_graph && !prof.on;
+        const int first = np - 1;
+        if (graph && (e = hipMemcpyAsync(step_pos, &first, 4, hipMemcpyHostToDevice, st)) != hipSuccess)
+            return hip_fail(e, "generate_topk: position upload");
+        if ((s = sample_after(t, k, graph ? step_pos : nullptr, first))) return s;
+        // the uploads read host memory asynchronously: wait before it dies
+        if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "generate_topk: sync");
+        if (graph) {
+            if ((!sample_graph || sample_temp != t || sample_k != k) && (s = capture_sample_graph(t, k))) return s;
+            for (int i = 1; i < n_gen; i++)
+                if ((e = hipGraphLaunch(sample_graph, st)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+            n_cur += n_gen - 1;
+            return NC_OK;
+        }
+        for (int i = 1; i < n_gen; i++) {
+            const int n = n_cur + 1;
+            sample_head = true;
+            s = forward(n - 1, n);
+            sample_head = false;
+            if (s || (s = sample_after(t, k, nullptr, n - 1))) return s;
             n_cur = n;
         }
         return NC_OK;
@@ -1053,6 +1164,16 @@ int nc_model_generate(void* model, const int32_t* prompt, int n_prompt, int n_ge
                  m->cfg.max_ctx);
     int s = m->prefill(prompt, n_prompt);
     if (!s) s = m->decode(n_gen - 1);
+    if (!s) s = m->fetch_generated(out, n_gen, n_out);
+    return s;
+}
+
+int nc_model_generate_topk(void* model, const int32_t* prompt, int n_prompt, int n_gen, float temp, int top_k,
+                           uint32_t seed, int32_t* out, int* n_out)
+{
+    NC_CHECK_ARG(model && out && n_out, "model_generate_topk: bad arguments");
+    auto* m = static_cast<Decoder*>(model);
+    int s = m->generate_topk(prompt, n_prompt, n_gen, temp, top_k, seed);
     if (!s) s = m->fetch_generated(out, n_gen, n_out);
     return s;
 }

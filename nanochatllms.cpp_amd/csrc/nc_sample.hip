@@ -1,0 +1,422 @@
+// nc_sample.hip -- top-k / temperature sampling of a logits row on the
+// device, with the reference's results (gten/sampler.cpp:63-143) and its
+// random source made reproducible: std::mt19937 seeded with a given value
+// instead of std::random_device (sampler.cpp:70-71).
+//
+// One sampling step of the reference, as libstdc++ runs its calls:
+//   1. pairs (logit / temp in double, index); std::partial_sort of the first
+//      k = min(top_k, 1000) by value, descending -- a heap select;
+//   2. e_j = std::exp(v_j) (glibc's double exp) and sum_exp = e_0 + e_1 + ...
+//      in that descending order; p_j = e_j / sum_exp;
+//   3. std::discrete_distribution over the n-entry weight vector (p_j at
+//      index i_j, zeros elsewhere): s = 0.0 + w_0 + ... + w_{n-1} in index
+//      order, q_i = w_i / s, cumulative c_i = q_0 + ... + q_i with c_{n-1}
+//      set to 1;
+//   4. u = generate_canonical<double, 53>: two mt19937 outputs,
+//      (u1 + u2 * 2^32) rounded to double, times 2^-64 (a result of 1 becomes
+//      the double below 1); the token is lower_bound(c, u).
+//
+// On the device, one workgroup of 1024 threads:
+//   * candidates: a systematic sample of 1024 logits is sorted; its rank
+//     giving about 1.5 k + 256 elements sets a threshold, and every logit at
+//     or above it is gathered in LDS (up to 4096) and bitonic-sorted.  The
+//     top k of that sort are the heap select's k when the k-th value is not
+//     tied with the next; the ordering of the logits equals that of
+//     logit / temp (distinct floats stay distinct doubles), with -0 == +0.
+//   * exact fallback: when the k-th value is tied with the (k+1)-th (the heap
+//     order then decides which tied indices stay), a logit is NaN, or the
+//     threshold gathers fewer than k or more than 4096, thread 0 replays the
+//     heap select (make_heap, pop_heap, the sift order of libstdc++) over
+//     every logit, staged through LDS; rare and slower (~1 ms).
+//   * the three sums are the reference's sequential chains, run by thread 0
+//     over LDS; exp, the divisions and the sorts are parallel.  Weights are
+//     nonzero only at the k indices, so the n-term sums and the cumulative
+//     table reduce to the k entries in index order (adding +0.0 changes
+//     nothing); lower_bound runs libstdc++'s binary search over the implied
+//     n-entry table.  A NaN weight (from NaN logits, or an exp overflow
+//     giving inf / inf) makes the sum NaN and every entry NaN: the table is
+//     then NaN up to the final 1.
+#include <hip/hip_runtime.h>
+
+#include "nc_device.h"
+#include "nc_exp64.h"
+#include "nc_kernels.h"
+
+namespace nc {
+
+constexpr int kSmThreads = 1024;
+constexpr int kSmCap = 4096;      // candidates sorted in LDS
+constexpr int kSmSample = 1024;   // threshold sample size
+constexpr int kSmStage = 8192;    // logits per LDS stage of the fallback
+
+// ---- std::mt19937 (state: 624 words, then the index of the next word) ----
+
+void mt_seed_host(uint32_t seed, uint32_t* st)
+{
+    st[0] = seed;
+    for (uint32_t i = 1; i < 624; i++) st[i] = 1812433253u * (st[i - 1] ^ (st[i - 1] >> 30)) + i;
+    st[624] = 624;
+}
+
+__device__ uint32_t mt_next(uint32_t* mt)
+{
+    if (mt[624] >= 624) {
+        for (int i = 0; i < 624; i++) {
+            const uint32_t y = (mt[i] & 0x80000000u) | (mt[i + 1 < 624 ? i + 1 : 0] & 0x7fffffffu);
+            mt[i] = mt[i + 397 < 624 ? i + 397 : i - 227] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+        }
+        mt[624] = 0;
+    }
+    uint32_t z = mt[mt[624]++];
+    z ^= z >> 11;
+    z ^= (z << 7) & 0x9d2c5680u;
+    z ^= (z << 15) & 0xefc60000u;
+    z ^= z >> 18;
+    return z;
+}
+
+// ---- ordering keys -------------------------------------------------------
+
+// Unsigned key with the float order; -0 and +0 share a key.  Finite and
+// infinite values map above 0x007fffff, so 0 pads below all of them.
+__device__ __forceinline__ uint32_t fkey(float x)
+{
+    uint32_t b = __float_as_uint(x);
+    if (b == 0x80000000u) b = 0;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float fkey_value(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? k ^ 0x80000000u : ~k); }
+
+// Bitonic sort of P (a power of two) entries in LDS, descending or ascending.
+template <bool DESC, typename T>
+__device__ void bitonic(T* a, int P)
+{
+    for (int size = 2; size <= P; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < P / 2; t += kSmThreads) {
+                const int i = 2 * t - (t & (stride - 1)), j = i + stride;
+                const bool up = (i & size) == 0;
+                const T x = a[i], y = a[j];
+                if (DESC ? (up ? x < y : x > y) : (up ? x > y : x < y)) {
+                    a[i] = y;
+                    a[j] = x;
+                }
+            }
+            lds_barrier();
+        }
+}
+
+__device__ __forceinline__ int pow2_at_least(int n)
+{
+    int p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+// ---- libstdc++'s heap over (value, index), ordered by value descending ----
+// (std::partial_sort's comparator a.first > b.first: the heap top is the
+// smallest kept value).
+
+__device__ void heap_push(float* hv, int* hi, int hole, int top, float v, int ix)
+{
+    int parent = (hole - 1) / 2;
+    while (hole > top && hv[parent] > v) {
+        hv[hole] = hv[parent];
+        hi[hole] = hi[parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    hv[hole] = v;
+    hi[hole] = ix;
+}
+
+__device__ void heap_adjust(float* hv, int* hi, int hole, int len, float v, int ix)
+{
+    const int top = hole;
+    int child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (hv[child] > hv[child - 1]) child--;
+        hv[hole] = hv[child];
+        hi[hole] = hi[child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        hv[hole] = hv[child - 1];
+        hi[hole] = hi[child - 1];
+        hole = child - 1;
+    }
+    heap_push(hv, hi, hole, top, v, ix);
+}
+
+struct SampleArgs {
+    const float* logits;
+    int n;
+    int k;          // min(top_k, 1000), 1 <= k <= n
+    double temp;    // min(temp, 2.0f), > 0
+    uint32_t* rng;  // 625 words, read and written back
+    int32_t* tokens;  // the token goes to tokens[pos + 1]
+    int* dpos;        // device position, advanced by one (or null: pos)
+    int pos;
+    double* probs;    // optional: the n normalized weights
+};
+
+__global__ __launch_bounds__(kSmThreads) void k_sample_topk(SampleArgs A)
+{
+    // cand: candidate (key << 32 | index); later the fallback's logit stage,
+    // then the index-ordered weights and cumulative table
+    __shared__ union {
+        uint64_t cand[kSmCap];
+        float stage[kSmStage];
+        struct {
+            double c[1024];
+            int idx[1024];
+        } t;
+    } U;
+    __shared__ union {
+        uint32_t samp[kSmSample];
+        struct {
+            float hv[1024];
+            int hi[1024];
+        } h;
+        uint64_t byidx[1024];  // (index << 32 | rank in descending order)
+    } V;
+    __shared__ double ev[1024];  // e_j, then p_j, in descending order
+    __shared__ uint32_t mt[625];
+    __shared__ int s_cnt, s_nan;
+    __shared__ double s_sum;
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int n = A.n, k = A.k;
+    const int pos = A.dpos ? load_pos(A.dpos) : A.pos;
+    for (int i = tid; i < 625; i += kSmThreads) mt[i] = A.rng[i];
+    if (A.probs)
+        for (int i = tid; i < n; i += kSmThreads) A.probs[i] = 0.0;
+    if (tid == 0) {
+        s_cnt = 0;
+        s_nan = 0;
+    }
+
+    // threshold: the sample's entry at rank ~(1.5 k + 256) n / 1024
+    uint32_t thr = 0;
+    if (n > kSmCap) {
+        V.samp[tid] = fkey(A.logits[(long long)tid * n / kSmSample]);
+        lds_barrier();
+        bitonic<true>(V.samp, kSmSample);
+        const long long r = ((long long)(3 * k / 2 + 256) * kSmSample) / n;
+        thr = V.samp[r < kSmSample - 1 ? r : kSmSample - 1];
+    }
+    __syncthreads();  // also orders the probs zero fill before later stores
+
+    // gather every logit with key >= thr (wave-compacted)
+    for (int base = 0; base < n; base += 4 * kSmThreads) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = base + u * kSmThreads + tid;
+            x[u] = i < n ? A.logits[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = base + u * kSmThreads + tid;
+            const bool in = i < n;
+            const bool nan = in && x[u] != x[u];
+            if (nan) s_nan = 1;
+            const uint32_t key = fkey(x[u]);
+            const bool take = in && !nan && key >= thr;
+            const unsigned long long m = __ballot(take);
+            const int cnt = __popcll(m);
+            int wbase = 0;
+            if (lane == 0 && cnt) wbase = atomicAdd(&s_cnt, cnt);
+            wbase = __shfl(wbase, 0);
+            const int at = wbase + __popcll(m & ((1ull << lane) - 1ull));
+            if (take && at < kSmCap) U.cand[at] = ((uint64_t)key << 32) | (uint32_t)i;
+        }
+    }
+    lds_barrier();
+    int C = s_cnt;
+    bool fallback = s_nan || C < k || C > kSmCap;
+    if (!fallback) {
+        const int P = pow2_at_least(C);
+        for (int i = C + tid; i < P; i += kSmThreads) U.cand[i] = 0;
+        lds_barrier();
+        bitonic<true>(U.cand, P);
+        // a tie between the k-th and (k+1)-th value: the heap order decides
+        if (C > k && (uint32_t)(U.cand[k - 1] >> 32) == (uint32_t)(U.cand[k] >> 32)) fallback = true;
+    }
+    if (fallback) {
+        // std::partial_sort's heap select, replayed by thread 0
+        for (int j = tid; j < k; j += kSmThreads) {
+            V.h.hv[j] = A.logits[j];
+            V.h.hi[j] = j;
+        }
+        lds_barrier();
+        if (tid == 0 && k >= 2)
+            for (int parent = (k - 2) / 2;; parent--) {
+                heap_adjust(V.h.hv, V.h.hi, parent, k, V.h.hv[parent], V.h.hi[parent]);
+                if (parent == 0) break;
+            }
+        for (int base = k; base < n; base += kSmStage) {
+            const int m = min(kSmStage, n - base);
+            lds_barrier();
+            for (int j = tid; j < m; j += kSmThreads) U.stage[j] = A.logits[base + j];
+            lds_barrier();
+            if (tid == 0)
+                for (int j = 0; j < m; j++) {
+                    const float v = U.stage[j];
+                    if (v > V.h.hv[0]) heap_adjust(V.h.hv, V.h.hi, 0, k, v, base + j);
+                }
+        }
+        lds_barrier();
+        // the kept k, sorted by value (their order among equal values does
+        // not change any sum)
+        const int P = pow2_at_least(k);
+        for (int j = tid; j < P; j += kSmThreads)
+            U.cand[j] = j < k ? ((uint64_t)fkey(V.h.hv[j]) << 32) | (uint32_t)V.h.hi[j] : 0ull;
+        lds_barrier();
+        bitonic<true>(U.cand, P);
+        C = k;
+    }
+
+    // e_j = exp(v_j / temp) in descending order; sum_exp in that order
+    int my_idx = 0;
+    if (tid < k) {
+        const uint64_t c = U.cand[tid];
+        my_idx = (int)(uint32_t)c;
+        const float x = s_nan ? A.logits[my_idx] : fkey_value((uint32_t)(c >> 32));
+        ev[tid] = exp_ref((double)x / A.temp);
+    }
+    lds_barrier();
+    if (tid == 0) {
+        double s = 0;
+        for (int j = 0; j < k; j++) s += ev[j];
+        s_sum = s;
+    }
+    lds_barrier();
+    if (tid < k) ev[tid] = ev[tid] / s_sum;
+    const int P2 = pow2_at_least(k);
+    if (tid < P2) V.byidx[tid] = tid < k ? ((uint64_t)(uint32_t)my_idx << 32) | (uint32_t)tid : ~0ull;
+    lds_barrier();
+    bitonic<false>(V.byidx, P2);
+    // index order: weights p, their sum, q = p / sum, the cumulative table
+    if (tid < k) {
+        const uint64_t b = V.byidx[tid];
+        U.t.idx[tid] = (int)(b >> 32);
+        U.t.c[tid] = ev[(uint32_t)b];
+    }
+    lds_barrier();
+    if (tid == 0) {
+        double s = 0.0;
+        for (int j = 0; j < k; j++) s += U.t.c[j];
+        s_sum = s;
+    }
+    lds_barrier();
+    // a NaN weight makes the sum NaN, and then every weight, the zeros
+    // included (0 / NaN), and every cumulative entry but the last
+    const bool nan_sum = s_sum != s_sum;
+    if (tid < k) {
+        const double q = U.t.c[tid] / s_sum;
+        U.t.c[tid] = q;
+        if (A.probs && !nan_sum) A.probs[U.t.idx[tid]] = q;
+    }
+    if (A.probs && nan_sum)
+        for (int i = tid; i < n; i += kSmThreads) A.probs[i] = s_sum;
+    lds_barrier();
+    if (tid == 0) {
+        double c = U.t.c[0];
+        for (int j = 1; j < k; j++) {
+            c = c + U.t.c[j];
+            U.t.c[j] = c;
+        }
+        if (U.t.idx[k - 1] == n - 1) U.t.c[k - 1] = 1.0;
+        // generate_canonical<double, 53>
+        double sum = 0.0, tmp = 1.0;
+        for (int r = 0; r < 2; r++) {
+            sum += (double)mt_next(mt) * tmp;
+            tmp *= 4294967296.0;
+        }
+        double u = sum / tmp;
+        if (u >= 1.0) u = 0x1.fffffffffffffp-1;
+        // lower_bound over the n-entry cumulative table
+        int first = 0, len = n;
+        while (len > 0) {
+            const int half = len >> 1, mid = first + half;
+            double cm;
+            if (mid == n - 1) {
+                cm = 1.0;
+            } else if (nan_sum) {
+                cm = s_sum;
+            } else {
+                int lo = 0, hi = k;  // number of kept indices <= mid
+                while (lo < hi) {
+                    const int h = (lo + hi) >> 1;
+                    if (U.t.idx[h] <= mid) lo = h + 1;
+                    else hi = h;
+                }
+                cm = lo ? U.t.c[lo - 1] : 0.0;
+            }
+            if (cm < u) {
+                first = mid + 1;
+                len = len - half - 1;
+            } else {
+                len = half;
+            }
+        }
+        A.tokens[pos + 1] = first;
+        if (A.dpos) A.dpos[0] = pos + 1;
+    }
+    lds_barrier();
+    for (int i = tid; i < 625; i += kSmThreads) A.rng[i] = mt[i];
+}
+
+int sample_topk_launch(const float* logits, int n, float temp, int top_k, uint32_t* rng, int32_t* tokens, int* dpos,
+                       int pos, double* probs, hipStream_t st)
+{
+    // sampler.cpp:66-67: std::min(top_k, 1000), std::min(temp, 2.0f)
+    const int k = 1000 < top_k ? 1000 : top_k;
+    const float t = 2.0f < temp ? 2.0f : temp;
+    NC_CHECK_ARG(logits && rng && tokens && n >= 2, "sample_topk: bad arguments (n = %d)", n);
+    NC_CHECK_ARG(k >= 1 && k <= n, "sample_topk: top_k %d for %d logits", top_k, n);
+    NC_CHECK_ARG(t > 0.0f, "sample_topk: temperature %g", (double)temp);
+    SampleArgs a{logits, n, k, (double)t, rng, tokens, dpos, pos, probs};
+    hipLaunchKernelGGL(k_sample_topk, dim3(1), dim3(kSmThreads), 0, st, a);
+    return launch_status("k_sample_topk");
+}
+
+__global__ void k_exp(const double* __restrict__ x, double* __restrict__ y, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = exp_ref(x[i]);
+}
+
+}  // namespace nc
+
+using namespace nc;
+
+extern "C" {
+
+int nc_rng_seed(uint32_t seed, uint32_t* state)
+{
+    NC_CHECK_ARG(state, "rng_seed: null state");
+    mt_seed_host(seed, state);
+    return NC_OK;
+}
+
+int nc_sample_topk(const float* logits, int n_vocab, float temp, int top_k, uint32_t* rng_state, int32_t* token,
+                   double* probs, void* stream)
+{
+    return sample_topk_launch(logits, n_vocab, temp, top_k, rng_state, token, nullptr, -1, probs, stream_of(stream));
+}
+
+double nc_exp_host(double x) { return exp_ref(x); }
+
+int nc_exp(const double* x, double* y, int64_t n, void* stream)
+{
+    NC_CHECK_ARG(x && y && n >= 0, "exp: bad arguments");
+    if (!n) return NC_OK;
+    hipLaunchKernelGGL(k_exp, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream_of(stream), x, y, n);
+    return launch_status("k_exp");
+}
+
+}  // extern "C"

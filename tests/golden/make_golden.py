@@ -10,6 +10,7 @@ Small models of every architecture are recorded the same way, with their
 full logits.
 
     python tests/golden/make_golden.py [workload ...]
+    python tests/golden/make_golden.py --topk [workload ...]   (sampled streams)
 """
 import hashlib
 import json
@@ -60,7 +61,39 @@ def record(name, w, full_logits=False):
     print(name, n, "tokens", fx["seconds"], "s", flush=True)
 
 
+# top-k / temperature runs: (temp, top_k, seed); temp 2.5 is clamped to 2.0
+# and top_k 5000 to 1000 as the reference clamps them
+TOPK_SMALL = [(0.8, 40, 7), (1.0, 1000, 11), (2.5, 5, 99), (0.6, 5000, 3)]
+TOPK_FULL = [(0.8, 40, 7), (1.0, 1000, 11)]
+TOPK_FULL_WORKLOADS = ["tinyllama-q4", "minicpm-q4"]
+
+
+def record_topk(name, w, runs, n_gen):
+    """topk_sample's loop with std::mt19937(seed), per run."""
+    ref = OL.Reference()
+    cfg = config_of(w)
+    prompt = prompt_of(w)
+    out = np.zeros(n_gen, np.int32)
+    recs = []
+    t0 = time.time()
+    for temp, k, seed in runs:
+        m = ref.model_create(cfg, w["seed"])
+        n = ref.generate_topk(m, OL.ptr(prompt), len(prompt), n_gen, temp, k, seed, OL.ptr(out))
+        ref.model_free(m)
+        recs.append(dict(temp=temp, top_k=k, seed=seed, n_gen=n_gen, tokens=out[:n].tolist()))
+    with open(os.path.join(HERE, f"{name}.topk.json"), "w") as f:
+        json.dump(dict(workload=name, prompt=prompt.tolist(), runs=recs), f)
+    print(name, "top-k", [len(r["tokens"]) for r in recs], round(time.time() - t0, 1), "s", flush=True)
+
+
 def main(argv):
+    if argv[:1] == ["--topk"]:
+        for name in argv[1:] or list(SMALL) + TOPK_FULL_WORKLOADS:
+            if name in SMALL:
+                record_topk(name, SMALL[name], TOPK_SMALL, SMALL[name]["gen"])
+            else:
+                record_topk(name, nc.WORKLOADS[name], TOPK_FULL, 64)
+        return
     names = argv or list(SMALL) + list(nc.WORKLOADS)
     for name in names:
         if name in SMALL:

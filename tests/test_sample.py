@@ -33,13 +33,19 @@ def logits_case(kind, n, seed):
         x[rng.integers(n)] = 40.0
     elif kind == "overflow":  # exp(x / temp) overflows: infinite sum, NaN weights
         x = rng.normal(0.0, 3.0, n)
-        x[: max(1, n // 100)] = 400.0
+        x[: max(1, n // 100)] = 1500.0
+    elif kind == "overflow_late":  # as above, the overflowing logits last: token 0 is drawn, unkept
+        x = rng.normal(0.0, 3.0, n)
+        x[-max(1, n // 100):] = 1500.0
+    elif kind == "nan":  # a NaN logit never compares greater: the heap order keeps or drops it
+        x = rng.normal(0.0, 3.0, n)
+        x[rng.integers(n)] = np.nan
     else:
         raise ValueError(kind)
     return np.ascontiguousarray(x, np.float32)
 
 
-KINDS = ["normal", "ties", "flat", "two_level", "signed_zero", "peaked", "overflow"]
+KINDS = ["normal", "ties", "flat", "two_level", "signed_zero", "peaked", "overflow", "overflow_late", "nan"]
 
 
 def case_seed(kind, n, k):
@@ -113,3 +119,52 @@ def test_tie_cases_exercise_the_heap_order(reference):
             stable = set(np.argsort(-x.astype(np.float64), kind="stable")[:k].tolist())
             differs += set(np.nonzero(pr)[0].tolist()) != stable
     assert differs > 0
+
+
+def test_kernel_exp_equals_host_libm(nc, oracle):
+    """The kernels' double exp (evaluated on the host from the same source)
+    equals the host glibc exp -- std::exp on double, the reference's -- on
+    10^8 inputs: the full bit-pattern range, [-750, 710] and [-40, 40]."""
+    fn = OL.C.cast(nc.lib().nc_exp_host, OL.C.c_void_p).value
+    first = OL.C.c_double()
+    bad = oracle.check_exp_fn(fn, 20241202, 100_000_000, OL.C.byref(first))
+    assert bad == 0, f"{bad} inputs differ, first x = {first.value!r}"
+    for x in [0.0, -0.0, 1e-300, -1e-300, 2.0**-54, 709.782712893384, 709.7827128933841, -708.3964185322641,
+              -745.1332191019411, -745.1332191019412, 512.0, -512.0, 1024.0, float("inf"), float("-inf"),
+              float("nan")]:
+        a, b = nc.lib().nc_exp_host(x), oracle.exp(x)
+        assert np.float64(a).view(np.uint64) == np.float64(b).view(np.uint64) or (np.isnan(a) and np.isnan(b)), x
+
+
+def test_rng_seed_matches_oracle(nc, oracle):
+    for seed in (0, 5489, 0xFFFFFFFF):
+        a, b = np.zeros(625, np.uint32), np.zeros(625, np.uint32)
+        assert nc.lib().nc_rng_seed(seed, OL.ptr(a)) == 0
+        oracle.mt_seed(seed, OL.ptr(b))
+        assert np.array_equal(a, b)
+
+
+def golden_topk(name):
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"{name}.topk.json")) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("name", sorted(__import__("workloads").SMALL))
+def test_oracle_topk_streams_match_reference_fixtures(oracle, name):
+    """The oracle's model with the oracle's sampler gives the reference's
+    sampled streams (tests/golden/*.topk.json, from the reference harness)."""
+    from workloads import SMALL, config_of, prompt_of
+    w = SMALL[name]
+    g = golden_topk(name)
+    cfg = config_of(w)
+    prompt = prompt_of(w)
+    assert prompt.tolist() == g["prompt"]
+    for r in g["runs"]:
+        m = oracle.model_create(cfg, w["seed"])
+        out = np.zeros(r["n_gen"], np.int32)
+        n = oracle.generate_topk(m, OL.ptr(prompt), len(prompt), r["n_gen"], r["temp"], r["top_k"], r["seed"],
+                                 OL.ptr(out))
+        oracle.model_free(m)
+        assert out[:n].tolist() == r["tokens"], r
