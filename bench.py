@@ -137,6 +137,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel directly instead of replaying "
                     "the captured decode-step graph (for profilers that do not follow graph launches)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
+    ap.add_argument("--no-topk", action="store_true", help="skip the sampled-decode measurement (profiler runs)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -173,6 +174,21 @@ def main():
     model.decode(args.steps)
     nc.check(L.nc_synchronize())
     dt = time.perf_counter() - t0
+    # sampled decode (top-k 40, temperature 0.8, mt19937 seed 7): the same
+    # step with the device sampler in place of the greedy pick; the rate is
+    # the difference of two calls, prompt + first token and prompt + first
+    # token + warmup + steps, after one call that captures the step graph
+    topk_tok_s = None
+    if not args.no_topk:
+        topk_args = (0.8, 40, 7)
+        model.generate_topk(prompt, 2, *topk_args)
+        t0 = time.perf_counter()
+        model.generate_topk(prompt, 1, *topk_args)
+        t_one = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        model.generate_topk(prompt, 1 + args.warmup + args.steps, *topk_args)
+        t_all = time.perf_counter() - t0
+        topk_tok_s = round((args.warmup + args.steps) / max(t_all - t_one, 1e-9), 2)
     # matvec timing: the same steps again (same positions, same tokens) with
     # direct launches, each matvec bracketed by HIP events on the model stream
     model.prefill(prompt)
@@ -223,6 +239,9 @@ def main():
                    "timed_positions": [w["prompt"] + args.warmup, w["prompt"] + args.warmup + args.steps]},
         "prefill_tok_s": round(w["prompt"] / prefill_s, 1),
         "direct_launch_tok_s": round(args.steps / dt_direct, 2),
+        "topk_decode_tok_s": topk_tok_s,
+        "topk_decode": "top_k 40, temperature 0.8, std::mt19937 seed 7; decode steps of one call (the graph "
+                       "replays with the device sampler), prompt and first token subtracted",
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": dom["kernel"], "avg_launch_us": dom["avg_launch_us"],
