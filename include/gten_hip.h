@@ -137,6 +137,32 @@ float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int* fast);
 /* Greedy pick of greedy_sample (src/gten/sampler.cpp:33-41): first index of
  * the maximum. */
 int nc_argmax(const float* x, int n, int32_t* out, void* stream);
+/* ---- tokenizers (host) ----------------------------------------------------
+ * The reference's LLamaTokenizer (src/gten/tokenizer.cpp:25-248: BPE with
+ * scores, byte fallback) and Gpt2Tokenizer (tokenizer.cpp:251-334: regex
+ * words, longest entries), with their results.  A tokenizer handle is a
+ * host object; none of these calls touch the GPU. */
+/* LLamaTokenizer(path, vocab_size, eos, prompt_prefix, prompt_suffix,
+ * tokens_prefix, tokens_suffix) (tokenizer.cpp:25-65). */
+int nc_tokenizer_load_bpe(const char* path, int vocab_size, int eos, const char* prompt_prefix,
+                          const char* prompt_suffix, const int32_t* tokens_prefix, int n_prefix,
+                          const int32_t* tokens_suffix, int n_suffix, void** tokenizer);
+/* Gpt2Tokenizer(vocab_path, n_vocab, eos) (tokenizer.cpp:251-269) with its
+ * encode prefix and suffix tokens as arguments (tokenizer.h:59-60). */
+int nc_tokenizer_load_words(const char* path, int vocab_size, int eos, const int32_t* tokens_prefix, int n_prefix,
+                            const int32_t* tokens_suffix, int n_suffix, void** tokenizer);
+/* The tokenizer nanochat.cpp builds for "tinyllama", "zephyr", "minicpm",
+ * "openelm_sm|md|lg" (src/nanochat.cpp:189-229) from its vocabulary file. */
+int nc_tokenizer_load_for_model(const char* model, const char* path, void** tokenizer);
+/* Tokenizer::encode (tokenizer.cpp:99-130, 283-334): *n_out = the token
+ * count; an error when it exceeds cap. */
+int nc_tokenizer_encode(void* tokenizer, const char* text, int32_t* out, int cap, int* n_out);
+/* Tokenizer::decode(prev_token, token) (tokenizer.cpp:77-90, 276-279): the
+ * text of one token, valid until the tokenizer is freed. */
+const char* nc_tokenizer_decode(void* tokenizer, int prev_token, int token);
+int nc_tokenizer_eos(void* tokenizer);
+int nc_tokenizer_free(void* tokenizer);
+
 /* std::mt19937(seed) as a 625-word state (624 words, then the index of the
  * next word), written to host memory `state`; the reference seeds its
  * generator from std::random_device (src/gten/sampler.cpp:70-71). */

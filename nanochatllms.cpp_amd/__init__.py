@@ -138,6 +138,13 @@ def lib():
         "nc_sample_topk": (I, [VP, I, C.c_float, I, VP, VP, VP, VP]),
         "nc_exp": (I, [VP, VP, C.c_int64, VP]),
         "nc_exp_host": (C.c_double, [C.c_double]),
+        "nc_tokenizer_load_bpe": (I, [C.c_char_p, I, I, C.c_char_p, C.c_char_p, VP, I, VP, I, C.POINTER(VP)]),
+        "nc_tokenizer_load_words": (I, [C.c_char_p, I, I, VP, I, VP, I, C.POINTER(VP)]),
+        "nc_tokenizer_load_for_model": (I, [C.c_char_p, C.c_char_p, C.POINTER(VP)]),
+        "nc_tokenizer_encode": (I, [VP, C.c_char_p, VP, I, C.POINTER(I)]),
+        "nc_tokenizer_decode": (C.c_char_p, [VP, I, I]),
+        "nc_tokenizer_eos": (I, [VP]),
+        "nc_tokenizer_free": (I, [VP]),
         "nc_model_layer_out": (I, [VP, I, I, VP]), "nc_model_generate": (I, [VP, VP, I, I, VP, C.POINTER(I)]),
         "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
         "nc_model_profile_begin": (I, [VP, I]),
@@ -169,6 +176,77 @@ def _ptr(a):
 # Launch roles of nc_model_profile_launches (NC_PROF_* in gten_hip.h).
 PROF_ROLES = {0: "qkv", 1: "o", 2: "gate_up", 3: "down", 4: "lm_head"}
 PROF_FUSED = 8
+
+
+class Tokenizer:
+    """The reference's tokenizers (gten/tokenizer.cpp) on the host.
+
+    Tokenizer.for_model("tinyllama", path) builds the one nanochat.cpp uses
+    for that model; bpe(...) / words(...) take the constructor arguments of
+    LLamaTokenizer / Gpt2Tokenizer.  encode(str) -> int32 array,
+    decode(prev, token) -> bytes (a piece may be part of a UTF-8 character).
+    """
+
+    def __init__(self, handle):
+        self.h = handle
+
+    @classmethod
+    def for_model(cls, model, path):
+        h = C.c_void_p()
+        check(lib().nc_tokenizer_load_for_model(model.encode(), os.fsencode(path), C.byref(h)), "tokenizer")
+        return cls(h)
+
+    @classmethod
+    def bpe(cls, path, vocab_size, eos, prompt_prefix="", prompt_suffix="", tokens_prefix=(), tokens_suffix=()):
+        import numpy as np
+        pre = np.ascontiguousarray(tokens_prefix, np.int32)
+        suf = np.ascontiguousarray(tokens_suffix, np.int32)
+        h = C.c_void_p()
+        check(lib().nc_tokenizer_load_bpe(os.fsencode(path), vocab_size, eos, prompt_prefix.encode(),
+                                          prompt_suffix.encode(), _ptr(pre), len(pre), _ptr(suf), len(suf),
+                                          C.byref(h)), "tokenizer")
+        return cls(h)
+
+    @classmethod
+    def words(cls, path, vocab_size, eos, tokens_prefix=(), tokens_suffix=()):
+        import numpy as np
+        pre = np.ascontiguousarray(tokens_prefix, np.int32)
+        suf = np.ascontiguousarray(tokens_suffix, np.int32)
+        h = C.c_void_p()
+        check(lib().nc_tokenizer_load_words(os.fsencode(path), vocab_size, eos, _ptr(pre), len(pre), _ptr(suf),
+                                            len(suf), C.byref(h)), "tokenizer")
+        return cls(h)
+
+    def encode(self, text):
+        import numpy as np
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        n = C.c_int()
+        cap = 2 * len(b) + 64
+        out = np.zeros(cap, np.int32)
+        st = lib().nc_tokenizer_encode(self.h, b, _ptr(out), cap, C.byref(n))
+        if st != 0 and n.value > cap:  # room for the count the first call reported
+            out = np.zeros(n.value, np.int32)
+            st = lib().nc_tokenizer_encode(self.h, b, _ptr(out), n.value, C.byref(n))
+        check(st, "encode")
+        return out[: n.value]
+
+    def decode(self, prev_token, token):
+        return lib().nc_tokenizer_decode(self.h, prev_token, token) or b""
+
+    @property
+    def eos(self):
+        return lib().nc_tokenizer_eos(self.h)
+
+    def close(self):
+        if self.h:
+            lib().nc_tokenizer_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class DeviceBuffer:

@@ -27,6 +27,7 @@
 #include <vector>
 
 #include "gten/gten.h"
+#include "gten/tokenizer.h"
 #include "minicpm/minicpm.h"
 #include "tinyllama/tinyllama.h"
 #include "zephyr/zephyr.h"
@@ -536,5 +537,50 @@ int ref_generate_topk(void* p, const int32_t* prompt, int n_prompt, int n_gen, f
     }
     return produced;
 }
+
+// The reference's tokenizers (gten/tokenizer.cpp) as nanochat.cpp builds
+// them (nanochat.cpp:189-229), behind a C interface for the tests.
+struct RefTokenizer {
+    std::unique_ptr<gten::LLamaTokenizer> llama;
+    std::unique_ptr<gten::Gpt2Tokenizer> gpt2;
+    gten::Tokenizer* t = nullptr;
+};
+
+void* ref_tok_llama_create(const char* path, int vocab_size, int eos, const char* prompt_prefix,
+                           const char* prompt_suffix, const int32_t* tokens_prefix, int n_prefix,
+                           const int32_t* tokens_suffix, int n_suffix)
+{
+    auto* r = new RefTokenizer;
+    r->llama = std::make_unique<gten::LLamaTokenizer>(
+            path, vocab_size, eos, std::string(prompt_prefix), std::string(prompt_suffix),
+            std::vector<int>(tokens_prefix, tokens_prefix + n_prefix),
+            std::vector<int>(tokens_suffix, tokens_suffix + n_suffix));
+    r->t = r->llama.get();
+    return r;
+}
+
+void* ref_tok_gpt2_create(const char* path, int vocab_size, int eos)
+{
+    auto* r = new RefTokenizer;
+    r->gpt2 = std::make_unique<gten::Gpt2Tokenizer>(std::string(path), vocab_size, eos);
+    r->t = r->gpt2.get();
+    return r;
+}
+
+// Number of tokens of Tokenizer::encode(text); the first `cap` go to out.
+int ref_tok_encode(void* p, const char* text, int32_t* out, int cap)
+{
+    std::string s(text);
+    const std::vector<int> v = static_cast<RefTokenizer*>(p)->t->encode(s);
+    for (int i = 0; i < (int)v.size() && i < cap; i++) out[i] = v[i];
+    return (int)v.size();
+}
+
+const char* ref_tok_decode(void* p, int prev_token, int token)
+{
+    return static_cast<RefTokenizer*>(p)->t->decode(prev_token, token);
+}
+
+void ref_tok_free(void* p) { delete static_cast<RefTokenizer*>(p); }
 
 }  // extern "C"

@@ -15,6 +15,8 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libgten_ref.so")
+# the reference source tree (build container only): its tokenizer vocabularies
+REFERENCE_ROOT = os.environ.get("NC_REFERENCE_ROOT", "/root/reference")
 
 I32, F16, F32, Q8, Q4 = 0, 1, 2, 3, 4
 LLAMA, ZEPHYR, MINICPM, OPENELM = 0, 1, 2, 3
@@ -150,6 +152,12 @@ class Reference(_Lib):
         self.rng_next = b("ref_rng_next", C.c_uint32, [_VP])
         self.topk_sample = b("ref_topk_sample", _I, [_VP, _VP, _I, _F, _I, _VP])
         self.generate_topk = b("ref_generate_topk", _I, [_VP, _VP, _I, _I, _F, _I, C.c_uint32, _VP])
+        self.tok_llama_create = b("ref_tok_llama_create", _VP, [C.c_char_p, _I, _I, C.c_char_p, C.c_char_p, _VP, _I,
+                                                                 _VP, _I])
+        self.tok_gpt2_create = b("ref_tok_gpt2_create", _VP, [C.c_char_p, _I, _I])
+        self.tok_encode = b("ref_tok_encode", _I, [_VP, C.c_char_p, _VP, _I])
+        self.tok_decode = b("ref_tok_decode", C.c_char_p, [_VP, _I, _I])
+        self.tok_free = b("ref_tok_free", None, [_VP])
 
     def token_embed(self, table, wdt, tokens, out, adt, d, vocab, start, n_ctx):
         self.token_embed_(table, wdt, tokens, out, adt, d, vocab, start, n_ctx)
