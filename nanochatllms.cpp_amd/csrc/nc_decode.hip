@@ -483,14 +483,13 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     constexpr int WV = WD / 4;
     constexpr int TP = ((NB + 3) & ~3) + 4;
     constexpr int IT = NB / 4;    // weight blocks per thread (64 rows)
-    constexpr int HALF = NB / 8;  // of them, the gate rows'
     static_assert(NB % 8 == 0 && IT <= kGluMaxItems, "gate|up block shape");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
     __shared__ float s_out[64];
     uint32_t* xs = lds;
-    float* T = reinterpret_cast<float*>(xs + NB * kStage);  // 32 rows x 4 lanes x TP
-    float* sq = T + 32 * 4 * TP;
+    float* T = reinterpret_cast<float*>(xs + NB * kStage);  // 64 rows (gate, then up) x 4 lanes x TP
+    float* sq = T + 64 * 4 * TP;
     const int tid = threadIdx.x;
     const int f = A.N / 2, nblk = f / 32;
 
@@ -514,33 +513,33 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     P.nb = NB;
     dmv_prologue<PRO, NCH>(P, xs, sq, ssh, [&] { load_block(b); });
 
-    // one half of the rows: terms of items [H*HALF, (H+1)*HALF), then the fold
-    auto half_pass = [&](auto hc) {
-        constexpr int H = decltype(hc)::value;
+    // the terms of all 64 rows, then the gate rows' folds (waves 0-1) and
+    // the up rows' folds (waves 2-3) side by side
+    auto pass = [&]() {
 #pragma unroll
-        for (int it = H * HALF; it < (H + 1) * HALF; it++) {
+        for (int it = 0; it < IT; it++) {
             const int j = tid + it * kDmvThreads;
             const int r = j / NB, i = j - r * NB;
             float tv[4];
             q_block_terms<WT>(xs + i * kStage, w[it], dw[it], tv);
-            float* t = T + (r - 32 * H) * 4 * TP + i;
+            float* t = T + r * 4 * TP + i;
 #pragma unroll
             for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
         }
         lds_barrier();
-        if (tid < 128) {
+        {
             const float acc = seq_sum<16>(T + tid * TP, NB);
             const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
             if ((tid & 3) == 0) {
-                s_out[32 * H + (tid >> 2)] = res;
-                if (A.raw) A.raw[(H ? f : 0) + 32 * b + (tid >> 2)] = res;
+                const int r = tid >> 2;  // 0..31 gate, 32..63 up
+                s_out[r] = res;
+                if (A.raw) A.raw[(r >= 32 ? f - 32 : 0) + 32 * b + r] = res;
             }
         }
         lds_barrier();
     };
     for (;;) {
-        half_pass(std::integral_constant<int, 0>{});
-        half_pass(std::integral_constant<int, 1>{});
+        pass();
         if (tid < 32) {
             const float gq = q8_roundtrip_lane(s_out[tid], true);
             const float gs = q8_roundtrip_lane(gq / (1.0f + expf_ref(-gq)), true);
@@ -665,7 +664,7 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
     const size_t lds0 = (size_t)A.nb * kStage * 4 + (norm ? K * 4 : 0);
     if (epi == EPI_SWIGLU) {
         const int tp = ((A.nb + 3) & ~3) + 4;
-        const size_t lds = lds0 + (size_t)32 * 4 * tp * 4;
+        const size_t lds = lds0 + (size_t)64 * 4 * tp * 4;
         // gate|up rows of 2048 (64 blocks) or 2304 (72 blocks) values
         if (A.nb == 64) {
             if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64>(A, lds, st, ev0, ev1);
