@@ -144,6 +144,88 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_f16(const uint8_t* __rest
     }
 }
 
+// F16, many activation rows (prefill): a 256-thread workgroup owns 32
+// weight rows (thread (row, lane j) as in k_matvec_f16) and runs the
+// activation rows kF16TileRows at a time, so each weight is read once per
+// tile instead of once per row.  Every (activation row, weight row, lane)
+// chain folds its lane's products over the 64-column groups in order, as the
+// reference's 8-lane fp32 dot does; the activation tile is staged in LDS
+// kF16TileGroups groups at a time.
+constexpr int kF16TileRows = 16;
+constexpr int kF16TileGroups = 8;  // 512 columns per stage
+
+__global__ __launch_bounds__(kMvThreads) void k_matvec_f16_tile(const uint8_t* __restrict__ x, int x_pitch,
+                                                               int n_xrows, const uint16_t* __restrict__ w,
+                                                               float* __restrict__ out, int out_pitch, int N, int K)
+{
+    // xs[p][gl][j][m] = x[p0 + p][64 (g0 + gl) + 8 m + j]
+    __shared__ __align__(16) float xs[kF16TileRows][kF16TileGroups][8][8];
+    const int tid = threadIdx.x;
+    const int j = tid & 7;
+    const int row = blockIdx.x * 32 + (tid >> 3);
+    const int G = K / 64;
+    const int npad = (N + 7) & ~7;
+    const int rowc = row < N ? row : N - 1;  // rows past N read a valid row and store nothing
+    const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;  // group 0
+    const size_t gstride = (size_t)npad * 8;                                         // uint4s per group
+
+    for (int p0 = 0; p0 < n_xrows; p0 += kF16TileRows) {
+        const int np = min(kF16TileRows, n_xrows - p0);
+        float acc[kF16TileRows];
+#pragma unroll
+        for (int p = 0; p < kF16TileRows; p++) acc[p] = 0.0f;
+        for (int g0 = 0; g0 < G; g0 += kF16TileGroups) {
+            const int ng = min(kF16TileGroups, G - g0);
+            // this stage's weights first, then the activation tile
+            uint4 wv4[kF16TileGroups];
+#pragma unroll
+            for (int gl = 0; gl < kF16TileGroups; gl++) wv4[gl] = wrow[(size_t)(g0 + (gl < ng ? gl : 0)) * gstride];
+            __syncthreads();  // the previous stage's tile is no longer read
+            // 8-value chunks: chunk c of row p covers columns 64 g0 + 8 c .. + 7
+            for (int q = tid; q < kF16TileRows * kF16TileGroups * 8; q += kMvThreads) {
+                const int p = q / (kF16TileGroups * 8), c = q % (kF16TileGroups * 8);
+                const int gl = c >> 3, m = c & 7;
+                float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                if (p < np && gl < ng) {
+                    const uint4 u = *reinterpret_cast<const uint4*>(x + (size_t)(p0 + p) * x_pitch +
+                                                                   ((size_t)(g0 + gl) * 64 + 8 * m) * 2);
+                    const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int t = 0; t < 8; t++) v[t] = h2f((uint16_t)(t & 1 ? h[t >> 1] >> 16 : h[t >> 1] & 0xFFFFu));
+                }
+#pragma unroll
+                for (int t = 0; t < 8; t++) xs[p][gl][t][m] = v[t];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int gl = 0; gl < kF16TileGroups; gl++) {
+                if (gl >= ng) break;
+                const uint32_t wq[4] = {wv4[gl].x, wv4[gl].y, wv4[gl].z, wv4[gl].w};
+                float wf[8];
+#pragma unroll
+                for (int m = 0; m < 8; m++) wf[m] = h2f((uint16_t)(m & 1 ? wq[m >> 1] >> 16 : wq[m >> 1] & 0xFFFFu));
+#pragma unroll
+                for (int p = 0; p < kF16TileRows; p++) {
+                    const float4 xa = *reinterpret_cast<const float4*>(&xs[p][gl][j][0]);
+                    const float4 xb = *reinterpret_cast<const float4*>(&xs[p][gl][j][4]);
+                    const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                    for (int m = 0; m < 8; m++) acc[p] = __builtin_fmaf(xv[m], wf[m], acc[p]);  // exact product
+                }
+            }
+        }
+        // lanes 0..7 of each row summed left to right
+        const int base = tid & ~7;
+#pragma unroll
+        for (int p = 0; p < kF16TileRows; p++) {
+            float sum = __shfl(acc[p], base);
+#pragma unroll
+            for (int l = 1; l < 8; l++) sum = sum + __shfl(acc[p], base + l);
+            if (j == 0 && row < N && p < np) out[(size_t)(p0 + p) * out_pitch + row] = sum;
+        }
+    }
+}
+
 // F16, one activation row (decode): a 64-thread workgroup owns 8 rows, thread
 // (row, lane j) folds lane j's chain over the 64-column groups in order
 // exactly as k_matvec_f16 does, but keeps two batches of kF16Batch weight
@@ -278,6 +360,11 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
             return launch_status("k_matvec_f16_row");
         }
         const dim3 grid((N + 31) / 32);
+        if (n_rows >= 4) {
+            NC_MV_LAUNCH(k_matvec_f16_tile, grid, 0, x, x_pitch, n_rows, (const uint16_t*)w->data, out, out_pitch, N,
+                         K);
+            return launch_status("k_matvec_f16_tile");
+        }
         NC_MV_LAUNCH(k_matvec_f16, grid, lds, x, x_pitch, n_rows, (const uint16_t*)w->data, out, out_pitch, N, K);
         return launch_status("k_matvec_f16");
     }
