@@ -26,20 +26,22 @@
 // vector-unit fold (13 fp32 operations per output and block).
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "nc_kernels.h"
 #include "nc_qdot.h"
 
 namespace nc {
 
-constexpr int kGmRows = 16;                // output rows per workgroup
 constexpr int kGmChunk = 4;                // activation blocks staged per step (double-buffered)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // NG 16-wide column groups per wavefront, NW wavefronts per workgroup (all
-// on the same 16 rows, side by side in columns); the first 64 threads stage
+// on the same rows, side by side in columns), MR groups of 4 rows (one MFMA
+// row operand each) per workgroup; the first 4 MR x kGmChunk threads stage
 // the activation blocks.
-template <int WT, int NG, int NW>
+template <int WT, int NG, int NW, int MR>
 __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
                                                       const uint32_t* __restrict__ wq,
                                                       const uint16_t* __restrict__ wd, float* __restrict__ out,
@@ -49,6 +51,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
     constexpr int WD = WT == Q4 ? 4 : 8;  // code dwords per weight block
     constexpr int kGmNg = NG;
     constexpr int kGmCols = 16 * NG * NW;  // columns per workgroup
+    constexpr int kGmRows = 4 * MR;        // rows per workgroup
     // staged activation blocks (nc_qdot.h layout): [buffer][block][row]
     __shared__ __align__(16) uint32_t xs[2][kGmChunk][kGmRows][kStage];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -57,9 +60,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
     const int c0 = blockIdx.x * kGmCols + wv * 16 * NG;
     const int nch = (nb + kGmChunk - 1) / kGmChunk;
 
-    // staging: thread t < 64 stages (row t % 16, block t / 16) of each chunk;
-    // rows past the end repeat the last row (their outputs are not stored)
-    const int srow = tid & 15, sblk = (tid >> 4) & (kGmChunk - 1);
+    // staging: thread t < kGmRows x kGmChunk stages (row t % kGmRows, block
+    // t / kGmRows) of each chunk; rows past the end repeat the last row
+    // (their outputs are not stored)
+    constexpr int kStagers = kGmRows * kGmChunk;
+    static_assert(kStagers <= 64 * NW, "every staged (row, block) needs its own thread");
+    const int srow = tid % kGmRows, sblk = (tid / kGmRows) & (kGmChunk - 1);
     const uint8_t* xrow = x + (size_t)min(r0 + srow, n_rows - 1) * x_pitch;
     auto stage_load = [&](int ch) { return load_x_block(xrow, nb, min(ch * kGmChunk + sblk, nb - 1)); };
 
@@ -81,9 +87,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
         }
     };
 
-    float acc[4][kGmNg][4];
+    float acc[MR][kGmNg][4];
 #pragma unroll
-    for (int m = 0; m < 4; m++)
+    for (int m = 0; m < MR; m++)
 #pragma unroll
         for (int n = 0; n < kGmNg; n++)
 #pragma unroll
@@ -93,9 +99,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
     uint16_t dc[kGmChunk][kGmNg];
     {
         XRaw xr{};
-        if (tid < 64) xr = stage_load(0);
+        if (tid < kStagers) xr = stage_load(0);
         w_load(0, wc, dc);
-        if (tid < 64) stage_x_block(xr, xs[0][sblk][srow]);
+        if (tid < kStagers) stage_x_block(xr, xs[0][sblk][srow]);
     }
     lds_barrier();
     for (int ch = 0; ch < nch; ch++) {
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
         uint32_t wn[kGmChunk][kGmNg][WV];
         uint16_t dn[kGmChunk][kGmNg];
         if (more) {
-            if (tid < 64) xn = stage_load(ch + 1);
+            if (tid < kStagers) xn = stage_load(ch + 1);
             w_load(ch + 1, wn, dn);
         }
 #pragma unroll
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
                 dw[n] = h2f(dc[j][n]);
             }
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
+            for (int m = 0; m < MR; m++) {
                 // activation operand: matrix row lc = 4 r' + k of row group m
                 // holds row (4m + r')'s lane-k codes in K group k only
                 const uint32_t* sa = xs[buf][j][4 * m + (lc >> 2)];
@@ -157,12 +163,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
                     for (int v = 0; v < WV; v++) wc[j][n][v] = wn[j][n][v];
                     dc[j][n] = dn[j][n];
                 }
-            if (tid < 64) stage_x_block(xn, xs[buf ^ 1][sblk][srow]);
+            if (tid < kStagers) stage_x_block(xn, xs[buf ^ 1][sblk][srow]);
         }
         lds_barrier();
     }
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
+    for (int m = 0; m < MR; m++) {
         const int row = r0 + 4 * m + lg;
 #pragma unroll
         for (int n = 0; n < kGmNg; n++) {
@@ -173,12 +179,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
     }
 }
 
-// Workgroup shape (measured on MI355X, prefill of 64 and 512 rows): one
-// wavefront per workgroup (a workgroup of four on the same rows is slower:
-// it shares the staging but waits at every chunk's barrier), and two
-// 16-wide column groups per wavefront once the product has enough
-// wavefronts to fill the CUs several times over, else one.
-constexpr int kGmWideWaves = 4096;
+// Workgroup shape (measured on MI355X, prefill of 64 and 512 rows, exact
+// results in every shape): one wavefront per workgroup (a workgroup of four
+// on the same rows is slower: it shares the staging but waits at every
+// chunk's barrier), four row groups (16 rows) per wavefront -- one or two
+// row groups are slower (7.4K, 10.9K tok/s against 11.2K for TinyLlama):
+// the weights a wavefront loads serve fewer rows -- and two 16-wide column
+// groups per wavefront for long prompts (MiniCPM, 512 rows: 12.3K against
+// 11.3K tok/s), one for short ones (TinyLlama, 64 rows: 11.2K against 9.9K).
+constexpr int kGemmWideRows = 256;
 
 int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
                hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop)
@@ -187,10 +196,8 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
     if (w->cols % 32 || w->cols <= 0 || w->rows <= 0 || n_rows <= 0)
         return fail(NC_ERR_ARG, "gemm: [%d x %d] weights, %d rows", w->rows, w->cols, n_rows);
     const int N = w->rows, nb = w->cols / 32;
-    const int rt = (n_rows + kGmRows - 1) / kGmRows;
-    const bool wide = (long long)rt * ((N + 31) / 32) >= kGmWideWaves;
-    auto go = [&](auto kern, int ng) {
-        const dim3 grid((N + 16 * ng - 1) / (16 * ng), rt);
+    auto go = [&](auto kern, int mr, int ng) {
+        const dim3 grid((N + 16 * ng - 1) / (16 * ng), (n_rows + 4 * mr - 1) / (4 * mr));
         if (ev_start)
             hipExtLaunchKernelGGL(kern, grid, dim3(64), 0, st, ev_start, ev_stop, 0, x, x_pitch, n_rows,
                                   (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
@@ -198,13 +205,14 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
             hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, x, x_pitch, n_rows, (const uint32_t*)w->data,
                                (const uint16_t*)w->deltas, out, out_pitch, N, nb);
     };
-    if (w->dtype == NC_Q4) {
-        if (wide) go(k_gemm_q<Q4, 2, 1>, 2);
-        else go(k_gemm_q<Q4, 1, 1>, 1);
-    } else {
-        if (wide) go(k_gemm_q<Q8, 2, 1>, 2);
-        else go(k_gemm_q<Q8, 1, 1>, 1);
-    }
+    const bool wide = n_rows >= kGemmWideRows;
+    auto by_type = [&](auto wt) {
+        constexpr int WT = decltype(wt)::value;
+        if (wide) go(k_gemm_q<WT, 2, 1, 4>, 4, 2);
+        else go(k_gemm_q<WT, 1, 1, 4>, 4, 1);
+    };
+    if (w->dtype == NC_Q4) by_type(std::integral_constant<int, Q4>{});
+    else by_type(std::integral_constant<int, Q8>{});
     return launch_status("k_gemm_q");
 }
 
