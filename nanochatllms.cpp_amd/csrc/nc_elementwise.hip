@@ -61,8 +61,14 @@ __global__ __launch_bounds__(1024) void k_norm(const uint8_t* __restrict__ a, in
 {
     __shared__ __align__(16) float buf[kNormMaxCols];
     __shared__ float stat[2];
+    __shared__ SsShared ssh;
     const int tid = threadIdx.x;
     const int bs = blockDim.x;
+    // a workgroup of 256 threads or more over a multiple of 256 values: the
+    // non-negative sums (rms_norm's squares, layer_norm's squared
+    // deviations) run as the workgroup-parallel restatement of the
+    // sequential loop (same result) on the first 256 threads
+    const bool block_sum = bs % kSsThreads == 0 && n % kSsThreads == 0;
     const int per = n / bs;
     const int r = blockIdx.y;
     const int seg0 = blockIdx.x * n;  // first column of this segment in the row
@@ -89,7 +95,13 @@ __global__ __launch_bounds__(1024) void k_norm(const uint8_t* __restrict__ a, in
         buf[tid + m * bs] = KIND == kRms ? x * x : x;
     }
     __syncthreads();
-    if (tid < kWave) {
+    if (KIND == kRms && block_sum) {
+        const float s1 = block_seq_sum_nonneg(buf, n, ssh);
+        if (tid == 0) {
+            stat[0] = 0.0f;
+            stat[1] = sqrtf(s1 / (float)n) + 1e-6f;  // rms + eps
+        }
+    } else if (tid < kWave) {
         const float s1 = seq_sum(buf, n);
         if (tid == 0) {
             stat[0] = KIND == kLayerNorm ? s1 / (float)n : 0.0f;
@@ -105,7 +117,10 @@ __global__ __launch_bounds__(1024) void k_norm(const uint8_t* __restrict__ a, in
             buf[tid + m * bs] = (xv[m] - mu) * (xv[m] - mu);
         }
         __syncthreads();
-        if (tid < kWave) {
+        if (block_sum) {
+            const float ssq = block_seq_sum_nonneg(buf, n, ssh);
+            if (tid == 0) stat[1] = sqrtf(ssq / (float)n) + 1e-05f;
+        } else if (tid < kWave) {
             const float ssq = seq_sum(buf, n);
             if (tid == 0) stat[1] = sqrtf(ssq / (float)n) + 1e-05f;
         }

@@ -146,8 +146,9 @@ __device__ __forceinline__ SsSeg wave_scan_seg(SsSeg x)
 }
 
 // Sum of t[0..n) in index order, as the sequential fp32 loop computes it,
-// for t >= 0 in LDS; n a multiple of 256, n <= 4096.  Called by all 256
-// threads of the workgroup; every thread returns the sum.  *fast (thread
+// for t >= 0 in LDS; n a multiple of 256, n <= 4096.  Called by every
+// thread of a workgroup of 256 or more threads (the first 256 compute, the
+// others only join the barriers); every thread returns the sum.  *fast (thread
 // 0's view) tells whether the parallel path was taken.  Synchronizes the
 // workgroup through LDS barriers only (global loads may stay in flight).
 //
@@ -160,6 +161,19 @@ __device__ __forceinline__ SsSeg wave_scan_seg(SsSeg x)
 template <int C>
 __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* fast)
 {
+    if (threadIdx.x >= kSsThreads) {
+        // waves past the first four (larger workgroups) only keep the
+        // barrier count of the path below: its four phase barriers, the
+        // fallback's barrier when it is taken, and the final one
+        lds_barrier();
+        lds_barrier();
+        lds_barrier();
+        lds_barrier();
+        if (!sh.ok) lds_barrier();
+        const float res = sh.result;
+        lds_barrier();
+        return res;
+    }
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
     const int c = C ? C : n / kSsThreads;
     const int i0 = tid * c;
