@@ -70,6 +70,18 @@ __device__ __forceinline__ float rope_lane(float x, int lane, int d_half, const 
     return x;
 }
 
+// The same with the lane's (cos, sin) pair already loaded (cs[lane] for
+// lane < d_half, cs[lane - d_half] for d_half <= lane < 2 d_half).
+__device__ __forceinline__ float rope_lane_pair(float x, int lane, int d_half, float2 t)
+{
+    const int d_r = 2 * d_half;
+    const int partner = lane < d_half ? lane + d_half : (lane < d_r ? lane - d_half : lane);
+    const float xp = __shfl(x, partner);
+    if (lane < d_half) return x * t.x - xp * t.y;
+    if (lane < d_r) return xp * t.y + x * t.x;
+    return x;
+}
+
 // Code of element e (0..31) in a lane-permuted weight block (see
 // nc_layout.h): dword index and byte position of the element.
 __device__ __forceinline__ int wblock_byte_pos(int e) { return (e & 1) + (((e & 15) >> 3) << 1); }

@@ -14,7 +14,8 @@
 //     four lane sums per block, P.V as eight fp32 lanes (position mod 8)
 //     summed left to right, then the n mod 8 tail.
 // The K and V rows of the earlier positions are requested first, into
-// registers, so their latency overlaps the q/k/v work.
+// registers, so their latency overlaps the q/k/v work (whose own inputs --
+// the qkv output and the RoPE pair -- are requested before them).
 #include <type_traits>
 
 #include "nc_act.h"
@@ -34,8 +35,8 @@ __device__ __forceinline__ void static_for(F&& f)
 }
 
 constexpr int kAdThreads = 256;
-constexpr int kAdMaxK = 3;   // K rows per thread held in registers (positions < 768)
-constexpr int kAdMaxV = 10;  // 16-byte V loads per thread held in registers (positions < 640)
+constexpr int kAdMaxK = 3;   // K rows per thread in registers at most (positions < 768)
+constexpr int kAdMaxV = 10;  // 16-byte V parts per thread in registers at most (positions < 640)
 constexpr int kAdVB = 80;    // LDS bytes per staged V position: 64 codes, 2 fp16 deltas, pad
 
 __device__ __forceinline__ uint32_t ad_pick(uint32_t lo, uint32_t hi, int odd)
@@ -86,7 +87,11 @@ __device__ __forceinline__ float wave_max(float v)
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-template <bool QKNORM>
+// MK K rows and MV 16-byte V parts per thread are requested into registers
+// at the start (every slot, so the load counts are static and the waits
+// exact); positions past them are read in the loops after.  The launcher
+// sizes them to the cache: issuing the loads is itself a cost.
+template <bool QKNORM, int MK, int MV>
 __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict__ raw, int hq, int hkv,
                                                          const uint16_t* __restrict__ qn_w,
                                                          const uint16_t* __restrict__ kn_w,
@@ -107,7 +112,16 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     // requested before the position is known
     const int col = w == 0 ? h * 64 : (w == 1 ? hq * 64 + g * 64 : hq * 64 + hkv * 64 + g * 64);
     const float raw_x = w < 3 ? raw[col + lane] : 0.0f;
+    // the lane's RoPE pair (q and k waves) is requested before the K / V
+    // rows: the vector memory counter completes in order, so a pair
+    // requested after them would be waited for together with all of them
+    const int pair = lane < d_half ? lane : lane - d_half;
+    const bool rope_lane_in = w < 2 && lane < 2 * d_half;
+    float2 rp = make_float2(0.0f, 0.0f);
+    if (rope_cur && rope_lane_in) rp = rope_cur[pair];
     const int pos = dpos ? load_pos(dpos) : pos_host;
+    if (!rope_cur && rope_lane_in) rp = table[(size_t)pos * d_half + pair];
+    __builtin_amdgcn_sched_barrier(0);
     const int n = pos + 1;
     // the shared-memory layout is sized by the cache rows, not by the position
     const int spad = (kv_rows + 3) & ~3;
@@ -119,9 +133,9 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     const uint8_t* vslice = vc + g * 64;
 
     // ---- K rows (positions < pos) into registers, V slices too
-    uint4 kr[kAdMaxK][4];
-    uint32_t kd[kAdMaxK];
-    static_for<0, kAdMaxK>([&](auto I) {
+    uint4 kr[MK][4];
+    uint32_t kd[MK];
+    static_for<0, MK>([&](auto I) {
         const int c = tid + I * kAdThreads;
         const int cc = c < pos ? c : 0;
         const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)cc * kv_pitch);
@@ -130,9 +144,9 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         kd[I] = reinterpret_cast<const uint32_t*>(kc + (size_t)cc * kv_pitch + kvd)[g];
     });
     const int vtotal = pos * 4;  // 16-byte parts of the earlier positions' V slices
-    uint32_t vr[kAdMaxV][4];  // plain words: an array of the uint4 union type stays in scratch memory
-    uint32_t vd[kAdMaxV];
-    static_for<0, kAdMaxV>([&](auto I) {
+    uint32_t vr[MV][4];  // plain words: an array of the uint4 union type stays in scratch memory
+    uint32_t vd[MV];
+    static_for<0, MV>([&](auto I) {
         const int idx = tid + I * kAdThreads;
         const int c = idx < vtotal ? idx >> 2 : 0, part = idx & 3;
         const uint4 t4 = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[part];
@@ -157,7 +171,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
                 const float rms = sqrtf(seq_sum(buf, 64) / 64.0f);
                 x = q8_roundtrip_lane(x / (rms + 1e-6f) * h2f((w == 0 ? qn_w : kn_w)[lane]), true);
             }
-            x = rope_lane(x, lane, d_half, rope_cur ? rope_cur : table + (size_t)pos * d_half);
+            x = rope_lane_pair(x, lane, d_half, rp);
         }
         uint16_t d16;
         const int8_t code = q8_quant_lane(x, true, &d16);
@@ -181,14 +195,14 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         for (int v = 0; v < 4; v++) qv[v] = reinterpret_cast<const uint4*>(s_q)[v];
         dq[0] = h2f(reinterpret_cast<const uint16_t*>(s_q + 64)[0]);
         dq[1] = h2f(reinterpret_cast<const uint16_t*>(s_q + 64)[1]);
-        static_for<0, kAdMaxK>([&](auto I) {
+        static_for<0, MK>([&](auto I) {
             const int c = tid + I * kAdThreads;
             if (c < pos) {
                 const float dk[2] = {h2f((uint16_t)(kd[I] & 0xFFFFu)), h2f((uint16_t)(kd[I] >> 16))};
                 S[c] = head_dot_q8(qv, dq, kr[I], dk) * scale;
             }
         });
-        for (int c = tid + kAdMaxK * kAdThreads; c < pos; c += kAdThreads) {
+        for (int c = tid + MK * kAdThreads; c < pos; c += kAdThreads) {
             uint4 kk[4];
             const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)c * kv_pitch);
 #pragma unroll
@@ -207,7 +221,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         }
     }
     // V slices of the earlier positions into shared memory
-    static_for<0, kAdMaxV>([&](auto I) {
+    static_for<0, MV>([&](auto I) {
         const int idx = tid + I * kAdThreads;
         if (idx < vtotal) {
             const int c = idx >> 2, part = idx & 3;
@@ -215,7 +229,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
             if (part == 0) reinterpret_cast<uint32_t*>(Vs + (size_t)c * kAdVB + 64)[0] = vd[I];
         }
     });
-    for (int idx = tid + kAdMaxV * kAdThreads; idx < vtotal; idx += kAdThreads) {
+    for (int idx = tid + MV * kAdThreads; idx < vtotal; idx += kAdThreads) {
         const int c = idx >> 2, part = idx & 3;
         reinterpret_cast<uint4*>(Vs + (size_t)c * kAdVB)[part] =
                 reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[part];
@@ -306,14 +320,22 @@ int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, 
     const size_t lds = ((size_t)((max_ctx + 3) & ~3) + 512) * 4 + (size_t)max_ctx * kAdVB;
     if (lds > 60 * 1024) return fail(NC_ERR_ARG, "attention: context %d too long", max_ctx);
     const float scale = 1.0f / sqrtf(64.0f);
-    if (qn_w)
-        hipLaunchKernelGGL(k_attn_dec<true>, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w,
-                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale,
-                           (const float2*)rope_cur, max_ctx);
-    else
-        hipLaunchKernelGGL(k_attn_dec<false>, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w,
-                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale,
-                           (const float2*)rope_cur, max_ctx);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w, (const float2*)table,
+                           d_half, pos, dpos, kc, vc, kv_pitch, out, scale, (const float2*)rope_cur, max_ctx);
+    };
+    // register slots for the cache's positions (K: one row per slot and
+    // thread, V: a quarter row)
+    auto by_norm = [&](auto qk) {
+        constexpr bool QK = decltype(qk)::value;
+        if (max_ctx <= 128) go(k_attn_dec<QK, 1, 2>);
+        else if (max_ctx <= 256) go(k_attn_dec<QK, 1, 4>);
+        else if (max_ctx <= 320) go(k_attn_dec<QK, 2, 5>);
+        else if (max_ctx <= 512) go(k_attn_dec<QK, 2, 8>);
+        else go(k_attn_dec<QK, kAdMaxK, kAdMaxV>);
+    };
+    if (qn_w) by_norm(std::true_type{});
+    else by_norm(std::false_type{});
     return launch_status("k_attn_dec");
 }
 

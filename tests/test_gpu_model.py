@@ -116,3 +116,17 @@ def test_full_workload_stream(gpu, name):
     first_diff = next((i for i, (a, b) in enumerate(zip(toks.tolist(), ref)) if a != b), None)
     assert toks.tolist() == ref, f"streams diverge at step {first_diff}"
     m.close()
+
+
+@pytest.mark.parametrize("max_ctx", [200, 400])
+@pytest.mark.parametrize("name", ["small-llama-q4", "small-openelm-q8"])
+def test_small_model_stream_with_larger_cache(gpu, name, max_ctx):
+    """The decode attention sizes its register prefetch to the cache: the
+    cache sizes of no full workload (200, 400 positions) give the same
+    stream."""
+    w = SMALL[name]
+    g = golden(name)
+    m = gpu.Model(config_of(w, cls=gpu.ModelConfig, max_ctx=max_ctx))
+    m.init_synthetic(w["seed"])
+    assert m.generate(prompt_of(w), w["gen"]).tolist() == g["tokens"]
+    m.close()
