@@ -678,35 +678,48 @@ extern "C" int nc_block_seq_sum(const float* t, int n, int count, float* out, in
 }
 
 // The same segment / crossing decomposition run on the host with the
-// kernels' step, composition and check functions, the binades predicted
-// from a double-precision prefix scaled by (1 + skew): a skew makes
-// predictions wrong on purpose, which the segment checks must catch (the
-// result stays the sequential sum; *fast says whether the checks passed).
+// kernels' representatives, composition and check functions, the binades
+// predicted from a double-precision prefix scaled by (1 + skew), and each
+// run's representatives started from that prediction: a skew makes
+// predictions wrong on purpose, which the checks must catch (the result
+// stays the sequential sum; *fast says whether the checks passed).
 extern "C" float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int* fast)
 {
     using namespace nc;
+    auto bits = [](float v) { return __builtin_bit_cast(int, v); };
+    auto flt = [](int b) { return __builtin_bit_cast(float, b); };
     double P = 0.0;
-    int Eb = ss_binade((float)(P * (1.0 + skew)));
-    int c0 = 0, c1 = 0;
+    float pred = (float)(P * (1.0 + skew));
+    int Eb = ss_binade(pred);
+    int b0 = ss_rep_base(pred);
+    float r0 = flt(b0), r1 = flt(b0 | 1);
     bool nz = false;
     float s = 0.0f;
     bool ok = true;
+    auto close = [&]() {
+        // the run's representatives must still be inside its binade
+        return r1 < ss_top(Eb) && ss_apply(s, SsMap{bits(r0) - b0, bits(r1) - (b0 | 1), nz}, Eb);
+    };
     for (int i = 0; i < n && ok; i++) {
         const double Pa = P + (double)t[i];
-        const int Ea = ss_binade((float)(Pa * (1.0 + skew)));
+        pred = (float)(Pa * (1.0 + skew));
+        const int Ea = ss_binade(pred);
         if (Ea == Eb) {
-            ss_advance(c0, c1, t[i], Eb, &c0, &c1);
+            r0 = r0 + t[i];
+            r1 = r1 + t[i];
             nz = nz || t[i] != 0.0f;
         } else {
-            ok = ss_apply(s, SsMap{c0, c1, nz}, Eb);
+            ok = close();
             s = s + t[i];
-            c0 = c1 = 0;
+            Eb = Ea;
+            b0 = ss_rep_base(pred);
+            r0 = flt(b0);
+            r1 = flt(b0 | 1);
             nz = false;
         }
         P = Pa;
-        Eb = Ea;
     }
-    if (ok) ok = ss_apply(s, SsMap{c0, c1, nz}, Eb);
+    if (ok) ok = close();
     if (fast) *fast = ok;
     if (ok) return s;
     float r = 0.0f;

@@ -9,6 +9,12 @@
 // to-nearest-even).  A run of such steps is therefore a map
 //     parity p  ->  C_p units added          (p = 0, 1)
 // and runs compose associatively:  (A then B)_p = A_p + B_{(p + A_p) & 1}.
+// A run's map is read off two representatives, an even and an odd value of
+// the binade: each takes the run's fp32 adds, and C_p is how far its bit
+// pattern moved (consecutive grid values have consecutive bit patterns).
+// The representatives start at the predicted running sum, so they stay in
+// the binade whenever the prediction is right; one that leaves it voids
+// the map.
 // Steps that leave the binade ("crossings") are few -- the sum of
 // non-negative terms only grows, so at most one per binade passed -- and
 // are replayed exactly, one fp32 add each, by a single lane.
@@ -51,22 +57,14 @@ NC_HD SsMap ss_compose(const SsMap& a, const SsMap& b)
     return r;
 }
 
-// The open map (c0, c1) followed by one step s -> RN(s + x) with s and the
-// result in binade E: the step adds D = floor(q) + (frac(q) > 1/2) grid
-// units, q = x / u exact (a power-of-two scale of a value below 2^(E+1), so
-// below 2^24 units), plus one more on a tie when the current value is odd:
-// track 0 is at parity c0, track 1 at parity 1 + c1.
-NC_HD void ss_advance(int c0, int c1, float x, int E, int* n0, int* n1)
-{
-    const float q = __builtin_ldexpf(x, 150 - E);
-    const float fl = __builtin_floorf(q);
-    const float fr = q - fl;
-    const int f = (int)fl;
-    const int base = f + (fr > 0.5f ? 1 : 0);
-    const int tie = fr == 0.5f ? 1 : 0;
-    *n0 = c0 + base + (tie & (c0 ^ f));
-    *n1 = c1 + base + (tie & (c1 ^ f ^ 1));
-}
+// First value above binade E (1 <= E <= 254): 2^(E-126); binade 254's is
+// +inf, and E = 255 (inf, NaN) gets -0, below everything.  A representative
+// r of E stays inside it while r < ss_top(E) (it only grows).
+NC_HD float ss_top(int E) { return __builtin_bit_cast(float, (uint32_t)(E + 1) << 23); }
+
+// Representatives of a run that starts near p: the even bit pattern at or
+// below p's (same binade: binade boundaries are even patterns) and the next.
+NC_HD int ss_rep_base(float p) { return __builtin_bit_cast(int, p) & ~1; }
 
 // Applies a segment map computed for binade E to the exact value s.
 // Within binade E consecutive grid values have consecutive bit patterns
@@ -215,44 +213,71 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
     float A = dpp_f<kDppWaveShr1>(I);  // the previous lane's I
     if (lane == 0) A = WP;
     // ---- walk (threads >= 1): binade of each step predicted from the
-    // approximate prefix; in-binade steps composed into the open map
-    // (c0, c1), crossing steps recorded with the map before them
-    int c0 = 0, c1 = 0, nz = 0, ncross = 0;
+    // approximate prefix; in-binade steps taken by the two representatives
+    // (r0 even, r1 odd, from bit pattern b0), crossing steps recorded with
+    // the map before them.  Steps before the last only grow the prefix, so
+    // one compare finds their crossings; the last step's prefix is I, which
+    // may round below the walked one.
+    int c0 = 0, c1 = 0, nz = 0, ncross = 0, bad = 0;
     int4 rec[kSsMaxRec];  // (c0, c1, binade or 0, term bits) of this chunk's crossings
 #pragma unroll
     for (int q = 0; q < kSsMaxRec; q++) rec[q] = make_int4(0, 0, 0, 0);
     if (tid > 0) {
         float P = A;
         int Eb = ss_binade(A);
+        float top = ss_top(Eb);
+        int b0 = ss_rep_base(A);
+        float r0 = __builtin_bit_cast(float, b0), r1 = __builtin_bit_cast(float, b0 | 1);
+        uint32_t nzb = 0;  // OR of the open run's term bits
 #pragma unroll
         for (int k = 0; k < kSsMaxPer; k++) {
             if (k < c) {
                 const float x = v[k];
-                const float Pa = k + 1 < c ? P + x : I;
-                const int Ea = ss_binade(Pa);
-                const bool cross = Ea != Eb;
-                int n0, n1;
-                ss_advance(c0, c1, x, Eb, &n0, &n1);
-                const int nn = nz | (x != 0.0f ? 1 : 0);
+                const bool last = k + 1 == c;
+                const float Pa = last ? I : P + x;
+                const bool cross = last ? ss_binade(Pa) != Eb : !(Pa < top);
+                const float n0 = r0 + x, n1 = r1 + x;
+                const uint32_t nn = nzb | __builtin_bit_cast(uint32_t, x);
                 if (__builtin_amdgcn_ballot_w64(cross)) {
-                    const int4 r = make_int4(c0, c1, nz ? Eb : 0, __builtin_bit_cast(int, x));
+                    if (cross) {
+                        bad |= !(r1 < top) ? 1 : 0;
+                        const int4 r = make_int4(__builtin_bit_cast(int, r0) - b0,
+                                                 __builtin_bit_cast(int, r1) - (b0 | 1), nzb ? Eb : 0,
+                                                 __builtin_bit_cast(int, x));
 #pragma unroll
-                    for (int q = 0; q < kSsMaxRec; q++)
-                        if (cross && ncross == q) rec[q] = r;
+                        for (int q = 0; q < kSsMaxRec; q++)
+                            if (ncross == q) rec[q] = r;
+                        ncross++;
+                        Eb = ss_binade(Pa);
+                        top = ss_top(Eb);
+                        b0 = ss_rep_base(Pa);
+                        r0 = __builtin_bit_cast(float, b0);
+                        r1 = __builtin_bit_cast(float, b0 | 1);
+                        nzb = 0;
+                    } else {
+                        r0 = n0;
+                        r1 = n1;
+                        nzb = nn;
+                    }
+                } else {
+                    r0 = n0;
+                    r1 = n1;
+                    nzb = nn;
                 }
-                c0 = cross ? 0 : n0;
-                c1 = cross ? 0 : n1;
-                nz = cross ? 0 : nn;
-                ncross += cross ? 1 : 0;
                 P = Pa;
-                Eb = Ea;
             }
         }
+        bad |= !(r1 < top) ? 1 : 0;
+        c0 = __builtin_bit_cast(int, r0) - b0;
+        c1 = __builtin_bit_cast(int, r1) - (b0 | 1);
+        nz = nzb ? 1 : 0;
     }
     // ---- segmented scan of (open map, has-crossing) and scan of the counts
     SsSeg x{c0, c1, nz | (ncross > 0 ? 2 : 0), ncross};
     x = wave_scan_seg(x);
-    const int over = __builtin_amdgcn_ballot_w64(ncross > kSsMaxRec) != 0;
+    // a chunk with too many crossings or a representative that left its
+    // binade takes the plain loop
+    const int over = __builtin_amdgcn_ballot_w64(ncross > kSsMaxRec || bad) != 0;
     if (lane == kWave - 1) {
         sh.wc0[w] = x.c0;
         sh.wc1[w] = x.c1;
