@@ -330,8 +330,8 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             const size_t b = j < nitems && g * R + r < A.N ? (size_t)(g * R + r) * nb + i : 0;
             const uint4* src = reinterpret_cast<const uint4*>(A.wq + b * WD);
 #pragma unroll
-            for (int v = 0; v < WV; v++) w[it][v] = src[v];
-            dw[it] = A.wd[b];
+            for (int v = 0; v < WV; v++) w[it][v] = load_stream(src + v);
+            dw[it] = load_stream(A.wd + b);
         }
     };
     const int G = gridDim.x;
@@ -504,8 +504,8 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
             const size_t bi = (size_t)row * NB + i;
             const uint4* src = reinterpret_cast<const uint4*>(A.wq + bi * WD);
 #pragma unroll
-            for (int v = 0; v < WV; v++) w[it][v] = src[v];
-            dw[it] = A.wd[bi];
+            for (int v = 0; v < WV; v++) w[it][v] = load_stream(src + v);
+            dw[it] = load_stream(A.wd + bi);
         }
     };
     int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks

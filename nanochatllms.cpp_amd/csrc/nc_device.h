@@ -14,6 +14,18 @@ namespace nc {
 
 constexpr int kWave = 64;
 
+// Streaming loads (the nt bit) for data a launch reads once, the weights of
+// a decode matvec: with the default policy the hundreds of MB of weights a
+// decode step streams through L2 push out the small rows every launch
+// re-reads (activations, norm gains, cache rows); streamed lines do not.
+typedef unsigned int NcU32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint4* p)
+{
+    const NcU32x4 v = __builtin_nontemporal_load(reinterpret_cast<const NcU32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint16_t load_stream(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+
 // fp16 -> fp32, exact (gten/gten_types.h:129-133).
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 

@@ -69,8 +69,8 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_q(const uint8_t* __restri
         const size_t b = ok ? (size_t)(row0 + r) * nb + i : 0;
         const uint4* src = reinterpret_cast<const uint4*>(wq + b * WD);
 #pragma unroll
-        for (int v = 0; v < WD / 4; v++) w[it][v] = src[v];
-        dw16[it] = wd[b];
+        for (int v = 0; v < WD / 4; v++) w[it][v] = load_stream(src + v);
+        dw16[it] = load_stream(wd + b);
     }
     for (int p = 0; p < n_xrows; p++) {
         const uint8_t* xr = x + (size_t)p * x_pitch;
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(64) void k_matvec_f16_row(const uint8_t* __restrict
 #pragma unroll
         for (int b = 0; b < kF16Batch; b++) {
             const int g = gbase + b;
-            dst[b] = wrow[(size_t)(g < G ? g : 0) * gstride];
+            dst[b] = load_stream(wrow + (size_t)(g < G ? g : 0) * gstride);
         }
     };
     // the activation row first (8 halves per load, K <= 8192), then the
