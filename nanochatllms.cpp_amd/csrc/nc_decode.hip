@@ -516,12 +516,20 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     // the terms of all 64 rows, then the gate rows' folds (waves 0-1) and
     // the up rows' folds (waves 2-3) side by side
     auto pass = [&]() {
+        // NB dividing the workgroup: every item of a thread is block
+        // tid % NB, read from LDS once
+        constexpr bool kOneBlock = kDmvThreads % NB == 0;
+        StagedX x0{};
+        if (kOneBlock) x0 = load_staged(xs + (tid % NB) * kStage);
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int j = tid + it * kDmvThreads;
             const int r = j / NB, i = j - r * NB;
             float tv[4];
-            q_block_terms<WT>(xs + i * kStage, w[it], dw[it], tv);
+            if (kOneBlock)
+                q_block_terms<WT>(x0, w[it], dw[it], tv);
+            else
+                q_block_terms<WT>(xs + i * kStage, w[it], dw[it], tv);
             float* t = T + r * 4 * TP + i;
 #pragma unroll
             for (int k = 0; k < 4; k++) t[k * TP] = tv[k];

@@ -59,19 +59,30 @@ __device__ __forceinline__ void stage_x_block(const XRaw& x, uint32_t* dst)
     for (int v = 0; v < 4; v++) d[v] = make_uint4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
 }
 
+// A staged activation block read back from LDS: the lane codes, the lane
+// offsets c_k and the delta.
+struct StagedX {
+    uint32_t xa[4], xb[4];
+    int c[4];
+    float dx;
+};
+
+__device__ __forceinline__ StagedX load_staged(const uint32_t* staged)
+{
+    const uint4* s = reinterpret_cast<const uint4*>(staged);
+    const uint4 s0 = s[0], s1 = s[1], s2 = s[2], s3 = s[3];
+    return StagedX{{s0.x, s0.z, s1.x, s1.z}, {s0.y, s0.w, s1.y, s1.w}, {(int)s2.x, (int)s2.y, (int)s2.z, (int)s2.w},
+                   __uint_as_float(s3.x)};
+}
+
 // The four lane terms of one weight block against a staged activation
 // block.  W holds the block's lane-permuted codes (4 dwords Q4, 8 Q8).
 template <int WT>
-__device__ __forceinline__ void q_block_terms(const uint32_t* staged, const uint4 (&w)[WT == Q4 ? 1 : 2], uint16_t dw16,
+__device__ __forceinline__ void q_block_terms(const StagedX& x, const uint4 (&w)[WT == Q4 ? 1 : 2], uint16_t dw16,
                                               float (&t)[4])
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
-    const uint4* s = reinterpret_cast<const uint4*>(staged);
-    const uint4 s0 = s[0], s1 = s[1], s2 = s[2], s3 = s[3];
-    const uint32_t xa[4] = {s0.x, s0.z, s1.x, s1.z};
-    const uint32_t xb[4] = {s0.y, s0.w, s1.y, s1.w};
-    const int c[4] = {(int)s2.x, (int)s2.y, (int)s2.z, (int)s2.w};
-    const float dd = __uint_as_float(s3.x) * h2f(dw16);
+    const float dd = x.dx * h2f(dw16);
     uint32_t W[WD];
 #pragma unroll
     for (int v = 0; v < WD / 4; v++) {
@@ -87,14 +98,21 @@ __device__ __forceinline__ void q_block_terms(const uint32_t* staged, const uint
             // value = code - 7: sum (code - 7) x = sum code x - 7 sum x, the
             // -7 sum x of the lane pre-computed at staging
             const uint32_t P = W[k];
-            L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)xa[k], c[k], false);
-            L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)xb[k], L, false);
+            L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)x.xa[k], x.c[k], false);
+            L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)x.xb[k], L, false);
         } else {
-            L = __builtin_amdgcn_sdot4((int)W[2 * k], (int)xa[k], 0, false);
-            L = __builtin_amdgcn_sdot4((int)W[2 * k + 1], (int)xb[k], L, false);
+            L = __builtin_amdgcn_sdot4((int)W[2 * k], (int)x.xa[k], 0, false);
+            L = __builtin_amdgcn_sdot4((int)W[2 * k + 1], (int)x.xb[k], L, false);
         }
         t[k] = (float)L * dd;
     }
+}
+
+template <int WT>
+__device__ __forceinline__ void q_block_terms(const uint32_t* staged, const uint4 (&w)[WT == Q4 ? 1 : 2], uint16_t dw16,
+                                              float (&t)[4])
+{
+    q_block_terms<WT>(load_staged(staged), w, dw16, t);
 }
 
 }  // namespace nc
