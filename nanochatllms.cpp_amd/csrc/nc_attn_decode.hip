@@ -263,38 +263,43 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     }
     lds_barrier();
 
-    // ---- P.V: thread = (column j, lanes l and l + 4), both chains in step
+    // ---- P.V: thread = (lane l = tid / 32, columns 2m and 2m + 1 with
+    // m = tid % 32): the chains (l, 2m) and (l, 2m + 1) over positions l,
+    // l + 8, ... in order, both column codes of a position in one load
     {
-        const int j = lane, l = w;
+        const int l = tid >> 5, m = tid & 31;
         const int n8 = n & ~7;
-        auto vval = [&](int c) -> float {
+        auto vpair = [&](int c, float& v0, float& v1) {
             const uint8_t* vrow = Vs + (size_t)c * kAdVB;
-            return (float)reinterpret_cast<const int8_t*>(vrow)[j] * h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[j >> 5]);
+            const uint32_t codes = reinterpret_cast<const uint16_t*>(vrow)[m];
+            const float d = h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[m >> 4]);  // block of column 2m
+            v0 = (float)(int8_t)(codes & 0xFFu) * d;
+            v1 = (float)(int8_t)(codes >> 8) * d;
         };
         float a0 = 0.0f, a1 = 0.0f;
         int c = 0;
         for (; c + 64 <= n8; c += 64) {
-            // eight positions of each chain: loads first, then the adds in order
-            float p0[8], v0[8], p1[8], v1[8];
+            // eight positions of both chains: loads first, then the adds in order
+            float p[8], v0[8], v1[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                p0[u] = S[c + 8 * u + l];
-                v0[u] = vval(c + 8 * u + l);
-                p1[u] = S[c + 8 * u + l + 4];
-                v1[u] = vval(c + 8 * u + l + 4);
+                p[u] = S[c + 8 * u + l];
+                vpair(c + 8 * u + l, v0[u], v1[u]);
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                a0 = p0[u] * v0[u] + a0;
-                a1 = p1[u] * v1[u] + a1;
+                a0 = p[u] * v0[u] + a0;
+                a1 = p[u] * v1[u] + a1;
             }
         }
         for (; c < n8; c += 8) {
-            a0 = S[c + l] * vval(c + l) + a0;
-            a1 = S[c + l + 4] * vval(c + l + 4) + a1;
+            float v0, v1;
+            vpair(c + l, v0, v1);
+            const float p = S[c + l];
+            a0 = p * v0 + a0;
+            a1 = p * v1 + a1;
         }
-        acc[l * 64 + j] = a0;
-        acc[(l + 4) * 64 + j] = a1;
+        *reinterpret_cast<float2*>(acc + l * 64 + 2 * m) = make_float2(a0, a1);
     }
     lds_barrier();
     if (w == 0) {
