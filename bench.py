@@ -127,6 +127,23 @@ def traffic_for(workload, kernel_role):
     return None if e is None else e.get("bytes_per_launch")
 
 
+def kernel_table(ms, nbytes, kind):
+    """Per matvec role: launches, total and average launch time, bytes per
+    launch and the achieved rate."""
+    out = []
+    for k in sorted(set(kind.tolist())):
+        sel = kind == k
+        role = nc.PROF_ROLES[k & 7]
+        fused = bool(k & nc.PROF_FUSED)
+        avg_ms = float(ms[sel].mean())
+        avg_b = float(nbytes[sel].mean())
+        out.append({"role": role, "kernel": FUSED_KERNEL[role] if fused else "k_matvec_q",
+                    "launches": int(sel.sum()), "total_ms": round(float(ms[sel].sum()), 4),
+                    "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(avg_b),
+                    "achieved_gbs": round(avg_b / (avg_ms * 1e-3) / 1e9, 1)})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +155,7 @@ def main():
                     "the captured decode-step graph (for profilers that do not follow graph launches)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     ap.add_argument("--no-topk", action="store_true", help="skip the sampled-decode measurement (profiler runs)")
+    ap.add_argument("--no-tree-profile", action="store_true", help="skip the per-kernel timing of the tree mode")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -174,6 +192,45 @@ def main():
     model.decode(args.steps)
     nc.check(L.nc_synchronize())
     dt = time.perf_counter() - t0
+    ordered_toks = model.decode(0, fetch=True)[: 1 + args.warmup + args.steps]
+    # the same steps in the tree reduction mode (tree sums in the fused
+    # kernels, results within rel-L2 1e-3 of the reference's): rate and how
+    # many tokens of the stream equal the ordered (bit-exact) stream
+    model.set_reduce(nc.REDUCE_TREE)
+    model.prefill(prompt)
+    model.decode(args.warmup)
+    nc.check(L.nc_synchronize())
+    t0 = time.perf_counter()
+    model.decode(args.steps)
+    nc.check(L.nc_synchronize())
+    dt_tree = time.perf_counter() - t0
+    tree_toks = model.decode(0, fetch=True)[: 1 + args.warmup + args.steps]
+    diff = np.nonzero(tree_toks != ordered_toks)[0]
+    tree_equal = int(diff[0]) if len(diff) else len(ordered_toks)
+    tree_ms, tree_b, tree_kind = None, None, None
+    if not args.no_tree_profile:
+        model.prefill(prompt)
+        model.decode(args.warmup)
+        model.profile_begin((4 * cfg.n_layers + 1) * args.steps)
+        model.decode(args.steps)
+        nc.check(L.nc_synchronize())
+        model.profile_end()
+        tree_ms, tree_b, tree_kind = model.profile_launches((4 * cfg.n_layers + 1) * args.steps)
+    # one step in both modes on the same cache: the first layer whose
+    # residual codes differ, and how far apart the logits end up
+    seq = np.concatenate([prompt, ordered_toks[:1]]).astype(np.int32)
+    model.set_reduce(nc.REDUCE_ORDERED)
+    model.logits(prompt, 0)
+    lo = model.logits(seq, len(seq) - 1)
+    ro = [model.layer_out(l, len(seq) - 1) for l in range(cfg.n_layers)]
+    model.set_reduce(nc.REDUCE_TREE)
+    lt = model.logits(seq, len(seq) - 1)
+    moved = [int((model.layer_out(l, len(seq) - 1) != ro[l]).sum()) for l in range(cfg.n_layers)]
+    tree_step = {"first_layer_moved": next((l for l, k in enumerate(moved) if k), None),
+                 "bytes_moved_last_layer": moved[-1],
+                 "logits_rel_l2": float(np.linalg.norm((lt - lo).astype(np.float64)) /
+                                        np.linalg.norm(lo.astype(np.float64)))}
+    model.set_reduce(nc.REDUCE_ORDERED)
     # sampled decode (top-k 40, temperature 0.8, mt19937 seed 7): the same
     # step with the device sampler in place of the greedy pick; the rate is
     # the difference of two calls, prompt + first token and prompt + first
@@ -203,17 +260,7 @@ def main():
     ms, nbytes, kind = model.profile_launches(launches_per_step * args.steps)
     model.close()
 
-    per_kernel = []
-    for k in sorted(set(kind.tolist())):
-        sel = kind == k
-        role = nc.PROF_ROLES[k & 7]
-        fused = bool(k & nc.PROF_FUSED)
-        avg_ms = float(ms[sel].mean())
-        avg_b = float(nbytes[sel].mean())
-        per_kernel.append({"role": role, "kernel": FUSED_KERNEL[role] if fused else "k_matvec_q",
-                           "launches": int(sel.sum()), "total_ms": round(float(ms[sel].sum()), 4),
-                           "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(avg_b),
-                           "achieved_gbs": round(avg_b / (avg_ms * 1e-3) / 1e9, 1)})
+    per_kernel = kernel_table(ms, nbytes, kind)
     dom = max(per_kernel, key=lambda e: e["total_ms"])
     traffic = traffic_for(args.workload, dom["role"])
 
@@ -247,7 +294,22 @@ def main():
                      "kernel": dom["kernel"], "avg_launch_us": dom["avg_launch_us"],
                      "bytes_per_launch": dom["bytes_per_launch"], "launches": dom["launches"]},
         "per_kernel": per_kernel,
+        "tree_reduce": {"decode_tok_s": round(args.steps / dt_tree, 2),
+                        "stream_equal_tokens": tree_equal, "stream_tokens": len(ordered_toks),
+                        "step_vs_ordered": tree_step,
+                        "note": "same steps with nc_model_set_reduce(TREE): rms_norm sums, matvec folds and the "
+                                "softmax sum as tree reductions, not bit-exact; stream_equal_tokens = leading "
+                                "tokens equal to the ordered (reference) stream; step_vs_ordered = one step of "
+                                "both modes on the same cache (first layer with a moved residual byte, bytes "
+                                "moved in the last layer's row, logits rel-L2)"},
     }
+    if tree_ms is not None:
+        tk = kernel_table(tree_ms, tree_b, tree_kind)
+        line["tree_reduce"]["per_kernel"] = [{k: e[k] for k in ("role", "avg_launch_us", "achieved_gbs")} for e in tk]
+        tdom = next((e for e in tk if e["role"] == dom["role"]), None)
+        if tdom:
+            line["tree_reduce"]["roofline"] = {"kernel": tdom["kernel"], "achieved": tdom["achieved_gbs"],
+                                               "frac": round(tdom["achieved_gbs"] / HBM_PEAK_GBS, 4)}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, prompt)
     print(json.dumps(line), flush=True)

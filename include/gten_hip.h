@@ -248,6 +248,24 @@ int nc_model_get_weight(void* model, int layer, int slot, void* ref_bytes, size_
 /* Model::logits(tokens, start_pos): processes rows [start_pos, n_tokens) and
  * copies the last row's fp32 logits to `logits` (host, n_vocab floats). */
 int nc_model_logits(void* model, const int32_t* tokens, int n_tokens, int start_pos, float* logits);
+/* Reduction order of the single-row decode step (no counterpart in the
+ * reference, which has one order; for callers that trade the reference's
+ * results for a faster step).
+ *   NC_REDUCE_ORDERED (default): the reference's sequential sums -- the
+ *     rms_norm sum of squares (src/gten/ops.cpp:830-903), each matvec row's
+ *     per-lane block chains (ops.cpp:292-490) and the softmax denominator
+ *     (ops.cpp:1061-1081) -- so every result equals the reference's bits.
+ *   NC_REDUCE_TREE: those three sums as tree reductions, in the fused Q8/Q4
+ *     decode kernels only.  Every rounding and requantization point stays;
+ *     only the order of the fp32 adds changes.  A sum that then rounds a
+ *     requantized code the other way changes every later matvec's outputs,
+ *     so on deep models the step's results drift well beyond the last bits
+ *     (TinyLlama, 22 layers: logits rel-L2 ~0.04).  Prefill, the op-by-op path
+ *     (fp16 activations, layer_norm) and the ops API stay ordered.
+ * Takes effect on the next decode step. */
+#define NC_REDUCE_ORDERED 0
+#define NC_REDUCE_TREE 1
+int nc_model_set_reduce(void* model, int mode);
 /* Residual stream after `layer` at `row`, in the reference's byte layout. */
 int nc_model_layer_out(void* model, int layer, int row, void* ref_bytes);
 /* greedy_sample (src/gten/sampler.cpp:11-60) without the tokenizer: prefill

@@ -22,6 +22,7 @@ W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN = range(7)
 W_ATTN_NORM, W_ATTN_NORM_B, W_MLP_NORM, W_MLP_NORM_B = 7, 8, 9, 10
 W_Q_BIAS, W_K_BIAS, W_V_BIAS, W_Q_NORM, W_K_NORM = 11, 12, 13, 14, 15
 TID_EMB, TID_NORM, TID_NORM_B, TID_LM = 0xFFFF0, 0xFFFF1, 0xFFFF2, 0xFFFF3
+REDUCE_ORDERED, REDUCE_TREE = 0, 1
 
 
 class HipError(RuntimeError):
@@ -145,6 +146,7 @@ def lib():
         "nc_tokenizer_decode": (C.c_char_p, [VP, I, I]),
         "nc_tokenizer_eos": (I, [VP]),
         "nc_tokenizer_free": (I, [VP]),
+        "nc_model_set_reduce": (I, [VP, I]),
         "nc_model_layer_out": (I, [VP, I, I, VP]), "nc_model_generate": (I, [VP, VP, I, I, VP, C.POINTER(I)]),
         "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
         "nc_model_profile_begin": (I, [VP, I]),
@@ -309,6 +311,11 @@ class Model:
         check(lib().nc_model_logits(self.h, _ptr(toks), len(toks), start_pos, _ptr(out)), "logits")
         return out
 
+    def set_reduce(self, mode):
+        """Reduction order of the decode step: REDUCE_ORDERED (the
+        reference's bits) or REDUCE_TREE (tree sums, within rel-L2 1e-3)."""
+        check(lib().nc_model_set_reduce(self.h, int(mode)), "set_reduce")
+
     def layer_out(self, layer, row):
         import numpy as np
         adt = F16 if self.cfg.wdtype == F16 else Q8
@@ -339,8 +346,16 @@ class Model:
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         check(lib().nc_model_prefill(self.h, _ptr(p), len(p)), "prefill")
 
-    def decode(self, n_steps):
-        check(lib().nc_model_decode(self.h, n_steps, None), "decode")
+    def decode(self, n_steps, fetch=False):
+        """n_steps more greedy steps; with fetch, returns every token
+        generated since the prompt (the first one included)."""
+        if not fetch:
+            check(lib().nc_model_decode(self.h, n_steps, None), "decode")
+            return None
+        import numpy as np
+        out = np.zeros(self.cfg.max_ctx + 1, np.int32)
+        check(lib().nc_model_decode(self.h, n_steps, _ptr(out)), "decode")
+        return out
 
     def profile_begin(self, max_launches):
         check(lib().nc_model_profile_begin(self.h, max_launches), "profile_begin")

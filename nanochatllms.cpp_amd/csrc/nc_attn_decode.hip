@@ -91,7 +91,7 @@ __device__ __forceinline__ float wave_max(float v)
 // at the start (every slot, so the load counts are static and the waits
 // exact); positions past them are read in the loops after.  The launcher
 // sizes them to the cache: issuing the loads is itself a cost.
-template <bool QKNORM, int MK, int MV>
+template <bool QKNORM, int MK, int MV, bool TR>
 __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict__ raw, int hq, int hkv,
                                                          const uint16_t* __restrict__ qn_w,
                                                          const uint16_t* __restrict__ kn_w,
@@ -246,14 +246,28 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     if (lane == 0) red[w] = mx;
     lds_barrier();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int c = tid; c < n; c += kAdThreads) S[c] = expf_ref(S[c] - mx);
-    lds_barrier();
-    if (w == 0) {
-        const float sum = seq_sum(S, n);
-        if (lane == 0) red[4] = sum;
+    float tsum = 0.0f;  // tree mode: this thread's share of the sum
+    for (int c = tid; c < n; c += kAdThreads) {
+        const float e = expf_ref(S[c] - mx);
+        S[c] = e;
+        if (TR) tsum += e;
     }
-    lds_barrier();
-    const float sum = red[4];
+    float sum;
+    if (TR) {
+        // tree mode: wave sums, then the four waves' in a fixed order
+        tsum = group_sum(tsum, kWave);
+        if (lane == 0) red[4 + w] = tsum;
+        lds_barrier();
+        sum = (red[4] + red[5]) + (red[6] + red[7]);
+    } else {
+        lds_barrier();
+        if (w == 0) {
+            const float ss = seq_sum(S, n);
+            if (lane == 0) red[4] = ss;
+        }
+        lds_barrier();
+        sum = red[4];
+    }
     for (int c0 = 0; c0 < n; c0 += kAdThreads) {
         const int c = c0 + tid;
         const bool valid = c < n;
@@ -318,7 +332,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
 
 int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
                        const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur)
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur, bool tree)
 {
     if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "attention: %d query heads over %d kv heads", hq, hkv);
     if (max_ctx > kAdMaxK * kAdThreads) return fail(NC_ERR_ARG, "attention: context %d too long", max_ctx);
@@ -331,16 +345,20 @@ int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, 
     };
     // register slots for the cache's positions (K: one row per slot and
     // thread, V: a quarter row)
-    auto by_norm = [&](auto qk) {
-        constexpr bool QK = decltype(qk)::value;
-        if (max_ctx <= 128) go(k_attn_dec<QK, 1, 2>);
-        else if (max_ctx <= 256) go(k_attn_dec<QK, 1, 4>);
-        else if (max_ctx <= 320) go(k_attn_dec<QK, 2, 5>);
-        else if (max_ctx <= 512) go(k_attn_dec<QK, 2, 8>);
-        else go(k_attn_dec<QK, kAdMaxK, kAdMaxV>);
+    auto by_norm = [&](auto qk, auto tr) {
+        constexpr bool QK = decltype(qk)::value, TR = decltype(tr)::value;
+        if (max_ctx <= 128) go(k_attn_dec<QK, 1, 2, TR>);
+        else if (max_ctx <= 256) go(k_attn_dec<QK, 1, 4, TR>);
+        else if (max_ctx <= 320) go(k_attn_dec<QK, 2, 5, TR>);
+        else if (max_ctx <= 512) go(k_attn_dec<QK, 2, 8, TR>);
+        else go(k_attn_dec<QK, kAdMaxK, kAdMaxV, TR>);
     };
-    if (qn_w) by_norm(std::true_type{});
-    else by_norm(std::false_type{});
+    auto by_mode = [&](auto qk) {
+        if (tree) by_norm(qk, std::true_type{});
+        else by_norm(qk, std::false_type{});
+    };
+    if (qn_w) by_mode(std::true_type{});
+    else by_mode(std::false_type{});
     return launch_status("k_attn_dec");
 }
 

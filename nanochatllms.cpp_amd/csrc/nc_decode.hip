@@ -114,7 +114,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx)
 // while the weights are in flight (LDS barriers do not wait for global
 // loads).  sq: K floats of LDS for the squares and the Act row.  Ends with
 // an LDS barrier.
-template <int PRO, int NCH, class LoadW>
+template <int PRO, int NCH, bool TR, class LoadW>
 __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, LoadW&& load_w)
 {
     const int tid = threadIdx.x;
@@ -166,6 +166,7 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
         load_w();
         __builtin_amdgcn_sched_barrier(0);
         if (fixed && A.dpos) pos = posv;
+        float tsq = 0.0f;  // tree mode: this thread's share of the sum of squares
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
@@ -196,12 +197,26 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
             if (valid) {
                 const float4 s0 = make_float4(h[j][0] * h[j][0], h[j][1] * h[j][1], h[j][2] * h[j][2], h[j][3] * h[j][3]);
                 const float4 s1 = make_float4(h[j][4] * h[j][4], h[j][5] * h[j][5], h[j][6] * h[j][6], h[j][7] * h[j][7]);
-                reinterpret_cast<float4*>(sq)[2 * ch] = s0;
-                reinterpret_cast<float4*>(sq)[2 * ch + 1] = s1;
+                if (TR) {
+                    tsq += ((s0.x + s0.y) + (s0.z + s0.w)) + ((s1.x + s1.y) + (s1.z + s1.w));
+                } else {
+                    reinterpret_cast<float4*>(sq)[2 * ch] = s0;
+                    reinterpret_cast<float4*>(sq)[2 * ch + 1] = s1;
+                }
             }
         }
-        lds_barrier();
-        const float ss = block_seq_sum_nonneg(sq, K, ssh);
+        float ss;
+        if (TR) {
+            // wave sums, then the four waves' in a fixed order
+            __shared__ float s_wsum[kDmvThreads / kWave];
+            tsq = group_sum(tsq, kWave);
+            if ((tid & (kWave - 1)) == 0) s_wsum[tid / kWave] = tsq;
+            lds_barrier();
+            ss = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
+        } else {
+            lds_barrier();
+            ss = block_seq_sum_nonneg(sq, K, ssh);
+        }
         const float denom = sqrtf(ss / (float)K) + 1e-6f;
         // the normalized row as stored (codes, then deltas) over sq's bytes
 #pragma unroll
@@ -300,7 +315,10 @@ __device__ __forceinline__ void next_step_inputs(const DmvArgs& A, int tok, int 
                 reinterpret_cast<const float2*>(A.rope_table)[(size_t)(pos + 1) * A.rope_half + tid];
 }
 
-template <int WT, int IT, int PRO, int EPI, int NCH>
+// Tree mode (TR): an item's four lane terms are added into one block term,
+// and each row's block terms are summed by kDmvThreads / R lanes (strided,
+// then xor butterflies) instead of four sequential lane chains.
+template <int WT, int IT, int PRO, int EPI, int NCH, bool TR>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
@@ -336,7 +354,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     };
     const int G = gridDim.x;
     int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
-    const int pos = dmv_prologue<PRO, NCH>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
+    const int pos = dmv_prologue<PRO, NCH, TR>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
 
     // EPI_ARGMAX: each row's lane-0 thread keeps the best key of its rows
     unsigned long long best = 0;
@@ -352,12 +370,31 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             const int r = j / nb, i = j - r * nb;
             float tv[4];
             q_block_terms<WT>(xs + i * kStage, wc[it], dc[it], tv);
-            float* t = T + r * 4 * tp + i;
+            if (TR) {
+                T[r * tp + i] = (tv[0] + tv[1]) + (tv[2] + tv[3]);
+            } else {
+                float* t = T + r * 4 * tp + i;
 #pragma unroll
-            for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
+                for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
+            }
         }
         lds_barrier();
-        if (tid < 4 * R) {
+        if (TR) {
+            // R divides the workgroup (R in {4, 8, 16, 32}): lanes per row 8..64
+            const int P = kDmvThreads / R;
+            const int r = tid / P, sub = tid - r * P;
+            float acc = 0.0f;
+            for (int i = sub; i < nb; i += P) acc += T[r * tp + i];
+            acc = group_sum(acc, P);
+            const int row = g * R + r;
+            if (sub == 0 && row < A.N) {
+                A.raw[row] = acc;
+                if (EPI == EPI_ARGMAX) {
+                    const unsigned long long key = argmax_key(acc, row);
+                    best = key > best ? key : best;
+                }
+            }
+        } else if (tid < 4 * R) {
             // thread 4r + k folds lane k of row r in block order
             const float acc = seq_sum<16>(T + tid * tp, nb);
             // lanes 4r..4r+3 hold row r's four lane sums; lane 4r reads
@@ -396,7 +433,8 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
         unsigned long long* sub = A.amax + 64;
         unsigned long long* cnt = A.amax + 192;
         unsigned long long* slot = A.amax + 320;
-        const int fold_waves = (4 * R + kWave - 1) / kWave;
+        // row results sit on lanes 4r (ordered) or on every wave (tree)
+        const int fold_waves = TR ? kDmvThreads / kWave : (4 * R + kWave - 1) / kWave;
         if (tid < fold_waves * kWave) {
 #pragma unroll
             for (int o = 4; o < kWave; o <<= 1) {
@@ -476,7 +514,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
 // block (tinyllama/tinyllama.cpp:88-97).  No workgroup waits for another.
 constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / 256 threads, NB <= 72
 
-template <int WT, int PRO, int NCH, int NB>
+template <int WT, int PRO, int NCH, int NB, bool TR>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
@@ -511,7 +549,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks
     DmvArgs P = A;
     P.nb = NB;
-    dmv_prologue<PRO, NCH>(P, xs, sq, ssh, [&] { load_block(b); });
+    dmv_prologue<PRO, NCH, TR>(P, xs, sq, ssh, [&] { load_block(b); });
 
     // the terms of all 64 rows, then the gate rows' folds (waves 0-1) and
     // the up rows' folds (waves 2-3) side by side
@@ -530,13 +568,27 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
                 q_block_terms<WT>(x0, w[it], dw[it], tv);
             else
                 q_block_terms<WT>(xs + i * kStage, w[it], dw[it], tv);
-            float* t = T + r * 4 * TP + i;
+            if (TR) {
+                T[r * TP + i] = (tv[0] + tv[1]) + (tv[2] + tv[3]);
+            } else {
+                float* t = T + r * 4 * TP + i;
 #pragma unroll
-            for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
+                for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
+            }
         }
         lds_barrier();
         {
-            const float acc = seq_sum<16>(T + tid * TP, NB);
+            // ordered: thread 4r + k folds lane k of row r in block order;
+            // tree: it sums blocks k, k + 4, ... of row r
+            float acc;
+            if (TR) {
+                const float* t = T + (tid >> 2) * TP;
+                acc = 0.0f;
+#pragma unroll 4
+                for (int i = tid & 3; i < NB; i += 4) acc += t[i];
+            } else {
+                acc = seq_sum<16>(T + tid * TP, NB);
+            }
             const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
             if ((tid & 3) == 0) {
                 const int r = tid >> 2;  // 0..31 gate, 32..63 up
@@ -605,10 +657,10 @@ DmvShape dmv_shape(int nb, int N, bool norm)
     return {best, false};
 }
 
-template <int WT, int IT, int PRO, int EPI, int NCH>
+template <int WT, int IT, int PRO, int EPI, int NCH, bool TR>
 int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv<WT, IT, PRO, EPI, NCH>;
+    auto kern = k_dmv<WT, IT, PRO, EPI, NCH, TR>;
     static int max_grid = 0;  // per instantiation: workgroups resident at once
     if (!max_grid) {
         int per_cu = 0;
@@ -626,10 +678,10 @@ int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, h
     return launch_status("k_dmv");
 }
 
-template <int WT, int PRO, int NCH, int NB>
+template <int WT, int PRO, int NCH, int NB, bool TR>
 int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv_glu<WT, PRO, NCH, NB>;
+    auto kern = k_dmv_glu<WT, PRO, NCH, NB, TR>;
     static int max_grid = 0;
     if (!max_grid) {
         int per_cu = 0;
@@ -646,21 +698,21 @@ int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
 }
 
 // Launch with the items per thread the group needs (1, 2, 4, 8 or 12).
-template <int WT, int PRO, int EPI, int NCH>
+template <int WT, int PRO, int EPI, int NCH, bool TR>
 int dmv_r(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     const int tp = ((A.nb + 3) & ~3) + 4;
     const size_t lds = lds0 + (size_t)sh.rows * 4 * tp * 4;
     A.rows = sh.rows;
     const int items = (sh.rows * A.nb + kDmvThreads - 1) / kDmvThreads;
-    if (items <= 1) return dmv_go<WT, 1, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
-    if (items <= 2) return dmv_go<WT, 2, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
-    if (items <= 4) return dmv_go<WT, 4, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
-    if (items <= 8) return dmv_go<WT, 8, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
-    return dmv_go<WT, 12, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 1) return dmv_go<WT, 1, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 2) return dmv_go<WT, 2, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 4) return dmv_go<WT, 4, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 8) return dmv_go<WT, 8, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
+    return dmv_go<WT, 12, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
 }
 
-template <int WT>
+template <int WT, bool TR>
 int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     const size_t K = (size_t)A.nb * 32;
@@ -675,25 +727,25 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
         const size_t lds = lds0 + (size_t)64 * 4 * tp * 4;
         // gate|up rows of 2048 (64 blocks) or 2304 (72 blocks) values
         if (A.nb == 64) {
-            if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64>(A, lds, st, ev0, ev1);
-            return glu_go<WT, PRO_RES_RMS, 1, 64>(A, lds, st, ev0, ev1);
+            if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64, TR>(A, lds, st, ev0, ev1);
+            return glu_go<WT, PRO_RES_RMS, 1, 64, TR>(A, lds, st, ev0, ev1);
         }
-        if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72>(A, lds, st, ev0, ev1);
-        return glu_go<WT, PRO_RES_RMS, 2, 72>(A, lds, st, ev0, ev1);
+        if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72, TR>(A, lds, st, ev0, ev1);
+        return glu_go<WT, PRO_RES_RMS, 2, 72, TR>(A, lds, st, ev0, ev1);
     }
-    if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
+    if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1, TR>(A, lds0, R, st, ev0, ev1);
     if (epi == EPI_ARGMAX) {
         if (pro == PRO_RMS)
-            return two ? dmv_r<WT, PRO_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
-                       : dmv_r<WT, PRO_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
-        return two ? dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
-                   : dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
+            return two ? dmv_r<WT, PRO_RMS, EPI_ARGMAX, 2, TR>(A, lds0, R, st, ev0, ev1)
+                       : dmv_r<WT, PRO_RMS, EPI_ARGMAX, 1, TR>(A, lds0, R, st, ev0, ev1);
+        return two ? dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 2, TR>(A, lds0, R, st, ev0, ev1)
+                   : dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 1, TR>(A, lds0, R, st, ev0, ev1);
     }
     if (pro == PRO_RMS)
-        return two ? dmv_r<WT, PRO_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
-                   : dmv_r<WT, PRO_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
-    return two ? dmv_r<WT, PRO_RES_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
-               : dmv_r<WT, PRO_RES_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
+        return two ? dmv_r<WT, PRO_RMS, EPI_RAW, 2, TR>(A, lds0, R, st, ev0, ev1)
+                   : dmv_r<WT, PRO_RMS, EPI_RAW, 1, TR>(A, lds0, R, st, ev0, ev1);
+    return two ? dmv_r<WT, PRO_RES_RMS, EPI_RAW, 2, TR>(A, lds0, R, st, ev0, ev1)
+               : dmv_r<WT, PRO_RES_RMS, EPI_RAW, 1, TR>(A, lds0, R, st, ev0, ev1);
 }
 
 }  // namespace
@@ -715,7 +767,11 @@ int decode_matvec(const DmvArgs& A, int wdtype, int pro, int epi, hipStream_t st
     if (!decode_matvec_supported(wdtype, A.nb * 32, A.N, pro, epi))
         return fail(NC_ERR_ARG, "decode matvec: unsupported [%d x %d] dtype %d prologue %d epilogue %d", A.N,
                     A.nb * 32, wdtype, pro, epi);
-    return wdtype == NC_Q4 ? dmv_dispatch<Q4>(A, pro, epi, st, ev0, ev1) : dmv_dispatch<Q8>(A, pro, epi, st, ev0, ev1);
+    if (A.tree)
+        return wdtype == NC_Q4 ? dmv_dispatch<Q4, true>(A, pro, epi, st, ev0, ev1)
+                               : dmv_dispatch<Q8, true>(A, pro, epi, st, ev0, ev1);
+    return wdtype == NC_Q4 ? dmv_dispatch<Q4, false>(A, pro, epi, st, ev0, ev1)
+                           : dmv_dispatch<Q8, false>(A, pro, epi, st, ev0, ev1);
 }
 
 // The next step's inputs for a token another kernel chose: the position is

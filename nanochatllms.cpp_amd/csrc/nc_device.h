@@ -166,6 +166,26 @@ __device__ __forceinline__ float q8_roundtrip_lane(float x, bool valid)
 
 __device__ __forceinline__ float f16_roundtrip(float x) { return h2f(f2h(x)); }
 
+// Sum over aligned groups of g lanes (g a power of two, 1..64; uniform; all
+// lanes of the wave active) in a fixed tree order: quad_perm xor 1 and xor 2,
+// row_half_mirror (lane i with 7 - i) and row_mirror (i with 15 - i) DPP
+// moves, a ds_swizzle for xor 16, the two half-waves' lane 0 for 64.  Each
+// step adds two partial sums that are the same pair on both lanes, so every
+// lane of a group ends with the same bits.  This is the reduction of the tree
+// mode, which gives up the reference's sequential orders.
+__device__ __forceinline__ float group_sum(float v, int g)
+{
+    if (g >= 2) v += dpp_f<kDppQuadXor1>(v);
+    if (g >= 4) v += dpp_f<kDppQuadXor2>(v);
+    if (g >= 8) v += dpp_f<0x141>(v);
+    if (g >= 16) v += dpp_f<0x140>(v);
+    if (g >= 32) v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    if (g >= 64)
+        v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    return v;
+}
+
 // Sequential fp32 sum of buf[0..n) in index order, every calling lane
 // reading the same addresses (an LDS broadcast), so every lane ends with the
 // sum.  This is the scalar accumulation loop of the reference's norms and

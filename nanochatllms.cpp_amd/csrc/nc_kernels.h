@@ -81,9 +81,11 @@ int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k
 // rows are appended to the caches at the position (*dpos when set, else
 // pos); out = the attention output Act row.  rope_cur, when set, is the
 // position's RoPE (cos, sin) row at a fixed address (read instead of the
-// table row, so that load does not wait for the position).
+// table row, so that load does not wait for the position).  tree: the
+// softmax denominator is summed as a tree, not in position order.
 int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
                        const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur = nullptr);
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur = nullptr,
+                       bool tree = false);
 
 }  // namespace nc

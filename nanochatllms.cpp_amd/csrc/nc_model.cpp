@@ -99,6 +99,9 @@ public:
     // shapes allow it (Q8 activations, RMS norms); NC_DECODE_FUSED=0 keeps
     // the op-by-op path.
     bool fused = false;
+    // Reduction order of the fused decode step: NC_REDUCE_ORDERED (the
+    // reference's sequential sums, bit-exact) or NC_REDUCE_TREE.
+    int reduce = NC_REDUCE_ORDERED;
     unsigned long long* am_scratch = nullptr;  // zeroed argmax scratch of the greedy step
     // Top-k sampling: the lm head writes logits only (sample_head), and the
     // sampler draws from the device-held mt19937 state rng (625 words).
@@ -747,9 +750,11 @@ public:
         if (!dpos && (s = embed_launch(&emb, tokens + pos, x0 + (size_t)pos * pd, pd, adt, 1, minicpm ? 12.0f : 1.0f,
                                        st, nullptr, cur_x0)))
             return s;
+        const bool tree = reduce == NC_REDUCE_TREE;
         DmvArgs base;
         base.pos = pos;
         base.dpos = dpos;
+        base.tree = tree;
         base.res_pitch = pd;
         base.bscale = bs;
         for (int l = 0; l < cfg.n_layers; l++) {
@@ -773,7 +778,7 @@ public:
             }
             if (!y.bq) {
                 if ((s = attn_decode_launch(qkv_raw, y.hq, y.hkv, y.qn, y.kn, rope, d_half, pos, dpos, y.kc, y.vc, pkv,
-                                            attn, cfg.max_ctx, st, dpos ? cur_rope : nullptr)))
+                                            attn, cfg.max_ctx, st, dpos ? cur_rope : nullptr, tree)))
                     return s;
             } else {
                 if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half,
@@ -1046,6 +1051,22 @@ public:
         return NC_OK;
     }
 
+    // A new reduction order for the fused decode step; captured step graphs
+    // hold the old kernels and are captured again on their next use.
+    int set_reduce(int mode)
+    {
+        NC_CHECK_ARG(mode == NC_REDUCE_ORDERED || mode == NC_REDUCE_TREE, "set_reduce: mode %d", mode);
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "set_reduce");
+        if (mode == reduce) return NC_OK;
+        reduce = mode;
+        if (step_graph) (void)hipGraphExecDestroy(step_graph);
+        if (sample_graph) (void)hipGraphExecDestroy(sample_graph);
+        step_graph = nullptr;
+        sample_graph = nullptr;
+        return NC_OK;
+    }
+
     int layer_out(int layer, int row, void* ref)
     {
         NC_CHECK_ARG(layer >= 0 && layer < cfg.n_layers && row >= 0 && row < cfg.max_ctx, "layer_out: %d/%d", layer,
@@ -1113,6 +1134,12 @@ int nc_model_logits(void* model, const int32_t* tokens, int n_tokens, int start_
 {
     NC_CHECK_ARG(model, "model: null");
     return static_cast<Decoder*>(model)->logits_call(tokens, n_tokens, start_pos, logits);
+}
+
+int nc_model_set_reduce(void* model, int mode)
+{
+    NC_CHECK_ARG(model, "model: null");
+    return static_cast<Decoder*>(model)->set_reduce(mode);
 }
 
 int nc_model_layer_out(void* model, int layer, int row, void* ref_bytes)
