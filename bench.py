@@ -127,7 +127,7 @@ def traffic_for(workload, kernel_role):
     return None if e is None else e.get("bytes_per_launch")
 
 
-def kernel_table(ms, nbytes, kind):
+def kernel_table(ms, nbytes, kind, wdtype):
     """Per matvec role: launches, total and average launch time, bytes per
     launch and the achieved rate."""
     out = []
@@ -137,7 +137,8 @@ def kernel_table(ms, nbytes, kind):
         fused = bool(k & nc.PROF_FUSED)
         avg_ms = float(ms[sel].mean())
         avg_b = float(nbytes[sel].mean())
-        out.append({"role": role, "kernel": FUSED_KERNEL[role] if fused else "k_matvec_q",
+        unfused = "k_matvec_f16_row (fp16 decode matvec)" if wdtype == nc.F16 else "k_matvec_q"
+        out.append({"role": role, "kernel": FUSED_KERNEL[role] if fused else unfused,
                     "launches": int(sel.sum()), "total_ms": round(float(ms[sel].sum()), 4),
                     "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(avg_b),
                     "achieved_gbs": round(avg_b / (avg_ms * 1e-3) / 1e9, 1)})
@@ -260,7 +261,7 @@ def main():
     ms, nbytes, kind = model.profile_launches(launches_per_step * args.steps)
     model.close()
 
-    per_kernel = kernel_table(ms, nbytes, kind)
+    per_kernel = kernel_table(ms, nbytes, kind, cfg.wdtype)
     dom = max(per_kernel, key=lambda e: e["total_ms"])
     traffic = traffic_for(args.workload, dom["role"])
 
@@ -304,7 +305,7 @@ def main():
                                 "moved in the last layer's row, logits rel-L2)"},
     }
     if tree_ms is not None:
-        tk = kernel_table(tree_ms, tree_b, tree_kind)
+        tk = kernel_table(tree_ms, tree_b, tree_kind, cfg.wdtype)
         line["tree_reduce"]["per_kernel"] = [{k: e[k] for k in ("role", "avg_launch_us", "achieved_gbs")} for e in tk]
         tdom = next((e for e in tk if e["role"] == dom["role"]), None)
         if tdom:
