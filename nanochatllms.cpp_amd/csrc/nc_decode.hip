@@ -315,6 +315,100 @@ __device__ __forceinline__ void next_step_inputs(const DmvArgs& A, int tok, int 
                 reinterpret_cast<const float2*>(A.rope_table)[(size_t)(pos + 1) * A.rope_half + tid];
 }
 
+// The greedy-token epilogue: `best` holds this thread's largest argmax key
+// (0 where it holds no row result; result lanes are multiples of 4 within
+// the first fold_waves waves).  Two-level reduction over the workgroups;
+// the workgroup that finds the token writes it (and the next step's inputs).
+template <int WT, int NCH>
+__device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long long best, int pos, int fold_waves,
+                                                unsigned long long* s_key, int* s_tok_p)
+{
+    const int tid = threadIdx.x;
+    const int G = gridDim.x;
+    int& s_tok = *s_tok_p;
+
+    // Two-level reduction over the workgroups: keys in slots, the last
+    // of each 32 workgroups reduces its slots, the last of those the
+    // rest.  Agent-scope stores and loads are coherent across the XCDs'
+    // L2s without a cache flush; the workgroup fences order each
+    // thread's own accesses.  Scratch layout (64-bit words): [0] top
+    // counter, [64, 192) level-1 results, [192, 320) level-1 counters,
+    // [320, 320 + grid) workgroup keys.
+    unsigned long long* top = A.amax;
+    unsigned long long* sub = A.amax + 64;
+    unsigned long long* cnt = A.amax + 192;
+    unsigned long long* slot = A.amax + 320;
+    if (tid < fold_waves * kWave) {
+#pragma unroll
+        for (int o = 4; o < kWave; o <<= 1) {
+            const unsigned long long other = __shfl_xor(best, o);
+            best = other > best ? other : best;
+        }
+        if ((tid & (kWave - 1)) == 0) s_key[tid / kWave] = best;
+    }
+    if (tid == 0) s_tok = -1;
+    lds_barrier();
+    if (tid == 0)
+        for (int w = 1; w < fold_waves; w++) best = s_key[w] > best ? s_key[w] : best;
+    const int grp = blockIdx.x >> 5;
+    const int ngrp = (G + 31) >> 5;
+    if (tid < kWave) {
+        unsigned long long done = 0;
+        if (tid == 0) {
+            __hip_atomic_store(slot + blockIdx.x, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            done = __hip_atomic_fetch_add(cnt + grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const int members = min(32, G - grp * 32);
+        done = __shfl(done, 0);
+        if (done == (unsigned long long)members - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            unsigned long long k = tid < members
+                    ? __hip_atomic_load(slot + grp * 32 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                    : 0ull;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const unsigned long long other = __shfl_xor(k, o);
+                k = other > k ? other : k;
+            }
+            unsigned long long done2 = 0;
+            if (tid == 0) {
+                __hip_atomic_store(cnt + grp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(sub + grp, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                done2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            done2 = __shfl(done2, 0);
+            if (done2 == (unsigned long long)ngrp - 1) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                unsigned long long b2 = 0;
+                for (int q = tid; q < ngrp; q += kWave) {
+                    const unsigned long long o = __hip_atomic_load(sub + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    b2 = o > b2 ? o : b2;
+                }
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) {
+                    const unsigned long long other = __shfl_xor(b2, o);
+                    b2 = other > b2 ? other : b2;
+                }
+                if (tid == 0) {
+                    const int tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull));
+                    A.tokens[pos + 1] = tok;
+                    if (A.dpos) A.pos_out[0] = pos + 1;
+                    __hip_atomic_store(top, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    s_tok = tok;
+                }
+            }
+        }
+    }
+    if (A.emb_codes) {
+        // the workgroup that found the token prepares the next step
+        lds_barrier();
+        const int tok = s_tok;
+        if (tok >= 0) next_step_inputs<WT, NCH>(A, tok, pos);
+    }
+}
+
 // Tree mode (TR): an item's four lane terms are added into one block term,
 // and each row's block terms are summed by kDmvThreads / R lanes (strided,
 // then xor butterflies) instead of four sequential lane chains.
@@ -422,88 +516,174 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     }
 
     if (EPI == EPI_ARGMAX) {
-        // Two-level reduction over the workgroups: keys in slots, the last
-        // of each 32 workgroups reduces its slots, the last of those the
-        // rest.  Agent-scope stores and loads are coherent across the XCDs'
-        // L2s without a cache flush; the workgroup fences order each
-        // thread's own accesses.  Scratch layout (64-bit words): [0] top
-        // counter, [64, 192) level-1 results, [192, 320) level-1 counters,
-        // [320, 320 + grid) workgroup keys.
-        unsigned long long* top = A.amax;
-        unsigned long long* sub = A.amax + 64;
-        unsigned long long* cnt = A.amax + 192;
-        unsigned long long* slot = A.amax + 320;
         // row results sit on lanes 4r (ordered) or on every wave (tree)
-        const int fold_waves = TR ? kDmvThreads / kWave : (4 * R + kWave - 1) / kWave;
-        if (tid < fold_waves * kWave) {
+        argmax_epilogue<WT, NCH>(A, best, pos, TR ? kDmvThreads / kWave : (4 * R + kWave - 1) / kWave, s_key,
+                                 &s_tok);
+    }
+}
+
+// Tall Q4 launches (a lm head of ~100k rows): each thread runs one (row,
+// lane) chain of the reference's fold itself, acc_k += t_k(i) for blocks i
+// in order, from its lane's weight dword and the staged activation block,
+// so the fold needs no LDS terms and no workgroup barriers.  A wavefront
+// holds 16 rows x 4 lanes, a workgroup 64 rows (a group); workgroups walk
+// groups g, g + grid, ...  Weights stream in chunks of 8 blocks, kRwDepth
+// chunks ahead across group boundaries: the four threads of a row load the
+// chunk's 128 contiguous bytes (streaming loads, every line used whole),
+// pass them through a wavefront-private LDS slice so each takes its lane's
+// dword of every block, and share the chunk's deltas by quad broadcast.  The
+// four lanes of a row then combine as (a0 + a1) + (a2 + a3) (the two
+// _mm_hadd_ps of gten/ops.cpp:358-360).
+constexpr int kRwRows = 64;   // rows per group: 4 wavefronts x 16 rows
+constexpr int kRwChunk = 8;   // blocks per chunk (nb % 8 == 0)
+constexpr int kRwDepth = 4;   // chunks in flight per thread
+
+template <int WT, int PRO, int EPI, int NCH, bool TR>
+__global__ __launch_bounds__(kDmvThreads) void k_dmv_rows(DmvArgs A)
+{
+    constexpr int WW = WT == Q4 ? 1 : 2;        // code dwords of one lane and block
+    constexpr int CV = WT == Q4 ? 2 : 4;        // 16-byte code loads per lane and chunk
+    constexpr int RS = WT == Q4 ? 36 : 68;      // LDS dwords per row of a chunk (32 / 64 used)
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ SsShared ssh;
+    __shared__ unsigned long long s_key[4];
+    __shared__ int s_tok;
+    const int nb = A.nb, K = nb * 32;
+    uint32_t* xs = lds;                                         // staged row: nb * kStage dwords
+    float* sq = reinterpret_cast<float*>(xs + nb * kStage);    // prologue scratch: K floats
+    uint32_t* wl = reinterpret_cast<uint32_t*>(sq + K);        // per wavefront: 16 rows x RS dwords
+    float* res = reinterpret_cast<float*>(wl + 4 * 16 * RS);   // row results: 64 per owned group
+    const int tid = threadIdx.x;
+    const int k = tid & 3;                                     // the thread's lane
+    const int rr = (tid & 63) >> 2;                            // its row within the wavefront
+    const int wrow = (tid >> 6) * 16 + rr;                     // its row within a group
+    uint32_t* wrow_lds = wl + (tid >> 6) * 16 * RS + rr * RS;  // its row's chunk in LDS
+    const int G = gridDim.x;
+    const int nch = nb / kRwChunk;                             // >= kRwDepth (launcher)
+    const int mine = (A.ngroups - (int)blockIdx.x + G - 1) / G;  // groups this workgroup owns
+    const int total = mine * nch;                              // its chunks, >= kRwDepth
+
+    // a chunk of a row is 8 blocks: thread (row, k) loads blocks 2k and 2k+1
+    // (contiguous, so a row's chunk is one coalesced span) and the two
+    // deltas of those blocks
+    uint4 wc[kRwDepth][CV];
+    uint32_t wd[kRwDepth];
+    // chunk j of this workgroup's stream: rows past N read row 0 (their
+    // results are not stored).  Every call issues the same loads, and no
+    // other global access sits between the issues and the waits, so the
+    // waits for a chunk are exact counts.
+    auto issue = [&](int j, uint4(&q)[CV], uint32_t& d) {
+        const int gi = j / nch;
+        const int c = j - gi * nch;
+        const int row = ((int)blockIdx.x + gi * G) * kRwRows + wrow;
+        const size_t b0 = (size_t)(row < A.N ? row : 0) * nb + (size_t)c * kRwChunk + 2 * k;
+        const uint4* src = reinterpret_cast<const uint4*>(A.wq + b0 * (WT == Q4 ? 4 : 8));
 #pragma unroll
-            for (int o = 4; o < kWave; o <<= 1) {
-                const unsigned long long other = __shfl_xor(best, o);
-                best = other > best ? other : best;
-            }
-            if ((tid & (kWave - 1)) == 0) s_key[tid / kWave] = best;
-        }
-        if (tid == 0) s_tok = -1;
-        lds_barrier();
-        if (tid == 0)
-            for (int w = 1; w < fold_waves; w++) best = s_key[w] > best ? s_key[w] : best;
-        const int grp = blockIdx.x >> 5;
-        const int ngrp = (G + 31) >> 5;
-        if (tid < kWave) {
-            unsigned long long done = 0;
-            if (tid == 0) {
-                __hip_atomic_store(slot + blockIdx.x, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                done = __hip_atomic_fetch_add(cnt + grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            const int members = min(32, G - grp * 32);
-            done = __shfl(done, 0);
-            if (done == (unsigned long long)members - 1) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                unsigned long long k = tid < members
-                        ? __hip_atomic_load(slot + grp * 32 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                        : 0ull;
+        for (int v = 0; v < CV; v++) q[v] = load_stream(src + v);
+        // the deltas (a ninth of the bytes) keep the default policy: the
+        // chunks after this one read the rest of their line
+        d = *reinterpret_cast<const uint32_t*>(A.wd + b0);
+    };
+    const int pos = dmv_prologue<PRO, NCH, TR>(A, xs, sq, ssh, [&] {
 #pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) {
-                    const unsigned long long other = __shfl_xor(k, o);
-                    k = other > k ? other : k;
-                }
-                unsigned long long done2 = 0;
-                if (tid == 0) {
-                    __hip_atomic_store(cnt + grp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(sub + grp, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                    done2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                done2 = __shfl(done2, 0);
-                if (done2 == (unsigned long long)ngrp - 1) {
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                    unsigned long long b2 = 0;
-                    for (int q = tid; q < ngrp; q += kWave) {
-                        const unsigned long long o = __hip_atomic_load(sub + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        b2 = o > b2 ? o : b2;
-                    }
+        for (int b = 0; b < kRwDepth; b++) issue(b, wc[b], wd[b]);
+    });
+
+    float acc = 0.0f;
+    // chunk j from buffer b: this lane's chain over the chunk's 8 blocks;
+    // at a group's last chunk lane 4r combines row r into res
+    auto consume = [&](int j, const uint4(&q)[CV], uint32_t d) {
+        const int gi = j / nch;
+        const int c = j - gi * nch;
+        // the row's chunk through this wavefront's LDS slice: lane k then
+        // reads its own dword(s) of each block (wavefront-private, and LDS
+        // operations of a wavefront complete in order)
 #pragma unroll
-                    for (int o = 32; o >= 1; o >>= 1) {
-                        const unsigned long long other = __shfl_xor(b2, o);
-                        b2 = other > b2 ? other : b2;
-                    }
-                    if (tid == 0) {
-                        const int tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull));
-                        A.tokens[pos + 1] = tok;
-                        if (A.dpos) A.pos_out[0] = pos + 1;
-                        __hip_atomic_store(top, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        s_tok = tok;
-                    }
-                }
+        for (int v = 0; v < CV; v++) reinterpret_cast<uint4*>(wrow_lds + k * 4 * CV)[v] = q[v];
+        uint32_t qv[kRwChunk][WW];
+#pragma unroll
+        for (int e = 0; e < kRwChunk; e++) {
+            if (WW == 1) {
+                qv[e][0] = wrow_lds[e * 4 + k];
+            } else {
+                const uint2 t2 = *reinterpret_cast<const uint2*>(wrow_lds + e * 8 + 2 * k);
+                qv[e][0] = t2.x;
+                qv[e][WW - 1] = t2.y;
             }
         }
-        if (A.emb_codes) {
-            // the workgroup that found the token prepares the next step
-            lds_barrier();
-            const int tok = s_tok;
-            if (tok >= 0) next_step_inputs<WT, NCH>(A, tok, pos);
+        // the chunk's eight deltas: lane m holds those of blocks 2m, 2m + 1
+        const uint32_t dws[4] = {(uint32_t)dpp_i<0x00>((int)d), (uint32_t)dpp_i<0x55>((int)d),
+                                 (uint32_t)dpp_i<0xAA>((int)d), (uint32_t)dpp_i<0xFF>((int)d)};
+#pragma unroll
+        for (int e = 0; e < kRwChunk; e++) {
+            const uint32_t* st = xs + (c * kRwChunk + e) * kStage;
+            // this lane's staged codes, offset and the block's delta
+            const uint32_t xa = st[2 * k];
+            const uint32_t xb = st[2 * k + 1];
+            const int cx = (int)st[8 + k];
+            const float dx = __uint_as_float(st[12]);
+            const float dd = dx * h2f((uint16_t)(dws[e >> 1] >> (16 * (e & 1))));
+            int L;
+            if (WT == Q4) {
+                const uint32_t P = qv[e][0];
+                L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)xa, cx, false);
+                L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)xb, L, false);
+            } else {
+                L = __builtin_amdgcn_sdot4((int)qv[e][0], (int)xa, 0, false);
+                L = __builtin_amdgcn_sdot4((int)qv[e][WW - 1], (int)xb, L, false);
+            }
+            acc = acc + (float)L * dd;
         }
+        if (c == nch - 1) {
+            const float a1 = dpp_f<kDppQuadXor1>(acc);
+            const float a2 = dpp_f<kDppQuadXor2>(acc);
+            const float a3 = dpp_f<0x1B>(acc);
+            if (k == 0) res[gi * kRwRows + wrow] = (acc + a1) + (a2 + a3);
+            acc = 0.0f;
+        }
+    };
+    int j0 = 0;
+    // steady state: each consumed chunk's buffer takes the chunk kRwDepth on
+    for (; j0 + 2 * kRwDepth <= total; j0 += kRwDepth) {
+#pragma unroll
+        for (int b = 0; b < kRwDepth; b++) {
+            consume(j0 + b, wc[b], wd[b]);
+            issue(j0 + b + kRwDepth, wc[b], wd[b]);
+        }
+    }
+    // the last kRwDepth .. 2 kRwDepth - 1 chunks
+    const int rest = total - j0 - kRwDepth;  // 0 .. kRwDepth - 1 still to issue
+#pragma unroll
+    for (int b = 0; b < kRwDepth; b++) {
+        consume(j0 + b, wc[b], wd[b]);
+        if (b < rest) issue(j0 + b + kRwDepth, wc[b], wd[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < kRwDepth; b++)
+        if (b < rest) consume(j0 + kRwDepth + b, wc[b], wd[b]);
+
+    // the workgroup's row results out, and the greedy token
+    lds_barrier();
+    unsigned long long best = 0;
+    for (int t = tid; t < mine * kRwRows; t += kDmvThreads) {
+        const int row = ((int)blockIdx.x + (t / kRwRows) * G) * kRwRows + (t % kRwRows);
+        if (row < A.N) {
+            const float v = res[t];
+            A.raw[row] = v;
+            if (EPI == EPI_ARGMAX) {
+                const unsigned long long key = argmax_key(v, row);
+                best = key > best ? key : best;
+            }
+        }
+    }
+    if (EPI == EPI_ARGMAX) {
+        // argmax_epilogue reduces keys held on lanes 4r: fold each quad first
+        // (keys of one quad's lanes are distinct rows here)
+        unsigned long long o = __shfl_xor(best, 1);
+        best = o > best ? o : best;
+        o = __shfl_xor(best, 2);
+        best = o > best ? o : best;
+        argmax_epilogue<WT, NCH>(A, best, pos, kDmvThreads / kWave, s_key, &s_tok);
     }
 }
 
@@ -697,6 +877,48 @@ int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
     return launch_status("k_dmv_glu");
 }
 
+// Q4 launches with this many rows and a norm prologue (MiniCPM's tied lm
+// head, 122753 rows) run k_dmv_rows: 45% of HBM peak there against 35% for
+// k_dmv.  At 32000 rows the two kernels take the same time, and for Q8 (twice
+// the code bytes per chunk through LDS) k_dmv is faster.
+constexpr int kRwMinRows = 65536;
+
+template <int WT, int PRO, int EPI, int NCH, bool TR>
+int rows_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    auto kern = k_dmv_rows<WT, PRO, EPI, NCH, TR>;
+    // staged row, prologue scratch, then the row results of the groups a
+    // workgroup owns (occupancy taken with room for 8 groups)
+    const size_t lds0 = (size_t)A.nb * kStage * 4 + (size_t)A.nb * 32 * 4 + 4 * 16 * (WT == Q4 ? 36 : 68) * 4;
+    static int max_grid = 0;
+    if (!max_grid) {
+        int per_cu = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kDmvThreads,
+                                                                    lds0 + 8 * kRwRows * 4);
+        if (e != hipSuccess) return hip_fail(e, "decode matvec: occupancy");
+        max_grid = std::min(kDmvMaxGrid, std::max(1, per_cu) * device_cus());
+    }
+    A.rows = kRwRows;
+    A.ngroups = (A.N + kRwRows - 1) / kRwRows;
+    const int grid_n = std::min(A.ngroups, max_grid);  // every workgroup owns at least one group
+    const int per_wg = (A.ngroups + grid_n - 1) / grid_n;
+    const size_t lds = lds0 + (size_t)per_wg * kRwRows * 4;
+    if (lds > 64 * 1024) return fail(NC_ERR_ARG, "decode matvec: %d rows in too few workgroups", A.N);
+    const dim3 grid(grid_n);
+    if (ev0)
+        hipExtLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, ev0, ev1, 0, A);
+    else
+        hipLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, A);
+    return launch_status("k_dmv_rows");
+}
+
+template <int WT, int PRO, int EPI, bool TR>
+int rows_nch(const DmvArgs& A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    if (A.nb * 32 > kDmvThreads * 8) return rows_go<WT, PRO, EPI, 2, TR>(A, st, ev0, ev1);
+    return rows_go<WT, PRO, EPI, 1, TR>(A, st, ev0, ev1);
+}
+
 // Launch with the items per thread the group needs (1, 2, 4, 8 or 12).
 template <int WT, int PRO, int EPI, int NCH, bool TR>
 int dmv_r(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
@@ -732,6 +954,16 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
         }
         if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72, TR>(A, lds, st, ev0, ev1);
         return glu_go<WT, PRO_RES_RMS, 2, 72, TR>(A, lds, st, ev0, ev1);
+    }
+    if constexpr (WT == Q4) {
+        if (norm && epi != EPI_SWIGLU && A.N >= kRwMinRows && A.nb % kRwChunk == 0 && A.nb >= kRwChunk * kRwDepth) {
+            // tall launches (lm heads): one fold chain per thread
+            if (epi == EPI_ARGMAX)
+                return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_ARGMAX, TR>(A, st, ev0, ev1)
+                                      : rows_nch<WT, PRO_RES_RMS, EPI_ARGMAX, TR>(A, st, ev0, ev1);
+            return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_RAW, TR>(A, st, ev0, ev1)
+                                  : rows_nch<WT, PRO_RES_RMS, EPI_RAW, TR>(A, st, ev0, ev1);
+        }
     }
     if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1, TR>(A, lds0, R, st, ev0, ev1);
     if (epi == EPI_ARGMAX) {

@@ -25,6 +25,13 @@ __device__ __forceinline__ uint4 load_stream(const uint4* p)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint16_t load_stream(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint32_t load_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+typedef unsigned int NcU32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 load_stream(const uint2* p)
+{
+    const NcU32x2 v = __builtin_nontemporal_load(reinterpret_cast<const NcU32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
 
 // fp16 -> fp32, exact (gten/gten_types.h:129-133).
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
