@@ -106,7 +106,10 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     __shared__ __align__(16) float s_nrm[2][64];
     __shared__ float red[8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int h = blockIdx.x;
+    // workgroup i runs on XCD i % 8: with hq % 8 == 0, XCD x takes heads
+    // x * hq/8 .. (x + 1) * hq/8 - 1, so the query heads of one kv head share
+    // an XCD and its L2 fetches their K/V slice once (a bijection on [0, hq))
+    const int h = hq % 8 == 0 ? (int)(blockIdx.x % 8) * (hq / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const int gs = hq / hkv, g = h / gs;
     // this wave's raw q / k / v value does not depend on the position: it is
     // requested before the position is known
