@@ -21,6 +21,11 @@ the same figures for each matvec role.  `traffic` is the measured HBM bytes
 per launch of that kernel, from the committed rocprofv3 counter summary
 (profiles/traffic.json), when one exists for the workload.
 
+`tree_reduce` repeats the timed steps with nc_model_set_reduce(TREE) (tree
+sums instead of the reference's sequential ones; not bit-exact) and reports
+its rate, how many leading tokens equal the ordered stream, and one step of
+both modes on the same cache.
+
     python bench.py --copy-calibration MIB   (one plain copy of MIB MiB: the
                                               reference dispatch for the
                                               profiler's byte counters)
