@@ -6,25 +6,25 @@ Workload (default): TinyLlama-1.1B-shaped decoder, Q4 weights (Q8
 activations), vocab 32000, synthetic N(0, 0.02) weights generated on the
 device, a 64-token prompt and greedy decode with the KV cache growing to 320
 positions.  A step is one greedy decode step (Model::logits with start_pos =
-n - 1, device argmax, token fed back on the device).
+n - 1, device argmax, token fed back on the device), one replay of the
+captured decode-step graph.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
 
 Prints one JSON line.  `value` is decode tokens/s over exactly K timed steps
-(warmup steps run first, on the same sequence).  `roofline` is for the
+(warmup steps run first, on the same sequence); `config.timed_positions`
+gives the positions they cover.  `full_stream` times the workload's whole
+greedy stream (every decode step after the prompt) and compares its tokens
+with the reference's (tests/golden/<workload>.json).  `roofline` is for the
 kernel that takes the most time in a decode step (the fused gate|up matvec
-for the Q4/Q8 workloads): algorithmic bytes per launch (weights once +
-its input rows + its output rows) over the launch's average duration, both
-measured with HIP events on the model stream during a second pass over the
-same timed steps with every kernel launched directly; `per_kernel` gives
-the same figures for each matvec role.  `traffic` is the measured HBM bytes
-per launch of that kernel, from the committed rocprofv3 counter summary
-(profiles/traffic.json), when one exists for the workload.
-
-`tree_reduce` repeats the timed steps with nc_model_set_reduce(TREE) (tree
-sums instead of the reference's sequential ones; not bit-exact) and reports
-its rate, how many leading tokens equal the ordered stream, and one step of
-both modes on the same cache.
+for the Q4/Q8 workloads): algorithmic bytes per launch (weights once + its
+input rows + its output rows) over the launch's average duration, both
+measured with HIP events recorded by the dispatches on the model stream,
+during a second pass over the same timed steps with every kernel launched
+directly; `per_kernel` gives the same figures for each matvec role.
+`traffic` is the measured HBM bytes per launch of that kernel, from the
+committed rocprofv3 counter summary (profiles/traffic.json), when one exists
+for the workload.
 
     python bench.py --copy-calibration MIB   (one plain copy of MIB MiB: the
                                               reference dispatch for the
@@ -32,16 +32,30 @@ both modes on the same cache.
 """
 import argparse
 import ctypes as C
+import importlib.util
 import json
 import os
 import sys
 import time
 
-ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path.insert(0, os.path.join(ROOT, "tests"))
-import numpy as np  # noqa: E402
+import numpy as np
 
-from nc_pkg import nc  # noqa: E402
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "nanochatllms.cpp_amd")
+
+
+def _load_package():
+    if "nanochat_amd" in sys.modules:
+        return sys.modules["nanochat_amd"]
+    spec = importlib.util.spec_from_file_location("nanochat_amd", os.path.join(PKG_DIR, "__init__.py"),
+                                                  submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["nanochat_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+nc = _load_package()
 
 METRIC = "decode tok/s (1 GPU) + Q4/Q8 matvec HBM GB/s as % of MI355X peak"
 HBM_PEAK_GBS = 8000.0
@@ -51,10 +65,6 @@ FUSED_KERNEL = {"qkv": "k_dmv (qkv, residual add + rms_norm prologue)",
                 "gate_up": "k_dmv_glu (gate|up, residual add + rms_norm prologue, SwiGLU epilogue)",
                 "down": "k_dmv (down)",
                 "lm_head": "k_dmv (lm head, residual add + final norm prologue, greedy-token epilogue)"}
-
-
-def workload_config(name):
-    return nc.workload_config(name)
 
 
 def prompt_tokens(w):
@@ -75,11 +85,58 @@ def prompt_tokens(w):
     return np.array(out, np.int32)
 
 
+def host_info():
+    """The host CPUs this process may run on: model name, logical CPUs,
+    physical cores among them (distinct (package, core) pairs), their NUMA
+    nodes, and the GPU's NUMA node when sysfs names it."""
+    cpus = sorted(os.sched_getaffinity(0))
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cores, nodes = set(), set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}"
+        try:
+            with open(f"{base}/topology/physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(f"{base}/topology/core_id") as f:
+                core = f.read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            pass
+        try:
+            nodes.update(n[4:] for n in os.listdir(base) if n.startswith("node") and n[4:].isdigit())
+        except OSError:
+            pass
+    gpu_node = None
+    try:
+        for card in sorted(os.listdir("/sys/class/drm")):
+            p = f"/sys/class/drm/{card}/device/numa_node"
+            if card.startswith("card") and "-" not in card and os.path.exists(p):
+                with open(p) as f:
+                    gpu_node = int(f.read().strip())
+                break
+    except (OSError, ValueError):
+        pass
+    return {"cpu_model": model, "logical_cpus": len(cpus), "physical_cores": len(cores) or None,
+            "numa_nodes": sorted(int(n) for n in nodes), "gpu_numa_node": gpu_node,
+            "affinity": f"{cpus[0]}-{cpus[-1]}" if cpus else None}
+
+
 def cpu_baseline(w, prompt, budget_s=12.0):
     """The reference's own CPU path (oracle/_ref, built from its sources) on
     the same workload: untimed prefill, then greedy decode steps timed until
-    the budget is spent.  Falls back to the oracle restatement ("port")."""
-    import oracle_lib as OL
+    the budget is spent.  Falls back to the oracle restatement ("port").
+    The checker is loaded from tests/ for this leg only."""
+    spec = importlib.util.spec_from_file_location("oracle_lib", os.path.join(ROOT, "tests", "oracle_lib.py"))
+    OL = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(OL)
     kind = "reference" if OL.have_reference() else "port"
     lib = OL.Reference() if kind == "reference" else OL.Oracle()
     cfg = nc.workload_config(w["name"], cls=OL.Config)
@@ -97,10 +154,12 @@ def cpu_baseline(w, prompt, budget_s=12.0):
         steps += 1
     dt = time.perf_counter() - t0
     lib.model_free(m)
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    hi = host_info()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or hi["logical_cpus"]
     return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": kind,
             "sample": f"{steps} greedy decode steps after an untimed {len(prompt)}-token prefill "
-                      f"({dt:.1f} s), same weights and prompt, OpenMP threads = {threads}"}
+                      f"({dt:.1f} s), same weights and prompt, OpenMP threads = {threads}",
+            "host": hi}
 
 
 def copy_calibration(mib):
@@ -132,6 +191,15 @@ def traffic_for(workload, kernel_role):
     return None if e is None else e.get("bytes_per_launch")
 
 
+def reference_stream(workload):
+    """The reference's greedy stream of the workload (golden fixture data)."""
+    path = os.path.join(ROOT, "tests", "golden", f"{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)["tokens"]
+
+
 def kernel_table(ms, nbytes, kind, wdtype):
     """Per matvec role: launches, total and average launch time, bytes per
     launch and the achieved rate."""
@@ -160,8 +228,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel directly instead of replaying "
                     "the captured decode-step graph (for profilers that do not follow graph launches)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
-    ap.add_argument("--no-topk", action="store_true", help="skip the sampled-decode measurement (profiler runs)")
-    ap.add_argument("--no-tree-profile", action="store_true", help="skip the per-kernel timing of the tree mode")
+    ap.add_argument("--no-topk", action="store_true", help="skip the sampled-decode measurement")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -177,66 +244,47 @@ def main():
     if args.no_graph:
         os.environ["NC_DECODE_GRAPH"] = "0"
     nc.init(0)
-    cfg = workload_config(args.workload)
+    cfg = nc.workload_config(args.workload)
     model = nc.Model(cfg)
     model.init_synthetic(w["seed"])
     prompt = prompt_tokens(w)
+    L = nc.lib()
+
+    def sync():
+        nc.check(L.nc_synchronize())
 
     # prefill (an untimed first one loads every kernel; the second is timed
     # on its own), warmup steps, then the timed steps (each step one replay
     # of the captured decode-step graph)
-    L = nc.lib()
     model.prefill(prompt)
-    nc.check(L.nc_synchronize())
+    sync()
     t0 = time.perf_counter()
     model.prefill(prompt)
-    nc.check(L.nc_synchronize())
+    sync()
     prefill_s = time.perf_counter() - t0
     model.decode(args.warmup)
-    nc.check(L.nc_synchronize())
+    sync()
     t0 = time.perf_counter()
     model.decode(args.steps)
-    nc.check(L.nc_synchronize())
+    sync()
     dt = time.perf_counter() - t0
-    ordered_toks = model.decode(0, fetch=True)[: 1 + args.warmup + args.steps]
-    # the same steps in the tree reduction mode (tree sums in the fused
-    # kernels, results within rel-L2 1e-3 of the reference's): rate and how
-    # many tokens of the stream equal the ordered (bit-exact) stream
-    model.set_reduce(nc.REDUCE_TREE)
+    timed_toks = model.decode(0, fetch=True)[: 1 + args.warmup + args.steps]
+    # the whole stream: every decode step after the prompt, timed as one
+    # call, its tokens compared with the reference's
+    n_full = w["gen"] - 1
     model.prefill(prompt)
-    model.decode(args.warmup)
-    nc.check(L.nc_synchronize())
+    sync()
     t0 = time.perf_counter()
-    model.decode(args.steps)
-    nc.check(L.nc_synchronize())
-    dt_tree = time.perf_counter() - t0
-    tree_toks = model.decode(0, fetch=True)[: 1 + args.warmup + args.steps]
-    diff = np.nonzero(tree_toks != ordered_toks)[0]
-    tree_equal = int(diff[0]) if len(diff) else len(ordered_toks)
-    tree_ms, tree_b, tree_kind = None, None, None
-    if not args.no_tree_profile:
-        model.prefill(prompt)
-        model.decode(args.warmup)
-        model.profile_begin((4 * cfg.n_layers + 1) * args.steps)
-        model.decode(args.steps)
-        nc.check(L.nc_synchronize())
-        model.profile_end()
-        tree_ms, tree_b, tree_kind = model.profile_launches((4 * cfg.n_layers + 1) * args.steps)
-    # one step in both modes on the same cache: the first layer whose
-    # residual codes differ, and how far apart the logits end up
-    seq = np.concatenate([prompt, ordered_toks[:1]]).astype(np.int32)
-    model.set_reduce(nc.REDUCE_ORDERED)
-    model.logits(prompt, 0)
-    lo = model.logits(seq, len(seq) - 1)
-    ro = [model.layer_out(l, len(seq) - 1) for l in range(cfg.n_layers)]
-    model.set_reduce(nc.REDUCE_TREE)
-    lt = model.logits(seq, len(seq) - 1)
-    moved = [int((model.layer_out(l, len(seq) - 1) != ro[l]).sum()) for l in range(cfg.n_layers)]
-    tree_step = {"first_layer_moved": next((l for l, k in enumerate(moved) if k), None),
-                 "bytes_moved_last_layer": moved[-1],
-                 "logits_rel_l2": float(np.linalg.norm((lt - lo).astype(np.float64)) /
-                                        np.linalg.norm(lo.astype(np.float64)))}
-    model.set_reduce(nc.REDUCE_ORDERED)
+    model.decode(n_full)
+    sync()
+    dt_full = time.perf_counter() - t0
+    full_toks = model.decode(0, fetch=True)[: w["gen"]].tolist()
+    ref = reference_stream(args.workload)
+    full_stream = {"decode_tok_s": round(n_full / dt_full, 2), "steps": n_full,
+                   "positions": [w["prompt"], w["prompt"] + n_full],
+                   "matches_reference": None if ref is None else full_toks[: len(ref)] == ref,
+                   "timed_tokens_match_reference": None if ref is None else
+                   timed_toks.tolist() == ref[: len(timed_toks)]}
     # sampled decode (top-k 40, temperature 0.8, mt19937 seed 7): the same
     # step with the device sampler in place of the greedy pick; the rate is
     # the difference of two calls, prompt + first token and prompt + first
@@ -260,7 +308,7 @@ def main():
     model.profile_begin(launches_per_step * args.steps)
     t1 = time.perf_counter()
     model.decode(args.steps)
-    nc.check(L.nc_synchronize())
+    sync()
     dt_direct = time.perf_counter() - t1
     model.profile_end()
     ms, nbytes, kind = model.profile_launches(launches_per_step * args.steps)
@@ -287,9 +335,11 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{args.workload}: d_model {cfg.n_embd}, {cfg.n_layers} layers, "
                                f"{cfg.n_heads[0]}/{cfg.n_kv_heads[0]} heads, ffn {cfg.n_ffn[0]}, "
-                               f"vocab {cfg.n_vocab}, prompt {w['prompt']}, decode {w['gen']} greedy tokens",
+                               f"vocab {cfg.n_vocab}, prompt {w['prompt']}, greedy decode of "
+                               f"{args.steps} timed steps after {args.warmup} warmup steps",
                    "prompt": w["prompt"], "max_ctx": cfg.max_ctx,
                    "timed_positions": [w["prompt"] + args.warmup, w["prompt"] + args.warmup + args.steps]},
+        "full_stream": full_stream,
         "prefill_tok_s": round(w["prompt"] / prefill_s, 1),
         "direct_launch_tok_s": round(args.steps / dt_direct, 2),
         "topk_decode_tok_s": topk_tok_s,
@@ -300,22 +350,7 @@ def main():
                      "kernel": dom["kernel"], "avg_launch_us": dom["avg_launch_us"],
                      "bytes_per_launch": dom["bytes_per_launch"], "launches": dom["launches"]},
         "per_kernel": per_kernel,
-        "tree_reduce": {"decode_tok_s": round(args.steps / dt_tree, 2),
-                        "stream_equal_tokens": tree_equal, "stream_tokens": len(ordered_toks),
-                        "step_vs_ordered": tree_step,
-                        "note": "same steps with nc_model_set_reduce(TREE): rms_norm sums, matvec folds and the "
-                                "softmax sum as tree reductions, not bit-exact; stream_equal_tokens = leading "
-                                "tokens equal to the ordered (reference) stream; step_vs_ordered = one step of "
-                                "both modes on the same cache (first layer with a moved residual byte, bytes "
-                                "moved in the last layer's row, logits rel-L2)"},
     }
-    if tree_ms is not None:
-        tk = kernel_table(tree_ms, tree_b, tree_kind, cfg.wdtype)
-        line["tree_reduce"]["per_kernel"] = [{k: e[k] for k in ("role", "avg_launch_us", "achieved_gbs")} for e in tk]
-        tdom = next((e for e in tk if e["role"] == dom["role"]), None)
-        if tdom:
-            line["tree_reduce"]["roofline"] = {"kernel": tdom["kernel"], "achieved": tdom["achieved_gbs"],
-                                               "frac": round(tdom["achieved_gbs"] / HBM_PEAK_GBS, 4)}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, prompt)
     print(json.dumps(line), flush=True)

@@ -117,7 +117,8 @@ int nc_multiply(const nc_tensor* a, const nc_tensor* b, nc_tensor* out, int star
 int nc_add(const nc_tensor* a, const nc_tensor* b, nc_tensor* out, int start, int n_ctx, void* stream); /* ops.h:12 */
 int nc_scale(nc_tensor* x, float s, int start, int n_ctx, void* stream);                        /* ops.h:30 */
 int nc_bias_add(nc_tensor* x, const uint16_t* b, int start, int n_ctx, void* stream);           /* ops.h:14 */
-/* qkv_attn (ops.h:24): causal GQA attention of rows [start, n_ctx). */
+/* qkv_attn (ops.h:24): causal GQA attention of rows [start, n_ctx), n_ctx up
+ * to NC_MAX_CTX positions. */
 int nc_qkv_attn(const nc_tensor* q, const nc_tensor* k, const nc_tensor* v, nc_tensor* out, int n_heads,
                 int n_kv_heads, int d_head, int start, int n_ctx, void* stream);
 /* The device's std::exp(float) as softmax and SiLU use it (src/gten/
@@ -196,7 +197,7 @@ typedef struct nc_model_config {
     int n_embd;
     int n_layers;
     int d_head;
-    int max_ctx; /* inference context: prompt + generated tokens */
+    int max_ctx; /* inference context: prompt + generated tokens, <= NC_MAX_CTX */
     int eos;
     float rope_pct;
     int n_heads[NC_MAX_LAYERS];
@@ -227,7 +228,11 @@ typedef struct nc_model_config {
 #define NC_TID_LM 0xFFFF3
 
 /* Model constructor (TinyLLama(n_ctx, dtype) and siblings): allocates every
- * weight and every [max_ctx, d] activation buffer in HBM. */
+ * weight and every [max_ctx, d] activation buffer in HBM.  max_ctx may be up
+ * to NC_MAX_CTX, the longest max_ctx of the reference's models (Zephyr's,
+ * src/zephyr/zephyr.h:12); its default inference context is 1024
+ * (src/nanochat.cpp:40). */
+#define NC_MAX_CTX 4096
 int nc_model_create(const nc_model_config* cfg, void** model);
 int nc_model_free(void* model);
 /* Synthetic weights generated and quantized on the device (same values as
@@ -248,24 +253,6 @@ int nc_model_get_weight(void* model, int layer, int slot, void* ref_bytes, size_
 /* Model::logits(tokens, start_pos): processes rows [start_pos, n_tokens) and
  * copies the last row's fp32 logits to `logits` (host, n_vocab floats). */
 int nc_model_logits(void* model, const int32_t* tokens, int n_tokens, int start_pos, float* logits);
-/* Reduction order of the single-row decode step (no counterpart in the
- * reference, which has one order; for callers that trade the reference's
- * results for a faster step).
- *   NC_REDUCE_ORDERED (default): the reference's sequential sums -- the
- *     rms_norm sum of squares (src/gten/ops.cpp:830-903), each matvec row's
- *     per-lane block chains (ops.cpp:292-490) and the softmax denominator
- *     (ops.cpp:1061-1081) -- so every result equals the reference's bits.
- *   NC_REDUCE_TREE: those three sums as tree reductions, in the fused Q8/Q4
- *     decode kernels only.  Every rounding and requantization point stays;
- *     only the order of the fp32 adds changes.  A sum that then rounds a
- *     requantized code the other way changes every later matvec's outputs,
- *     so on deep models the step's results drift well beyond the last bits
- *     (TinyLlama, 22 layers: logits rel-L2 ~0.04).  Prefill, the op-by-op path
- *     (fp16 activations, layer_norm) and the ops API stay ordered.
- * Takes effect on the next decode step. */
-#define NC_REDUCE_ORDERED 0
-#define NC_REDUCE_TREE 1
-int nc_model_set_reduce(void* model, int mode);
 /* Residual stream after `layer` at `row`, in the reference's byte layout. */
 int nc_model_layer_out(void* model, int layer, int row, void* ref_bytes);
 /* greedy_sample (src/gten/sampler.cpp:11-60) without the tokenizer: prefill

@@ -22,7 +22,7 @@ W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN = range(7)
 W_ATTN_NORM, W_ATTN_NORM_B, W_MLP_NORM, W_MLP_NORM_B = 7, 8, 9, 10
 W_Q_BIAS, W_K_BIAS, W_V_BIAS, W_Q_NORM, W_K_NORM = 11, 12, 13, 14, 15
 TID_EMB, TID_NORM, TID_NORM_B, TID_LM = 0xFFFF0, 0xFFFF1, 0xFFFF2, 0xFFFF3
-REDUCE_ORDERED, REDUCE_TREE = 0, 1
+MAX_CTX = 4096  # NC_MAX_CTX
 
 
 class HipError(RuntimeError):
@@ -146,7 +146,6 @@ def lib():
         "nc_tokenizer_decode": (C.c_char_p, [VP, I, I]),
         "nc_tokenizer_eos": (I, [VP]),
         "nc_tokenizer_free": (I, [VP]),
-        "nc_model_set_reduce": (I, [VP, I]),
         "nc_model_layer_out": (I, [VP, I, I, VP]), "nc_model_generate": (I, [VP, VP, I, I, VP, C.POINTER(I)]),
         "nc_model_prefill": (I, [VP, VP, I]), "nc_model_decode": (I, [VP, I, VP]),
         "nc_model_profile_begin": (I, [VP, I]),
@@ -310,11 +309,6 @@ class Model:
         out = np.zeros(self.cfg.n_vocab, np.float32)
         check(lib().nc_model_logits(self.h, _ptr(toks), len(toks), start_pos, _ptr(out)), "logits")
         return out
-
-    def set_reduce(self, mode):
-        """Reduction order of the decode step: REDUCE_ORDERED (the
-        reference's bits) or REDUCE_TREE (tree sums, within rel-L2 1e-3)."""
-        check(lib().nc_model_set_reduce(self.h, int(mode)), "set_reduce")
 
     def layer_out(self, layer, row):
         import numpy as np

@@ -7,19 +7,24 @@
 //     outputs; OpenELM's per-head QK RMSNorm (requantized); RoPE of q and k
 //     (requantized when stored) -- gten/modules.cpp:242-267, openelm.cpp:33-60;
 //   the group's first head appends k_g and v_g to the caches at the position
-//     (the others read that position from shared memory, so no workgroup
+//     (the others take that position from shared memory, so no workgroup
 //     waits for another);
 //   scores, softmax (max, expf, sequential sum, divide, requantize per 32
 //     positions) and P.V as qkv_attn (gten/ops.cpp:1017-1220): the Q8 dot's
 //     four lane sums per block, P.V as eight fp32 lanes (position mod 8)
 //     summed left to right, then the n mod 8 tail.
-// The K and V rows of the earlier positions are requested first, into
-// registers, so their latency overlaps the q/k/v work (whose own inputs --
-// the qkv output and the RoPE pair -- are requested before them).
+// Any context up to kAdMaxCtx positions: the scores sit in shared memory,
+// the K rows are read straight into registers (the next row requested before
+// the current one is used), and the V slice streams through shared memory in
+// double-buffered chunks of kAdVc positions while the P.V lane chains run
+// over them in position order.  The softmax denominator of a long row is the
+// exact workgroup-parallel restatement of the sequential sum (nc_seqsum.h);
+// short rows take the plain loop on one wavefront.
 #include <type_traits>
 
 #include "nc_act.h"
 #include "nc_kernels.h"
+#include "nc_seqsum.h"
 
 namespace nc {
 
@@ -35,9 +40,10 @@ __device__ __forceinline__ void static_for(F&& f)
 }
 
 constexpr int kAdThreads = 256;
-constexpr int kAdMaxK = 3;   // K rows per thread in registers at most (positions < 768)
-constexpr int kAdMaxV = 10;  // 16-byte V parts per thread in registers at most (positions < 640)
-constexpr int kAdVB = 80;    // LDS bytes per staged V position: 64 codes, 2 fp16 deltas, pad
+constexpr int kAdMaxK = 2;      // K rows per thread requested at kernel start, at most
+constexpr int kAdVB = 80;       // LDS bytes per staged V position: 64 codes, 2 fp16 deltas, pad
+constexpr int kAdVc = 128;      // positions per staged V chunk (2 16-byte parts per thread)
+constexpr int kAdSeqMax = 1024; // softmax rows up to this long are summed by one wavefront's loop
 
 __device__ __forceinline__ uint32_t ad_pick(uint32_t lo, uint32_t hi, int odd)
 {
@@ -87,11 +93,81 @@ __device__ __forceinline__ float wave_max(float v)
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-// MK K rows and MV 16-byte V parts per thread are requested into registers
-// at the start (every slot, so the load counts are static and the waits
-// exact); positions past them are read in the loops after.  The launcher
-// sizes them to the cache: issuing the loads is itself a cost.
-template <bool QKNORM, int MK, int MV, bool TR>
+// A K row's 64 codes and its two fp16 deltas (as one dword).
+struct KRow {
+    uint4 q[4];
+    uint32_t d;
+};
+
+__device__ __forceinline__ KRow load_krow(const uint8_t* kslice, const uint8_t* kdelta, int c, int kv_pitch, int g)
+{
+    KRow r;
+    const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)c * kv_pitch);
+#pragma unroll
+    for (int v = 0; v < 4; v++) r.q[v] = p[v];
+    r.d = reinterpret_cast<const uint32_t*>(kdelta + (size_t)c * kv_pitch)[g];
+    return r;
+}
+
+__device__ __forceinline__ float score_of(const uint4 (&qv)[4], const float (&dq)[2], const KRow& k)
+{
+    const float dk[2] = {h2f((uint16_t)(k.d & 0xFFFFu)), h2f((uint16_t)(k.d >> 16))};
+    return head_dot_q8(qv, dq, k.q, dk);
+}
+
+// The V parts of one chunk a thread carries: 16-byte parts tid and tid + 256
+// (position = part / 4 within the chunk), and the delta dword of position tid
+// (threads below kAdVc).
+struct VChunk {
+    uint32_t p[2][4];  // plain words: an array of the uint4 union type stays in scratch memory
+    uint32_t d;
+};
+
+// Loads chunk `ch`; positions are clamped to the cache's rows (those past the
+// context are never read back).
+__device__ __forceinline__ void load_vchunk(VChunk& v, const uint8_t* vslice, const uint8_t* vdelta, int ch,
+                                            int kv_pitch, int g, int kv_rows)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int idx = tid + i * kAdThreads;
+        const int c = min(ch * kAdVc + (idx >> 2), kv_rows - 1);
+        const uint4 t4 = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[idx & 3];
+        v.p[i][0] = t4.x;
+        v.p[i][1] = t4.y;
+        v.p[i][2] = t4.z;
+        v.p[i][3] = t4.w;
+    }
+    const int c = min(ch * kAdVc + (tid & (kAdVc - 1)), kv_rows - 1);
+    v.d = reinterpret_cast<const uint32_t*>(vdelta + (size_t)c * kv_pitch)[g];
+}
+
+// Parks a loaded chunk in a shared-memory buffer [kAdVc][kAdVB]; the new
+// position `pos` (not yet in the cache for every head) comes from s_v.
+__device__ __forceinline__ void store_vchunk(const VChunk& v, uint8_t* buf, int ch, int pos, const uint8_t* s_v)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int idx = tid + i * kAdThreads;
+        const int cl = idx >> 2, part = idx & 3;
+        uint4 t4 = make_uint4(v.p[i][0], v.p[i][1], v.p[i][2], v.p[i][3]);
+        if (ch * kAdVc + cl == pos) t4 = reinterpret_cast<const uint4*>(s_v)[part];
+        reinterpret_cast<uint4*>(buf + cl * kAdVB)[part] = t4;
+    }
+    if (tid < kAdVc) {
+        uint32_t d = v.d;
+        if (ch * kAdVc + tid == pos) d = reinterpret_cast<const uint32_t*>(s_v + 64)[0];
+        reinterpret_cast<uint32_t*>(buf + tid * kAdVB + 64)[0] = d;
+    }
+}
+
+// MK K rows per thread are requested into registers at the start (every
+// slot, so the load counts are static and the waits exact); later rows are
+// read in the score loop, one row ahead.  The launcher sizes MK to the cache:
+// issuing the loads is itself a cost.
+template <bool QKNORM, int MK>
 __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict__ raw, int hq, int hkv,
                                                          const uint16_t* __restrict__ qn_w,
                                                          const uint16_t* __restrict__ kn_w,
@@ -102,9 +178,10 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
                                                          const float2* __restrict__ rope_cur, int kv_rows)
 {
     extern __shared__ __align__(16) float sm[];
-    __shared__ __align__(16) uint8_t s_q[kAdVB], s_k[kAdVB];
+    __shared__ __align__(16) uint8_t s_q[kAdVB], s_k[kAdVB], s_v[kAdVB];
     __shared__ __align__(16) float s_nrm[2][64];
     __shared__ float red[8];
+    __shared__ SsShared ssh;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     // workgroup i runs on XCD i % 8: with hq % 8 == 0, XCD x takes heads
     // x * hq/8 .. (x + 1) * hq/8 - 1, so the query heads of one kv head share
@@ -122,42 +199,28 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     const bool rope_lane_in = w < 2 && lane < 2 * d_half;
     float2 rp = make_float2(0.0f, 0.0f);
     if (rope_cur && rope_lane_in) rp = rope_cur[pair];
+    const int kvd = act_delta_offset(hkv * 64);
+    const uint8_t* kslice = kc + g * 64;
+    const uint8_t* vslice = vc + g * 64;
+    // the first V chunk does not depend on the position either
+    VChunk vch;
+    load_vchunk(vch, vslice, vc + kvd, 0, kv_pitch, g, kv_rows);
     const int pos = dpos ? load_pos(dpos) : pos_host;
     if (!rope_cur && rope_lane_in) rp = table[(size_t)pos * d_half + pair];
     __builtin_amdgcn_sched_barrier(0);
     const int n = pos + 1;
-    // the shared-memory layout is sized by the cache rows, not by the position
-    const int spad = (kv_rows + 3) & ~3;
-    float* S = sm;                                           // scores / probabilities [spad]
-    float* acc = S + spad;                                   // [8 lanes][64 columns]
-    uint8_t* Vs = reinterpret_cast<uint8_t*>(acc + 512);    // [n][kAdVB]
-    const int kvd = act_delta_offset(hkv * 64);
-    const uint8_t* kslice = kc + g * 64;
-    const uint8_t* vslice = vc + g * 64;
+    // shared memory: scores [spad] (whole 256-position chunks, zero-padded
+    // for the block sum), P.V lane sums [8][64], two V chunk buffers
+    const int spad = (kv_rows + kSsThreads - 1) & ~(kSsThreads - 1);
+    float* S = sm;
+    float* acc = S + spad;
+    uint8_t* Vb = reinterpret_cast<uint8_t*>(acc + 512);
 
-    // ---- K rows (positions < pos) into registers, V slices too
-    uint4 kr[MK][4];
-    uint32_t kd[MK];
+    // ---- K rows (positions < pos) into registers
+    KRow kr[MK];
     static_for<0, MK>([&](auto I) {
         const int c = tid + I * kAdThreads;
-        const int cc = c < pos ? c : 0;
-        const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)cc * kv_pitch);
-#pragma unroll
-        for (int v = 0; v < 4; v++) kr[I][v] = p[v];
-        kd[I] = reinterpret_cast<const uint32_t*>(kc + (size_t)cc * kv_pitch + kvd)[g];
-    });
-    const int vtotal = pos * 4;  // 16-byte parts of the earlier positions' V slices
-    uint32_t vr[MV][4];  // plain words: an array of the uint4 union type stays in scratch memory
-    uint32_t vd[MV];
-    static_for<0, MV>([&](auto I) {
-        const int idx = tid + I * kAdThreads;
-        const int c = idx < vtotal ? idx >> 2 : 0, part = idx & 3;
-        const uint4 t4 = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[part];
-        vr[I][0] = t4.x;
-        vr[I][1] = t4.y;
-        vr[I][2] = t4.z;
-        vr[I][3] = t4.w;
-        vd[I] = reinterpret_cast<const uint32_t*>(vc + (size_t)c * kv_pitch + kvd)[g];
+        kr[I] = load_krow(kslice, kc + kvd, c < pos ? c : 0, kv_pitch, g);
     });
 
     // ---- q_h (wave 0), k_g (wave 1), v_g (wave 2) of the new position
@@ -178,7 +241,7 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         }
         uint16_t d16;
         const int8_t code = q8_quant_lane(x, true, &d16);
-        uint8_t* st = w == 0 ? s_q : (w == 1 ? s_k : Vs + (size_t)pos * kAdVB);
+        uint8_t* st = w == 0 ? s_q : (w == 1 ? s_k : s_v);
         st[lane] = (uint8_t)code;
         if ((lane & 31) == 0) reinterpret_cast<uint16_t*>(st + 64)[lane >> 5] = d16;
         if (w > 0 && h % gs == 0) {
@@ -190,6 +253,11 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     }
     lds_barrier();
 
+    // the first V chunk into buffer 0; the second one requested
+    const int nch = (n + kAdVc - 1) / kAdVc;
+    store_vchunk(vch, Vb, 0, pos, s_v);
+    if (nch > 1) load_vchunk(vch, vslice, vc + kvd, 1, kv_pitch, g, kv_rows);
+
     // ---- scores of positions c <= pos (thread = position)
     {
         uint4 qv[4];
@@ -200,45 +268,28 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         dq[1] = h2f(reinterpret_cast<const uint16_t*>(s_q + 64)[1]);
         static_for<0, MK>([&](auto I) {
             const int c = tid + I * kAdThreads;
-            if (c < pos) {
-                const float dk[2] = {h2f((uint16_t)(kd[I] & 0xFFFFu)), h2f((uint16_t)(kd[I] >> 16))};
-                S[c] = head_dot_q8(qv, dq, kr[I], dk) * scale;
-            }
+            if (c < pos) S[c] = score_of(qv, dq, kr[I]) * scale;
         });
-        for (int c = tid + MK * kAdThreads; c < pos; c += kAdThreads) {
-            uint4 kk[4];
-            const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)c * kv_pitch);
-#pragma unroll
-            for (int v = 0; v < 4; v++) kk[v] = p[v];
-            const uint32_t kdd = reinterpret_cast<const uint32_t*>(kc + (size_t)c * kv_pitch + kvd)[g];
-            const float dk[2] = {h2f((uint16_t)(kdd & 0xFFFFu)), h2f((uint16_t)(kdd >> 16))};
-            S[c] = head_dot_q8(qv, dq, kk, dk) * scale;
+        int c = tid + MK * kAdThreads;
+        if (c < pos) {
+            KRow cur = load_krow(kslice, kc + kvd, c, kv_pitch, g);
+            for (;;) {
+                const int cn = c + kAdThreads;
+                KRow nxt = cur;
+                if (cn < pos) nxt = load_krow(kslice, kc + kvd, cn, kv_pitch, g);
+                S[c] = score_of(qv, dq, cur) * scale;
+                if (cn >= pos) break;
+                cur = nxt;
+                c = cn;
+            }
         }
         if (tid == (pos & (kAdThreads - 1))) {
-            uint4 kk[4];
+            KRow kk;
 #pragma unroll
-            for (int v = 0; v < 4; v++) kk[v] = reinterpret_cast<const uint4*>(s_k)[v];
-            const float dk[2] = {h2f(reinterpret_cast<const uint16_t*>(s_k + 64)[0]),
-                                 h2f(reinterpret_cast<const uint16_t*>(s_k + 64)[1])};
-            S[pos] = head_dot_q8(qv, dq, kk, dk) * scale;
+            for (int v = 0; v < 4; v++) kk.q[v] = reinterpret_cast<const uint4*>(s_k)[v];
+            kk.d = reinterpret_cast<const uint32_t*>(s_k + 64)[0];
+            S[pos] = score_of(qv, dq, kk) * scale;
         }
-    }
-    // V slices of the earlier positions into shared memory
-    static_for<0, MV>([&](auto I) {
-        const int idx = tid + I * kAdThreads;
-        if (idx < vtotal) {
-            const int c = idx >> 2, part = idx & 3;
-            reinterpret_cast<uint4*>(Vs + (size_t)c * kAdVB)[part] = make_uint4(vr[I][0], vr[I][1], vr[I][2], vr[I][3]);
-            if (part == 0) reinterpret_cast<uint32_t*>(Vs + (size_t)c * kAdVB + 64)[0] = vd[I];
-        }
-    });
-    for (int idx = tid + MV * kAdThreads; idx < vtotal; idx += kAdThreads) {
-        const int c = idx >> 2, part = idx & 3;
-        reinterpret_cast<uint4*>(Vs + (size_t)c * kAdVB)[part] =
-                reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[part];
-        if (part == 0)
-            reinterpret_cast<uint32_t*>(Vs + (size_t)c * kAdVB + 64)[0] =
-                    reinterpret_cast<const uint32_t*>(vc + (size_t)c * kv_pitch + kvd)[g];
     }
     lds_barrier();
 
@@ -249,21 +300,16 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     if (lane == 0) red[w] = mx;
     lds_barrier();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float tsum = 0.0f;  // tree mode: this thread's share of the sum
-    for (int c = tid; c < n; c += kAdThreads) {
-        const float e = expf_ref(S[c] - mx);
-        S[c] = e;
-        if (TR) tsum += e;
-    }
+    const bool long_row = n > kAdSeqMax;
+    const int npad = (n + kSsThreads - 1) & ~(kSsThreads - 1);
+    for (int c = tid; c < (long_row ? npad : n); c += kAdThreads) S[c] = c < n ? expf_ref(S[c] - mx) : 0.0f;
+    lds_barrier();
     float sum;
-    if (TR) {
-        // tree mode: wave sums, then the four waves' in a fixed order
-        tsum = group_sum(tsum, kWave);
-        if (lane == 0) red[4 + w] = tsum;
-        lds_barrier();
-        sum = (red[4] + red[5]) + (red[6] + red[7]);
+    if (long_row) {
+        // the exact parallel sum of the terms; the zero padding leaves a sum
+        // of non-negative terms as it is
+        sum = block_seq_sum_nonneg(S, npad, ssh);
     } else {
-        lds_barrier();
         if (w == 0) {
             const float ss = seq_sum(S, n);
             if (lane == 0) red[4] = ss;
@@ -282,20 +328,25 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
 
     // ---- P.V: thread = (lane l = tid / 32, columns 2m and 2m + 1 with
     // m = tid % 32): the chains (l, 2m) and (l, 2m + 1) over positions l,
-    // l + 8, ... in order, both column codes of a position in one load
-    {
-        const int l = tid >> 5, m = tid & 31;
-        const int n8 = n & ~7;
+    // l + 8, ... in order, both column codes of a position in one load.
+    // Chunk ch sits in buffer ch & 1 while chunk ch + 1 is parked in the
+    // other and chunk ch + 2 is requested.
+    const int l = tid >> 5, m = tid & 31;
+    const int n8 = n & ~7;
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int ch = 0; ch < nch; ch++) {
+        const uint8_t* B = Vb + (ch & 1) * (kAdVc * kAdVB);
+        const int c0 = ch * kAdVc;
+        const int cend = min(c0 + kAdVc, n8);
         auto vpair = [&](int c, float& v0, float& v1) {
-            const uint8_t* vrow = Vs + (size_t)c * kAdVB;
+            const uint8_t* vrow = B + (c - c0) * kAdVB;
             const uint32_t codes = reinterpret_cast<const uint16_t*>(vrow)[m];
             const float d = h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[m >> 4]);  // block of column 2m
             v0 = (float)(int8_t)(codes & 0xFFu) * d;
             v1 = (float)(int8_t)(codes >> 8) * d;
         };
-        float a0 = 0.0f, a1 = 0.0f;
-        int c = 0;
-        for (; c + 64 <= n8; c += 64) {
+        int c = c0;
+        for (; c + 64 <= cend; c += 64) {
             // eight positions of both chains: loads first, then the adds in order
             float p[8], v0[8], v1[8];
 #pragma unroll
@@ -309,23 +360,32 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
                 a1 = p[u] * v1[u] + a1;
             }
         }
-        for (; c < n8; c += 8) {
+        for (; c < cend; c += 8) {
             float v0, v1;
             vpair(c + l, v0, v1);
             const float p = S[c + l];
             a0 = p * v0 + a0;
             a1 = p * v1 + a1;
         }
-        *reinterpret_cast<float2*>(acc + l * 64 + 2 * m) = make_float2(a0, a1);
+        if (ch + 1 < nch) {
+            store_vchunk(vch, Vb + ((ch + 1) & 1) * (kAdVc * kAdVB), ch + 1, pos, s_v);
+            if (ch + 2 < nch) load_vchunk(vch, vslice, vc + kvd, ch + 2, kv_pitch, g, kv_rows);
+        }
+        lds_barrier();
     }
+    *reinterpret_cast<float2*>(acc + l * 64 + 2 * m) = make_float2(a0, a1);
     lds_barrier();
     if (w == 0) {
+        // lanes left to right, then the tail positions [n8, n) in order (all
+        // in the last chunk, still in its buffer)
         const int j = lane;
         float s = acc[j];
 #pragma unroll
-        for (int l = 1; l < 8; l++) s = s + acc[l * 64 + j];
-        for (int c = n & ~7; c < n; c++) {
-            const uint8_t* vrow = Vs + (size_t)c * kAdVB;
+        for (int q = 1; q < 8; q++) s = s + acc[q * 64 + j];
+        const uint8_t* B = Vb + ((nch - 1) & 1) * (kAdVc * kAdVB);
+        const int c0 = (nch - 1) * kAdVc;
+        for (int c = n8; c < n; c++) {
+            const uint8_t* vrow = B + (c - c0) * kAdVB;
             s = s + S[c] * ((float)reinterpret_cast<const int8_t*>(vrow)[j] *
                             h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[j >> 5]));
         }
@@ -333,35 +393,41 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     }
 }
 
+// Shared memory of k_attn_dec for a cache of max_ctx rows.
+static size_t attn_decode_lds(int max_ctx)
+{
+    const size_t spad = ((size_t)max_ctx + kSsThreads - 1) & ~(size_t)(kSsThreads - 1);
+    return (spad + 512) * 4 + 2 * (size_t)kAdVc * kAdVB;
+}
+
+bool attn_decode_supported(int hq, int hkv, int max_ctx)
+{
+    return hkv > 0 && hq % hkv == 0 && max_ctx > 0 && max_ctx <= kAttnMaxCtx;
+}
+
 int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
                        const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur, bool tree)
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur)
 {
     if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "attention: %d query heads over %d kv heads", hq, hkv);
-    if (max_ctx > kAdMaxK * kAdThreads) return fail(NC_ERR_ARG, "attention: context %d too long", max_ctx);
-    const size_t lds = ((size_t)((max_ctx + 3) & ~3) + 512) * 4 + (size_t)max_ctx * kAdVB;
-    if (lds > 60 * 1024) return fail(NC_ERR_ARG, "attention: context %d too long", max_ctx);
+    if (max_ctx <= 0 || max_ctx > kAttnMaxCtx)
+        return fail(NC_ERR_ARG, "attention: context %d (at most %d positions)", max_ctx, kAttnMaxCtx);
+    if (!dpos && (pos < 0 || pos >= max_ctx)) return fail(NC_ERR_ARG, "attention: position %d of %d", pos, max_ctx);
+    const size_t lds = attn_decode_lds(max_ctx);
     const float scale = 1.0f / sqrtf(64.0f);
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w, (const float2*)table,
                            d_half, pos, dpos, kc, vc, kv_pitch, out, scale, (const float2*)rope_cur, max_ctx);
     };
-    // register slots for the cache's positions (K: one row per slot and
-    // thread, V: a quarter row)
-    auto by_norm = [&](auto qk, auto tr) {
-        constexpr bool QK = decltype(qk)::value, TR = decltype(tr)::value;
-        if (max_ctx <= 128) go(k_attn_dec<QK, 1, 2, TR>);
-        else if (max_ctx <= 256) go(k_attn_dec<QK, 1, 4, TR>);
-        else if (max_ctx <= 320) go(k_attn_dec<QK, 2, 5, TR>);
-        else if (max_ctx <= 512) go(k_attn_dec<QK, 2, 8, TR>);
-        else go(k_attn_dec<QK, kAdMaxK, kAdMaxV, TR>);
+    // K rows requested at the start: one per thread for caches of up to 256
+    // positions, two beyond
+    auto by_ctx = [&](auto qk) {
+        constexpr bool QK = decltype(qk)::value;
+        if (max_ctx <= kAdThreads) go(k_attn_dec<QK, 1>);
+        else go(k_attn_dec<QK, kAdMaxK>);
     };
-    auto by_mode = [&](auto qk) {
-        if (tree) by_norm(qk, std::true_type{});
-        else by_norm(qk, std::false_type{});
-    };
-    if (qn_w) by_mode(std::true_type{});
-    else by_mode(std::false_type{});
+    if (qn_w) by_ctx(std::true_type{});
+    else by_ctx(std::false_type{});
     return launch_status("k_attn_dec");
 }
 

@@ -62,11 +62,6 @@ struct DmvArgs {
     const float* rope_table = nullptr;  // [max_ctx][rope_half] (cos, sin) pairs
     float* rope_cur = nullptr;
     int rope_half = 0;
-    // Tree mode (nonzero): the rms_norm sum of squares and each row's fold
-    // over blocks and lanes run as tree reductions instead of the
-    // reference's sequential chains.  Same operations and requantization
-    // points; only the order of the fp32 adds differs.
-    int tree = 0;
 };
 
 constexpr int kDmvArgmaxWords = 320 + 4096;

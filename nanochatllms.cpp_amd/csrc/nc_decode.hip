@@ -99,22 +99,13 @@ __device__ __forceinline__ void load_f32_chunk(const float* p, int ch, float (&v
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-// Argmax key: order-preserving float bits << 32 | ~index, so the largest
-// key is the first index of the largest value.
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx)
-{
-    const uint32_t u = __float_as_uint(v);
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (uint32_t)idx);
-}
-
 // The prologue: builds the activation row the matvec consumes and stages
 // it in LDS by AVX lane (xs).  The inputs are requested first, then
 // load_w() requests the workgroup's first weights, and the row is built
 // while the weights are in flight (LDS barriers do not wait for global
 // loads).  sq: K floats of LDS for the squares and the Act row.  Ends with
 // an LDS barrier.
-template <int PRO, int NCH, bool TR, class LoadW>
+template <int PRO, int NCH, class LoadW>
 __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, LoadW&& load_w)
 {
     const int tid = threadIdx.x;
@@ -166,7 +157,6 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
         load_w();
         __builtin_amdgcn_sched_barrier(0);
         if (fixed && A.dpos) pos = posv;
-        float tsq = 0.0f;  // tree mode: this thread's share of the sum of squares
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * kDmvThreads;
@@ -197,26 +187,12 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
             if (valid) {
                 const float4 s0 = make_float4(h[j][0] * h[j][0], h[j][1] * h[j][1], h[j][2] * h[j][2], h[j][3] * h[j][3]);
                 const float4 s1 = make_float4(h[j][4] * h[j][4], h[j][5] * h[j][5], h[j][6] * h[j][6], h[j][7] * h[j][7]);
-                if (TR) {
-                    tsq += ((s0.x + s0.y) + (s0.z + s0.w)) + ((s1.x + s1.y) + (s1.z + s1.w));
-                } else {
-                    reinterpret_cast<float4*>(sq)[2 * ch] = s0;
-                    reinterpret_cast<float4*>(sq)[2 * ch + 1] = s1;
-                }
+                reinterpret_cast<float4*>(sq)[2 * ch] = s0;
+                reinterpret_cast<float4*>(sq)[2 * ch + 1] = s1;
             }
         }
-        float ss;
-        if (TR) {
-            // wave sums, then the four waves' in a fixed order
-            __shared__ float s_wsum[kDmvThreads / kWave];
-            tsq = group_sum(tsq, kWave);
-            if ((tid & (kWave - 1)) == 0) s_wsum[tid / kWave] = tsq;
-            lds_barrier();
-            ss = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
-        } else {
-            lds_barrier();
-            ss = block_seq_sum_nonneg(sq, K, ssh);
-        }
+        lds_barrier();
+        const float ss = block_seq_sum_nonneg(sq, K, ssh);
         const float denom = sqrtf(ss / (float)K) + 1e-6f;
         // the normalized row as stored (codes, then deltas) over sq's bytes
 #pragma unroll
@@ -329,11 +305,14 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
 
     // Two-level reduction over the workgroups: keys in slots, the last
     // of each 32 workgroups reduces its slots, the last of those the
-    // rest.  Agent-scope stores and loads are coherent across the XCDs'
-    // L2s without a cache flush; the workgroup fences order each
-    // thread's own accesses.  Scratch layout (64-bit words): [0] top
-    // counter, [64, 192) level-1 results, [192, 320) level-1 counters,
-    // [320, 320 + grid) workgroup keys.
+    // rest.  Keys and level-1 results are written with agent-scope atomic
+    // stores (through the XCD's L2) and read with agent-scope atomic loads,
+    // so they are coherent across the XCDs' L2s without a cache flush.  A
+    // writer waits for its store to complete (wait_stores_done) before it
+    // bumps the counter, so a reader that sees the count sees every key
+    // counted; the reader's loads depend on the count it got back.
+    // Scratch layout (64-bit words): [0] top counter, [64, 192) level-1
+    // results, [192, 320) level-1 counters, [320, 320 + grid) workgroup keys.
     unsigned long long* top = A.amax;
     unsigned long long* sub = A.amax + 64;
     unsigned long long* cnt = A.amax + 192;
@@ -356,13 +335,12 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
         unsigned long long done = 0;
         if (tid == 0) {
             __hip_atomic_store(slot + blockIdx.x, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            wait_stores_done();
             done = __hip_atomic_fetch_add(cnt + grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         const int members = min(32, G - grp * 32);
         done = __shfl(done, 0);
         if (done == (unsigned long long)members - 1) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             unsigned long long k = tid < members
                     ? __hip_atomic_load(slot + grp * 32 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                     : 0ull;
@@ -375,12 +353,11 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
             if (tid == 0) {
                 __hip_atomic_store(cnt + grp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(sub + grp, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                wait_stores_done();
                 done2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             done2 = __shfl(done2, 0);
             if (done2 == (unsigned long long)ngrp - 1) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
                 unsigned long long b2 = 0;
                 for (int q = tid; q < ngrp; q += kWave) {
                     const unsigned long long o = __hip_atomic_load(sub + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -409,10 +386,7 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
     }
 }
 
-// Tree mode (TR): an item's four lane terms are added into one block term,
-// and each row's block terms are summed by kDmvThreads / R lanes (strided,
-// then xor butterflies) instead of four sequential lane chains.
-template <int WT, int IT, int PRO, int EPI, int NCH, bool TR>
+template <int WT, int IT, int PRO, int EPI, int NCH>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
@@ -448,7 +422,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     };
     const int G = gridDim.x;
     int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
-    const int pos = dmv_prologue<PRO, NCH, TR>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
+    const int pos = dmv_prologue<PRO, NCH>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
 
     // EPI_ARGMAX: each row's lane-0 thread keeps the best key of its rows
     unsigned long long best = 0;
@@ -464,31 +438,12 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             const int r = j / nb, i = j - r * nb;
             float tv[4];
             q_block_terms<WT>(xs + i * kStage, wc[it], dc[it], tv);
-            if (TR) {
-                T[r * tp + i] = (tv[0] + tv[1]) + (tv[2] + tv[3]);
-            } else {
-                float* t = T + r * 4 * tp + i;
+            float* t = T + r * 4 * tp + i;
 #pragma unroll
-                for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
-            }
+            for (int k = 0; k < 4; k++) t[k * tp] = tv[k];
         }
         lds_barrier();
-        if (TR) {
-            // R divides the workgroup (R in {4, 8, 16, 32}): lanes per row 8..64
-            const int P = kDmvThreads / R;
-            const int r = tid / P, sub = tid - r * P;
-            float acc = 0.0f;
-            for (int i = sub; i < nb; i += P) acc += T[r * tp + i];
-            acc = group_sum(acc, P);
-            const int row = g * R + r;
-            if (sub == 0 && row < A.N) {
-                A.raw[row] = acc;
-                if (EPI == EPI_ARGMAX) {
-                    const unsigned long long key = argmax_key(acc, row);
-                    best = key > best ? key : best;
-                }
-            }
-        } else if (tid < 4 * R) {
+        if (tid < 4 * R) {
             // thread 4r + k folds lane k of row r in block order
             const float acc = seq_sum<16>(T + tid * tp, nb);
             // lanes 4r..4r+3 hold row r's four lane sums; lane 4r reads
@@ -501,7 +456,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
             if ((tid & 3) == 0 && row < A.N) {
                 A.raw[row] = res;
                 if (EPI == EPI_ARGMAX) {
-                    const unsigned long long key = argmax_key(res, row);
+                    const unsigned long long key = greedy_key(res, row);
                     best = key > best ? key : best;
                 }
             }
@@ -516,9 +471,8 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     }
 
     if (EPI == EPI_ARGMAX) {
-        // row results sit on lanes 4r (ordered) or on every wave (tree)
-        argmax_epilogue<WT, NCH>(A, best, pos, TR ? kDmvThreads / kWave : (4 * R + kWave - 1) / kWave, s_key,
-                                 &s_tok);
+        // row results sit on lanes 4r
+        argmax_epilogue<WT, NCH>(A, best, pos, (4 * R + kWave - 1) / kWave, s_key, &s_tok);
     }
 }
 
@@ -538,7 +492,7 @@ constexpr int kRwRows = 64;   // rows per group: 4 wavefronts x 16 rows
 constexpr int kRwChunk = 8;   // blocks per chunk (nb % 8 == 0)
 constexpr int kRwDepth = 4;   // chunks in flight per thread
 
-template <int WT, int PRO, int EPI, int NCH, bool TR>
+template <int WT, int PRO, int EPI, int NCH>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv_rows(DmvArgs A)
 {
     constexpr int WW = WT == Q4 ? 1 : 2;        // code dwords of one lane and block
@@ -584,7 +538,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_rows(DmvArgs A)
         // chunks after this one read the rest of their line
         d = *reinterpret_cast<const uint32_t*>(A.wd + b0);
     };
-    const int pos = dmv_prologue<PRO, NCH, TR>(A, xs, sq, ssh, [&] {
+    const int pos = dmv_prologue<PRO, NCH>(A, xs, sq, ssh, [&] {
 #pragma unroll
         for (int b = 0; b < kRwDepth; b++) issue(b, wc[b], wd[b]);
     });
@@ -671,7 +625,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_rows(DmvArgs A)
             const float v = res[t];
             A.raw[row] = v;
             if (EPI == EPI_ARGMAX) {
-                const unsigned long long key = argmax_key(v, row);
+                const unsigned long long key = greedy_key(v, row);
                 best = key > best ? key : best;
             }
         }
@@ -694,7 +648,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_rows(DmvArgs A)
 // block (tinyllama/tinyllama.cpp:88-97).  No workgroup waits for another.
 constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / 256 threads, NB <= 72
 
-template <int WT, int PRO, int NCH, int NB, bool TR>
+template <int WT, int PRO, int NCH, int NB>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
@@ -729,7 +683,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks
     DmvArgs P = A;
     P.nb = NB;
-    dmv_prologue<PRO, NCH, TR>(P, xs, sq, ssh, [&] { load_block(b); });
+    dmv_prologue<PRO, NCH>(P, xs, sq, ssh, [&] { load_block(b); });
 
     // the terms of all 64 rows, then the gate rows' folds (waves 0-1) and
     // the up rows' folds (waves 2-3) side by side
@@ -748,27 +702,14 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
                 q_block_terms<WT>(x0, w[it], dw[it], tv);
             else
                 q_block_terms<WT>(xs + i * kStage, w[it], dw[it], tv);
-            if (TR) {
-                T[r * TP + i] = (tv[0] + tv[1]) + (tv[2] + tv[3]);
-            } else {
-                float* t = T + r * 4 * TP + i;
+            float* t = T + r * 4 * TP + i;
 #pragma unroll
-                for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
-            }
+            for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
         }
         lds_barrier();
         {
-            // ordered: thread 4r + k folds lane k of row r in block order;
-            // tree: it sums blocks k, k + 4, ... of row r
-            float acc;
-            if (TR) {
-                const float* t = T + (tid >> 2) * TP;
-                acc = 0.0f;
-#pragma unroll 4
-                for (int i = tid & 3; i < NB; i += 4) acc += t[i];
-            } else {
-                acc = seq_sum<16>(T + tid * TP, NB);
-            }
+            // thread 4r + k folds lane k of row r in block order
+            const float acc = seq_sum<16>(T + tid * TP, NB);
             const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
             if ((tid & 3) == 0) {
                 const int r = tid >> 2;  // 0..31 gate, 32..63 up
@@ -837,10 +778,10 @@ DmvShape dmv_shape(int nb, int N, bool norm)
     return {best, false};
 }
 
-template <int WT, int IT, int PRO, int EPI, int NCH, bool TR>
+template <int WT, int IT, int PRO, int EPI, int NCH>
 int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv<WT, IT, PRO, EPI, NCH, TR>;
+    auto kern = k_dmv<WT, IT, PRO, EPI, NCH>;
     static int max_grid = 0;  // per instantiation: workgroups resident at once
     if (!max_grid) {
         int per_cu = 0;
@@ -858,10 +799,10 @@ int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, h
     return launch_status("k_dmv");
 }
 
-template <int WT, int PRO, int NCH, int NB, bool TR>
+template <int WT, int PRO, int NCH, int NB>
 int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv_glu<WT, PRO, NCH, NB, TR>;
+    auto kern = k_dmv_glu<WT, PRO, NCH, NB>;
     static int max_grid = 0;
     if (!max_grid) {
         int per_cu = 0;
@@ -883,10 +824,10 @@ int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
 // the code bytes per chunk through LDS) k_dmv is faster.
 constexpr int kRwMinRows = 65536;
 
-template <int WT, int PRO, int EPI, int NCH, bool TR>
+template <int WT, int PRO, int EPI, int NCH>
 int rows_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv_rows<WT, PRO, EPI, NCH, TR>;
+    auto kern = k_dmv_rows<WT, PRO, EPI, NCH>;
     // staged row, prologue scratch, then the row results of the groups a
     // workgroup owns (occupancy taken with room for 8 groups)
     const size_t lds0 = (size_t)A.nb * kStage * 4 + (size_t)A.nb * 32 * 4 + 4 * 16 * (WT == Q4 ? 36 : 68) * 4;
@@ -912,29 +853,29 @@ int rows_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
     return launch_status("k_dmv_rows");
 }
 
-template <int WT, int PRO, int EPI, bool TR>
+template <int WT, int PRO, int EPI>
 int rows_nch(const DmvArgs& A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    if (A.nb * 32 > kDmvThreads * 8) return rows_go<WT, PRO, EPI, 2, TR>(A, st, ev0, ev1);
-    return rows_go<WT, PRO, EPI, 1, TR>(A, st, ev0, ev1);
+    if (A.nb * 32 > kDmvThreads * 8) return rows_go<WT, PRO, EPI, 2>(A, st, ev0, ev1);
+    return rows_go<WT, PRO, EPI, 1>(A, st, ev0, ev1);
 }
 
 // Launch with the items per thread the group needs (1, 2, 4, 8 or 12).
-template <int WT, int PRO, int EPI, int NCH, bool TR>
+template <int WT, int PRO, int EPI, int NCH>
 int dmv_r(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     const int tp = ((A.nb + 3) & ~3) + 4;
     const size_t lds = lds0 + (size_t)sh.rows * 4 * tp * 4;
     A.rows = sh.rows;
     const int items = (sh.rows * A.nb + kDmvThreads - 1) / kDmvThreads;
-    if (items <= 1) return dmv_go<WT, 1, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
-    if (items <= 2) return dmv_go<WT, 2, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
-    if (items <= 4) return dmv_go<WT, 4, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
-    if (items <= 8) return dmv_go<WT, 8, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
-    return dmv_go<WT, 12, PRO, EPI, NCH, TR>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 1) return dmv_go<WT, 1, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 2) return dmv_go<WT, 2, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 4) return dmv_go<WT, 4, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 8) return dmv_go<WT, 8, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
+    return dmv_go<WT, 12, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
 }
 
-template <int WT, bool TR>
+template <int WT>
 int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     const size_t K = (size_t)A.nb * 32;
@@ -949,35 +890,35 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
         const size_t lds = lds0 + (size_t)64 * 4 * tp * 4;
         // gate|up rows of 2048 (64 blocks) or 2304 (72 blocks) values
         if (A.nb == 64) {
-            if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64, TR>(A, lds, st, ev0, ev1);
-            return glu_go<WT, PRO_RES_RMS, 1, 64, TR>(A, lds, st, ev0, ev1);
+            if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64>(A, lds, st, ev0, ev1);
+            return glu_go<WT, PRO_RES_RMS, 1, 64>(A, lds, st, ev0, ev1);
         }
-        if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72, TR>(A, lds, st, ev0, ev1);
-        return glu_go<WT, PRO_RES_RMS, 2, 72, TR>(A, lds, st, ev0, ev1);
+        if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72>(A, lds, st, ev0, ev1);
+        return glu_go<WT, PRO_RES_RMS, 2, 72>(A, lds, st, ev0, ev1);
     }
     if constexpr (WT == Q4) {
         if (norm && epi != EPI_SWIGLU && A.N >= kRwMinRows && A.nb % kRwChunk == 0 && A.nb >= kRwChunk * kRwDepth) {
             // tall launches (lm heads): one fold chain per thread
             if (epi == EPI_ARGMAX)
-                return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_ARGMAX, TR>(A, st, ev0, ev1)
-                                      : rows_nch<WT, PRO_RES_RMS, EPI_ARGMAX, TR>(A, st, ev0, ev1);
-            return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_RAW, TR>(A, st, ev0, ev1)
-                                  : rows_nch<WT, PRO_RES_RMS, EPI_RAW, TR>(A, st, ev0, ev1);
+                return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_ARGMAX>(A, st, ev0, ev1)
+                                      : rows_nch<WT, PRO_RES_RMS, EPI_ARGMAX>(A, st, ev0, ev1);
+            return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_RAW>(A, st, ev0, ev1)
+                                  : rows_nch<WT, PRO_RES_RMS, EPI_RAW>(A, st, ev0, ev1);
         }
     }
-    if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1, TR>(A, lds0, R, st, ev0, ev1);
+    if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
     if (epi == EPI_ARGMAX) {
         if (pro == PRO_RMS)
-            return two ? dmv_r<WT, PRO_RMS, EPI_ARGMAX, 2, TR>(A, lds0, R, st, ev0, ev1)
-                       : dmv_r<WT, PRO_RMS, EPI_ARGMAX, 1, TR>(A, lds0, R, st, ev0, ev1);
-        return two ? dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 2, TR>(A, lds0, R, st, ev0, ev1)
-                   : dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 1, TR>(A, lds0, R, st, ev0, ev1);
+            return two ? dmv_r<WT, PRO_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
+                       : dmv_r<WT, PRO_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
+        return two ? dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
+                   : dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
     }
     if (pro == PRO_RMS)
-        return two ? dmv_r<WT, PRO_RMS, EPI_RAW, 2, TR>(A, lds0, R, st, ev0, ev1)
-                   : dmv_r<WT, PRO_RMS, EPI_RAW, 1, TR>(A, lds0, R, st, ev0, ev1);
-    return two ? dmv_r<WT, PRO_RES_RMS, EPI_RAW, 2, TR>(A, lds0, R, st, ev0, ev1)
-               : dmv_r<WT, PRO_RES_RMS, EPI_RAW, 1, TR>(A, lds0, R, st, ev0, ev1);
+        return two ? dmv_r<WT, PRO_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
+                   : dmv_r<WT, PRO_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
+    return two ? dmv_r<WT, PRO_RES_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
+               : dmv_r<WT, PRO_RES_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
 }
 
 }  // namespace
@@ -999,11 +940,7 @@ int decode_matvec(const DmvArgs& A, int wdtype, int pro, int epi, hipStream_t st
     if (!decode_matvec_supported(wdtype, A.nb * 32, A.N, pro, epi))
         return fail(NC_ERR_ARG, "decode matvec: unsupported [%d x %d] dtype %d prologue %d epilogue %d", A.N,
                     A.nb * 32, wdtype, pro, epi);
-    if (A.tree)
-        return wdtype == NC_Q4 ? dmv_dispatch<Q4, true>(A, pro, epi, st, ev0, ev1)
-                               : dmv_dispatch<Q8, true>(A, pro, epi, st, ev0, ev1);
-    return wdtype == NC_Q4 ? dmv_dispatch<Q4, false>(A, pro, epi, st, ev0, ev1)
-                           : dmv_dispatch<Q8, false>(A, pro, epi, st, ev0, ev1);
+    return wdtype == NC_Q4 ? dmv_dispatch<Q4>(A, pro, epi, st, ev0, ev1) : dmv_dispatch<Q8>(A, pro, epi, st, ev0, ev1);
 }
 
 // The next step's inputs for a token another kernel chose: the position is

@@ -98,6 +98,28 @@ __device__ __forceinline__ int load_pos(const int* dpos)
     return __hip_atomic_load(dpos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Greedy-token key of logit v at index idx: the largest key over a row is
+// the index greedy_sample (gten/sampler.cpp:30-38) picks.  That scan starts
+// from max = -inf, index 0, and takes a value only when `val > max`: NaN and
+// -inf are never taken (rank 0 here, so with nothing else the smallest index,
+// 0, wins), -0 ties with +0, and of equal values the first wins.  Key =
+// order-preserving bits << 32 | ~index.  Every key is nonzero, so 0 can pad.
+__device__ __forceinline__ unsigned long long greedy_key(float v, int idx)
+{
+    uint32_t u = __float_as_uint(v);
+    if (u == 0x80000000u) u = 0;
+    uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    if (v != v || u == 0xFF800000u) ord = 0;
+    return ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// Orders this thread's earlier global stores and atomics before its later
+// ones at agent scope, for data written with agent-scope atomic stores: those
+// write through the XCD's L2, and the wait for their completion is the whole
+// ordering they need (no L2 write-back, which a release fence adds for plain
+// stores).
+__device__ __forceinline__ void wait_stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
 // accesses, not for its global loads (which may stay in flight across it).
 __device__ __forceinline__ void lds_barrier()
@@ -172,26 +194,6 @@ __device__ __forceinline__ float q8_roundtrip_lane(float x, bool valid)
 }
 
 __device__ __forceinline__ float f16_roundtrip(float x) { return h2f(f2h(x)); }
-
-// Sum over aligned groups of g lanes (g a power of two, 1..64; uniform; all
-// lanes of the wave active) in a fixed tree order: quad_perm xor 1 and xor 2,
-// row_half_mirror (lane i with 7 - i) and row_mirror (i with 15 - i) DPP
-// moves, a ds_swizzle for xor 16, the two half-waves' lane 0 for 64.  Each
-// step adds two partial sums that are the same pair on both lanes, so every
-// lane of a group ends with the same bits.  This is the reduction of the tree
-// mode, which gives up the reference's sequential orders.
-__device__ __forceinline__ float group_sum(float v, int g)
-{
-    if (g >= 2) v += dpp_f<kDppQuadXor1>(v);
-    if (g >= 4) v += dpp_f<kDppQuadXor2>(v);
-    if (g >= 8) v += dpp_f<0x141>(v);
-    if (g >= 16) v += dpp_f<0x140>(v);
-    if (g >= 32) v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-    if (g >= 64)
-        v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    return v;
-}
 
 // Sequential fp32 sum of buf[0..n) in index order, every calling lane
 // reading the same addresses (an LDS broadcast), so every lane ends with the

@@ -325,8 +325,7 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
 
 // Greedy step epilogue for graph replay: every workgroup reduces a slice of
 // x to (value, first index), folded across workgroups with a 64-bit
-// atomicMax on key = (order-preserving bits of value) << 32 | ~index, so the
-// largest value wins and, among equal values, the smallest index.  The last
+// atomicMax on greedy_key (the index greedy_sample's scan takes).  The last
 // workgroup to finish writes the token to tokens[pos + 1], advances pos and
 // re-zeroes the scratch words for the next replay.
 __global__ __launch_bounds__(256) void k_argmax_advance(const float* __restrict__ x, int n, int32_t* __restrict__ tokens,
@@ -336,9 +335,7 @@ __global__ __launch_bounds__(256) void k_argmax_advance(const float* __restrict_
     const int tid = threadIdx.x;
     unsigned long long best = 0;
     for (int i = blockIdx.x * 256 + tid; i < n; i += gridDim.x * 256) {
-        const uint32_t u = __float_as_uint(x[i]);
-        const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-        const unsigned long long key = ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (uint32_t)i);
+        const unsigned long long key = greedy_key(x[i], i);
         best = key > best ? key : best;
     }
     sk[tid] = best;

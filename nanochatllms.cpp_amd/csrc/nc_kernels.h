@@ -59,9 +59,10 @@ int argmax_advance_launch(const float* x, int n, int32_t* tokens, int* dpos, uns
 // One top-k / temperature sampling step (gten/sampler.cpp:90-127) of the
 // logits row x[n] with the mt19937 state rng (625 words, updated): the token
 // goes to tokens[pos + 1], pos being *dpos (then advanced by one) when dpos
-// is given.  probs (optional): the n normalized weights.
+// is given.  probs (optional): the n normalized weights.  dset (optional):
+// device words {k, temp} (already clamped) read instead of top_k and temp.
 int sample_topk_launch(const float* logits, int n, float temp, int top_k, uint32_t* rng, int32_t* tokens, int* dpos,
-                       int pos, double* probs, hipStream_t st);
+                       int pos, double* probs, hipStream_t st, const double* dset = nullptr);
 void mt_seed_host(uint32_t seed, uint32_t* state);
 
 int ew_launch(int op, int adt, const uint8_t* a, int a_pitch, const uint8_t* b, int b_pitch, const uint16_t* bias,
@@ -76,16 +77,19 @@ int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k
                 uint8_t* out, int out_pitch, int hq, int hkv, int start, int n_ctx, hipStream_t st,
                 const int* dpos = nullptr, int max_ctx = 0);
 
+// Longest context (cached positions) the attention kernels take: Zephyr's
+// max_ctx (zephyr/zephyr.h:12); TinyLlama and MiniCPM stop at 2048.
+constexpr int kAttnMaxCtx = NC_MAX_CTX;
+
 // Decode attention with the q/k/v post-processing fused in (Q8 activations,
 // no qkv bias): raw = the qkv matvec's fp32 row [q | k | v]; the new k / v
 // rows are appended to the caches at the position (*dpos when set, else
 // pos); out = the attention output Act row.  rope_cur, when set, is the
 // position's RoPE (cos, sin) row at a fixed address (read instead of the
-// table row, so that load does not wait for the position).  tree: the
-// softmax denominator is summed as a tree, not in position order.
+// table row, so that load does not wait for the position).
+bool attn_decode_supported(int hq, int hkv, int max_ctx);
 int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
                        const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur = nullptr,
-                       bool tree = false);
+                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur = nullptr);
 
 }  // namespace nc

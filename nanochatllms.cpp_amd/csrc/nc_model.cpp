@@ -99,17 +99,20 @@ public:
     // shapes allow it (Q8 activations, RMS norms); NC_DECODE_FUSED=0 keeps
     // the op-by-op path.
     bool fused = false;
-    // Reduction order of the fused decode step: NC_REDUCE_ORDERED (the
-    // reference's sequential sums, bit-exact) or NC_REDUCE_TREE.
-    int reduce = NC_REDUCE_ORDERED;
     unsigned long long* am_scratch = nullptr;  // zeroed argmax scratch of the greedy step
     // Top-k sampling: the lm head writes logits only (sample_head), and the
-    // sampler draws from the device-held mt19937 state rng (625 words).
+    // sampler draws from the device-held mt19937 state rng (625 words) with
+    // the device-held setting sample_set = {k, temp}, so one captured
+    // sampling step serves every setting.
     bool sample_head = false;
     uint32_t* rng = nullptr;
+    double* sample_set = nullptr;
     hipGraphExec_t sample_graph = nullptr;
-    float sample_temp = 0.0f;
-    int sample_k = 0;
+    // Pinned host staging for every upload from host memory: the copy is a
+    // DMA from memory the model owns, and each upload waits for its copy
+    // before it returns (upload()), so no queued copy outlives its source.
+    uint8_t* hstage = nullptr;
+    size_t hstage_bytes = 0;
 
     // Matvec launch timing: a start/end event pair recorded on the model's
     // stream around every matvec launch while profiling is on.
@@ -121,13 +124,37 @@ public:
         size_t used = 0;
     } prof;
 
+    // The captured step graphs live as long as the model: each is captured
+    // on first use and only destroyed here, after the stream has drained.
     ~Decoder()
     {
+        if (st) (void)hipStreamSynchronize(st);
         if (step_graph) (void)hipGraphExecDestroy(step_graph);
         if (sample_graph) (void)hipGraphExecDestroy(sample_graph);
         for (hipEvent_t e : prof.ev) (void)hipEventDestroy(e);
         for (void* p : allocs) (void)hipFree(p);
+        if (hstage) (void)hipHostFree(hstage);
     }
+
+    // Copies n host bytes to device memory through the pinned staging
+    // buffer and waits for the copy (and everything queued before it).
+    int upload(void* dst, const void* src, size_t n, const char* what)
+    {
+        NC_CHECK_ARG(n <= hstage_bytes, "%s: %zu bytes exceed the %zu-byte staging buffer", what, n, hstage_bytes);
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, what);
+        std::memcpy(hstage, src, n);
+        e = hipMemcpyAsync(dst, hstage, n, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        return e == hipSuccess ? NC_OK : hip_fail(e, what);
+    }
+
+    // Waits for the stream when it leaves scope: calls that queue copies
+    // into caller memory drain them on every return path.
+    struct Drain {
+        hipStream_t s;
+        ~Drain() { (void)hipStreamSynchronize(s); }
+    };
 
     // Algorithmic HBM bytes of one matvec launch: every weight byte once,
     // plus each activation row read and each fp32 output row written.
@@ -251,12 +278,22 @@ public:
         NC_CHECK_ARG(c->n_layers > 0 && c->n_layers <= NC_MAX_LAYERS, "model: %d layers", c->n_layers);
         NC_CHECK_ARG(c->d_head == 64, "model: head size %d (kernels are built for 64)", c->d_head);
         NC_CHECK_ARG(c->n_embd % 64 == 0 && c->max_ctx > 0 && c->n_vocab > 0, "model: bad shape");
+        NC_CHECK_ARG(c->max_ctx <= kAttnMaxCtx, "model: max_ctx %d (the attention kernels take up to %d positions)",
+                     c->max_ctx, kAttnMaxCtx);
         NC_CHECK_ARG(c->arch >= NC_ARCH_LLAMA && c->arch <= NC_ARCH_OPENELM, "model: arch %d", c->arch);
         if (!initialized()) {
             int s = nc_init(0);
             if (s) return s;
         }
         st = stream_of(nullptr);
+        // staging for the largest upload: a prompt of max_ctx tokens (the
+        // generator state of 625 words and the small fields fit too)
+        hstage_bytes = std::max((size_t)8192, (size_t)(c->max_ctx + 1) * 4);
+        hipError_t he = hipHostMalloc((void**)&hstage, hstage_bytes, hipHostMallocDefault);
+        if (he != hipSuccess) {
+            hstage = nullptr;
+            return hip_fail(he, "hipHostMalloc");
+        }
         adt = c->wdtype == NC_F16 ? NC_F16 : NC_Q8;
         if (const char* g = std::getenv("NC_DECODE_GRAPH")) use_graph = std::atoi(g) != 0;
         d = c->n_embd;
@@ -750,11 +787,9 @@ public:
         if (!dpos && (s = embed_launch(&emb, tokens + pos, x0 + (size_t)pos * pd, pd, adt, 1, minicpm ? 12.0f : 1.0f,
                                        st, nullptr, cur_x0)))
             return s;
-        const bool tree = reduce == NC_REDUCE_TREE;
         DmvArgs base;
         base.pos = pos;
         base.dpos = dpos;
-        base.tree = tree;
         base.res_pitch = pd;
         base.bscale = bs;
         for (int l = 0; l < cfg.n_layers; l++) {
@@ -778,7 +813,7 @@ public:
             }
             if (!y.bq) {
                 if ((s = attn_decode_launch(qkv_raw, y.hq, y.hkv, y.qn, y.kn, rope, d_half, pos, dpos, y.kc, y.vc, pkv,
-                                            attn, cfg.max_ctx, st, dpos ? cur_rope : nullptr, tree)))
+                                            attn, cfg.max_ctx, st, dpos ? cur_rope : nullptr)))
                     return s;
             } else {
                 if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half,
@@ -879,12 +914,11 @@ public:
         NC_CHECK_ARG(toks && out && n > 0 && n <= cfg.max_ctx && sp >= 0 && sp < n,
                      "logits: %d tokens from %d with max_ctx %d", n, sp, cfg.max_ctx);
         NC_CHECK_ARG(sp == 0 || sp <= n_cur, "logits: start_pos %d beyond the %d cached rows", sp, n_cur);
-        hipError_t e = hipMemcpyAsync(tokens, toks, (size_t)n * 4, hipMemcpyHostToDevice, st);
-        if (e != hipSuccess) return hip_fail(e, "token upload");
-        int s = forward(sp, n);
-        if (s) return s;
+        Drain drain{st};
+        int s = upload(tokens, toks, (size_t)n * 4, "token upload");
+        if (s || (s = forward(sp, n))) return s;
         n_cur = n;
-        e = hipMemcpyAsync(out, logits, (size_t)cfg.n_vocab * 4, hipMemcpyDeviceToHost, st);
+        hipError_t e = hipMemcpyAsync(out, logits, (size_t)cfg.n_vocab * 4, hipMemcpyDeviceToHost, st);
         if (e == hipSuccess) e = hipStreamSynchronize(st);
         return e == hipSuccess ? NC_OK : hip_fail(e, "logits download");
     }
@@ -892,9 +926,8 @@ public:
     int prefill(const int32_t* prompt, int np)
     {
         NC_CHECK_ARG(prompt && np > 0 && np < cfg.max_ctx + 1, "prefill: %d prompt tokens, max_ctx %d", np, cfg.max_ctx);
-        hipError_t e = hipMemcpyAsync(tokens, prompt, (size_t)np * 4, hipMemcpyHostToDevice, st);
-        if (e != hipSuccess) return hip_fail(e, "token upload");
-        int s = forward(0, np);
+        int s = upload(tokens, prompt, (size_t)np * 4, "token upload");
+        if (s || (s = forward(0, np))) return s;
         if (s) return s;
         if ((s = argmax_launch(logits, cfg.n_vocab, tokens + np, st))) return s;
         n_cur = np;
@@ -917,8 +950,8 @@ public:
         if (use_graph && !prof.on) {
             if (!step_graph && (s = capture_step_graph())) return s;
             const int pos = n_cur;
-            hipError_t e = hipMemcpyAsync(step_pos, &pos, 4, hipMemcpyHostToDevice, st);
-            if (e != hipSuccess) return hip_fail(e, "decode: position upload");
+            if ((s = upload(step_pos, &pos, 4, "decode: position upload"))) return s;
+            hipError_t e = hipSuccess;
             if (fused) {
                 // the first replayed step's inputs (later steps' come from the
                 // lm head before them): its token's embedding and RoPE row
@@ -929,8 +962,6 @@ public:
                                                       hipMemcpyDeviceToDevice, st)) != hipSuccess)
                     return hip_fail(e, "decode: rope row");
             }
-            // the upload reads host memory asynchronously: wait before `pos` dies
-            if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "decode: sync");
             for (int i = 0; i < n_steps; i++)
                 if ((e = hipGraphLaunch(step_graph, st)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
             n_cur += n_steps;
@@ -948,9 +979,9 @@ public:
     // One sampling step after the logits of position pos: the sampler writes
     // tokens[pos + 1] (pos from the device when dpos is given, which it then
     // advances) and, for the fused step, the next step's input rows.
-    int sample_after(float temp, int k, int* dpos, int pos)
+    int sample_after(float temp, int k, int* dpos, int pos, const double* dset = nullptr)
     {
-        int s = sample_topk_launch(logits, cfg.n_vocab, temp, k, rng, tokens, dpos, pos, nullptr, st);
+        int s = sample_topk_launch(logits, cfg.n_vocab, temp, k, rng, tokens, dpos, pos, nullptr, st, dset);
         if (s || !fused || !dpos) return s;
         DmvArgs a;
         next_input_fields(&a, dpos);
@@ -958,13 +989,9 @@ public:
     }
 
     // A decode step that samples instead of taking the greedy token, as a
-    // HIP graph (temp and k are baked in).
-    int capture_sample_graph(float temp, int k)
+    // HIP graph; the sampler reads its setting from sample_set.
+    int capture_sample_graph()
     {
-        if (sample_graph) {
-            (void)hipGraphExecDestroy(sample_graph);
-            sample_graph = nullptr;
-        }
         hipError_t e = hipStreamSynchronize(st);
         if (e != hipSuccess) return hip_fail(e, "capture: sync");
         if ((e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal)) != hipSuccess)
@@ -974,7 +1001,7 @@ public:
         sample_head = true;
         int s = forward(0, 0, step_pos);
         sample_head = false;
-        if (!s) s = sample_after(temp, k, step_pos, 0);
+        if (!s) s = sample_after(0.0f, 0, step_pos, 0, sample_set);
         prof.on = was_on;
         hipGraph_t g = nullptr;
         e = hipStreamEndCapture(st, &g);
@@ -985,10 +1012,7 @@ public:
         if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
         e = hipGraphInstantiate(&sample_graph, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
-        if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
-        sample_temp = temp;
-        sample_k = k;
-        return NC_OK;
+        return e == hipSuccess ? NC_OK : hip_fail(e, "hipGraphInstantiate");
     }
 
     // topk_sample (gten/sampler.cpp:63-143) with std::mt19937(seed): the
@@ -1005,23 +1029,24 @@ public:
         int s;
         if (!rng && (s = alloc_t(&rng, 625 * 4))) return s;
         if (!step_pos && (s = alloc_t(&step_pos, 16))) return s;
+        if (!sample_set && (s = alloc_t(&sample_set, 16))) return s;
         uint32_t st0[625];
         mt_seed_host(seed, st0);
-        hipError_t e = hipMemcpyAsync(rng, st0, sizeof(st0), hipMemcpyHostToDevice, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(tokens, prompt, (size_t)np * 4, hipMemcpyHostToDevice, st);
-        if (e != hipSuccess) return hip_fail(e, "generate_topk: upload");
+        const double set[2] = {(double)k, (double)t};
+        if ((s = upload(rng, st0, sizeof(st0), "generate_topk: generator upload")) ||
+            (s = upload(sample_set, set, sizeof(set), "generate_topk: setting upload")) ||
+            (s = upload(tokens, prompt, (size_t)np * 4, "generate_topk: token upload")))
+            return s;
         if ((s = forward(0, np))) return s;
         n_cur = np;
         n_prompt = np;
         const bool graph = use_graph && !prof.on;
         const int first = np - 1;
-        if (graph && (e = hipMemcpyAsync(step_pos, &first, 4, hipMemcpyHostToDevice, st)) != hipSuccess)
-            return hip_fail(e, "generate_topk: position upload");
+        if (graph && (s = upload(step_pos, &first, 4, "generate_topk: position upload"))) return s;
         if ((s = sample_after(t, k, graph ? step_pos : nullptr, first))) return s;
-        // the uploads read host memory asynchronously: wait before it dies
-        if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "generate_topk: sync");
+        hipError_t e = hipSuccess;
         if (graph) {
-            if ((!sample_graph || sample_temp != t || sample_k != k) && (s = capture_sample_graph(t, k))) return s;
+            if (!sample_graph && (s = capture_sample_graph())) return s;
             for (int i = 1; i < n_gen; i++)
                 if ((e = hipGraphLaunch(sample_graph, st)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
             n_cur += n_gen - 1;
@@ -1048,22 +1073,6 @@ public:
         int k = 0;
         while (k < cnt && out[k] != cfg.eos) k++;  // greedy_sample stops at eos
         *n_out = k;
-        return NC_OK;
-    }
-
-    // A new reduction order for the fused decode step; captured step graphs
-    // hold the old kernels and are captured again on their next use.
-    int set_reduce(int mode)
-    {
-        NC_CHECK_ARG(mode == NC_REDUCE_ORDERED || mode == NC_REDUCE_TREE, "set_reduce: mode %d", mode);
-        hipError_t e = hipStreamSynchronize(st);
-        if (e != hipSuccess) return hip_fail(e, "set_reduce");
-        if (mode == reduce) return NC_OK;
-        reduce = mode;
-        if (step_graph) (void)hipGraphExecDestroy(step_graph);
-        if (sample_graph) (void)hipGraphExecDestroy(sample_graph);
-        step_graph = nullptr;
-        sample_graph = nullptr;
         return NC_OK;
     }
 
@@ -1134,12 +1143,6 @@ int nc_model_logits(void* model, const int32_t* tokens, int n_tokens, int start_
 {
     NC_CHECK_ARG(model, "model: null");
     return static_cast<Decoder*>(model)->logits_call(tokens, n_tokens, start_pos, logits);
-}
-
-int nc_model_set_reduce(void* model, int mode)
-{
-    NC_CHECK_ARG(model, "model: null");
-    return static_cast<Decoder*>(model)->set_reduce(mode);
 }
 
 int nc_model_layer_out(void* model, int layer, int row, void* ref_bytes)

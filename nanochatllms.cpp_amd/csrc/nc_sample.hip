@@ -160,6 +160,9 @@ struct SampleArgs {
     int* dpos;        // device position, advanced by one (or null: pos)
     int pos;
     double* probs;    // optional: the n normalized weights
+    // optional: {k, temp} read on the device instead of the two fields
+    // above (a captured step then serves every setting)
+    const double* dset;
 };
 
 __global__ __launch_bounds__(kSmThreads) void k_sample_topk(SampleArgs A)
@@ -188,7 +191,9 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_topk(SampleArgs A)
     __shared__ double s_sum;
 
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int n = A.n, k = A.k;
+    const int n = A.n;
+    const int k = A.dset ? (int)A.dset[0] : A.k;
+    const double temp = A.dset ? A.dset[1] : A.temp;
     const int pos = A.dpos ? load_pos(A.dpos) : A.pos;
     for (int i = tid; i < 625; i += kSmThreads) mt[i] = A.rng[i];
     if (A.probs)
@@ -285,7 +290,7 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_topk(SampleArgs A)
         const uint64_t c = U.cand[tid];
         my_idx = (int)(uint32_t)c;
         const float x = s_nan ? A.logits[my_idx] : fkey_value((uint32_t)(c >> 32));
-        ev[tid] = exp_ref((double)x / A.temp);
+        ev[tid] = exp_ref((double)x / temp);
     }
     lds_barrier();
     if (tid == 0) {
@@ -371,15 +376,15 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_topk(SampleArgs A)
 }
 
 int sample_topk_launch(const float* logits, int n, float temp, int top_k, uint32_t* rng, int32_t* tokens, int* dpos,
-                       int pos, double* probs, hipStream_t st)
+                       int pos, double* probs, hipStream_t st, const double* dset)
 {
     // sampler.cpp:66-67: std::min(top_k, 1000), std::min(temp, 2.0f)
     const int k = 1000 < top_k ? 1000 : top_k;
     const float t = 2.0f < temp ? 2.0f : temp;
     NC_CHECK_ARG(logits && rng && tokens && n >= 2, "sample_topk: bad arguments (n = %d)", n);
-    NC_CHECK_ARG(k >= 1 && k <= n, "sample_topk: top_k %d for %d logits", top_k, n);
-    NC_CHECK_ARG(t > 0.0f, "sample_topk: temperature %g", (double)temp);
-    SampleArgs a{logits, n, k, (double)t, rng, tokens, dpos, pos, probs};
+    NC_CHECK_ARG(dset || (k >= 1 && k <= n), "sample_topk: top_k %d for %d logits", top_k, n);
+    NC_CHECK_ARG(dset || t > 0.0f, "sample_topk: temperature %g", (double)temp);
+    SampleArgs a{logits, n, k, (double)t, rng, tokens, dpos, pos, probs, dset};
     hipLaunchKernelGGL(k_sample_topk, dim3(1), dim3(kSmThreads), 0, st, a);
     return launch_status("k_sample_topk");
 }

@@ -2,12 +2,15 @@
 
 Runs in the build container only (it needs oracle/_ref/libgten_ref.so, the
 reference's gten sources compiled by oracle/Makefile).  For every workload it
-builds the model from the reference's modules with the synthetic weights,
-runs Model::logits on the prompt (start_pos = 0) and the reference's greedy
-loop, and records the prompt, the generated tokens, digests of the prefill
-logits and of every layer's residual-stream row, and the top prefill logits.
-Small models of every architecture are recorded the same way, with their
-full logits.
+builds the model from the reference's modules with the synthetic weights and
+runs greedy_sample's loop (src/gten/sampler.cpp:17-48) over the reference's
+Model::logits: the prompt with start_pos = 0, then each decode step with
+start_pos = n - 1 (the reference's K/V caches carry the earlier rows).  It
+records the prompt, the generated tokens, digests of the prefill logits and
+of every layer's residual-stream row, the top prefill logits, and at decode
+steps 1, 2, 16, 64 and the last one the digests of that step's fp32 logits
+and of every layer's row at its position.  Small models of every
+architecture are recorded the same way, with their full prefill logits.
 
     python tests/golden/make_golden.py [workload ...]
     python tests/golden/make_golden.py --topk [workload ...]   (sampled streams)
@@ -24,13 +27,22 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 import oracle_lib as OL  # noqa: E402
-from workloads import SMALL, config_of, prompt_of  # noqa: E402
+from workloads import LONG, SMALL, WIDE, config_of, prompt_of  # noqa: E402
 from nc_pkg import nc  # noqa: E402
 
+# decode steps (1 = the first step after the prompt) whose digests are kept
+DIGEST_STEPS = (1, 2, 16, 64)
 
 
 def sha(b):
     return hashlib.sha256(np.ascontiguousarray(b).tobytes()).hexdigest()
+
+
+def greedy_pick(logits):
+    """The scan of greedy_sample (src/gten/sampler.cpp:30-38): max starts at
+    -inf and index 0, and a value is taken only when `val > max`."""
+    x = np.where(np.isnan(logits), -np.inf, logits)
+    return int(np.argmax(x)) if np.any(x > -np.inf) else 0
 
 
 def record(name, w, full_logits=False):
@@ -39,26 +51,47 @@ def record(name, w, full_logits=False):
     t0 = time.time()
     m = ref.model_create(cfg, w["seed"])
     prompt = prompt_of(w)
-    logits = np.zeros(cfg.n_vocab, np.float32)
-    ref.model_logits(m, OL.ptr(prompt), len(prompt), 0, OL.ptr(logits))
     adt = OL.F16 if w["wdtype"] == OL.F16 else OL.Q8
     rb = OL.row_bytes(adt, cfg.n_embd)
-    layers = []
-    for l in range(cfg.n_layers):
-        p = ref.model_layer_out(m, l, len(prompt) - 1)
-        layers.append(sha(np.ctypeslib.as_array((OL.C.c_uint8 * rb).from_address(p))))
-    top = np.argsort(-logits, kind="stable")[:16]
-    out = np.zeros(w["gen"], np.int32)
-    n = ref.generate_greedy(m, OL.ptr(prompt), len(prompt), w["gen"], OL.ptr(out))
+
+    def layer_digests(row):
+        out = []
+        for l in range(cfg.n_layers):
+            p = ref.model_layer_out(m, l, row)
+            out.append(sha(np.ctypeslib.as_array((OL.C.c_uint8 * rb).from_address(p))))
+        return out
+
+    logits = np.zeros(cfg.n_vocab, np.float32)
+    ref.model_logits(m, OL.ptr(prompt), len(prompt), 0, OL.ptr(logits))
+    prefill = logits.copy()
+    layers = layer_digests(len(prompt) - 1)
+    top = np.argsort(-prefill, kind="stable")[:16]
+    # greedy_sample's loop, step by step
+    toks = [int(t) for t in prompt]
+    gen, steps = [], []
+    for i in range(w["gen"]):
+        if i > 0:
+            seq = np.array(toks, np.int32)
+            ref.model_logits(m, OL.ptr(seq), len(seq), len(seq) - 1, OL.ptr(logits))
+        t = greedy_pick(logits)
+        last = i == w["gen"] - 1 or t == cfg.eos
+        if i > 0 and (i in DIGEST_STEPS or last):
+            steps.append(dict(step=i, pos=len(toks) - 1, logits_sha256=sha(logits),
+                              layer_out_sha256=layer_digests(len(toks) - 1)))
+        if t == cfg.eos:
+            break
+        gen.append(t)
+        toks.append(t)
     ref.model_free(m)
-    fx = dict(workload=name, seed=w["seed"], prompt=prompt.tolist(), tokens=out[:n].tolist(),
-              prefill_logits_sha256=sha(logits), layer_out_sha256=layers,
-              prefill_top=[[int(i), float(logits[i])] for i in top], seconds=round(time.time() - t0, 1))
+    fx = dict(workload=name, seed=w["seed"], prompt=prompt.tolist(), tokens=gen,
+              prefill_logits_sha256=sha(prefill), layer_out_sha256=layers,
+              prefill_top=[[int(i), float(prefill[i])] for i in top], decode_steps=steps,
+              seconds=round(time.time() - t0, 1))
     with open(os.path.join(HERE, f"{name}.json"), "w") as f:
         json.dump(fx, f)
     if full_logits:
-        np.save(os.path.join(HERE, f"{name}.prefill_logits.npy"), logits)
-    print(name, n, "tokens", fx["seconds"], "s", flush=True)
+        np.save(os.path.join(HERE, f"{name}.prefill_logits.npy"), prefill)
+    print(name, len(gen), "tokens", fx["seconds"], "s", flush=True)
 
 
 # top-k / temperature runs: (temp, top_k, seed); temp 2.5 is clamped to 2.0
@@ -94,10 +127,11 @@ def main(argv):
             else:
                 record_topk(name, nc.WORKLOADS[name], TOPK_FULL, 64)
         return
-    names = argv or list(SMALL) + list(nc.WORKLOADS)
+    models = dict(SMALL, **WIDE, **LONG)
+    names = argv or list(models) + list(nc.WORKLOADS)
     for name in names:
-        if name in SMALL:
-            record(name, SMALL[name], full_logits=True)
+        if name in models:
+            record(name, models[name], full_logits=name in SMALL)
         else:
             record(name, nc.WORKLOADS[name], full_logits=name == "tinyllama-q4")
 

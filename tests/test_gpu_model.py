@@ -2,9 +2,13 @@
 
 Small models of every architecture: device weights, prefill logits, every
 layer's residual row and the greedy stream must equal the oracle's and the
-golden fixtures made by the reference (tests/golden/).  Full-size workloads:
-the greedy stream and the prefill digests must equal the reference's golden
-fixtures.
+golden fixtures made by the reference (tests/golden/).  Every model with a
+fixture -- small, full-width, long-context and the five full-size
+workloads -- replays the reference's greedy loop step by step: the prefill
+digests, and at the recorded decode steps the digests of the step's fp32
+logits and of every layer's residual row, must equal the reference's, and
+the greedy stream (also through the captured step graph) must equal its
+stream.
 """
 import hashlib
 import json
@@ -14,7 +18,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as OL
-from workloads import ALL, SMALL, config_of, prompt_of
+from workloads import ALL, LONG, SMALL, WIDE, config_of, prompt_of
 
 pytestmark = pytest.mark.gpu
 
@@ -118,15 +122,88 @@ def test_full_workload_stream(gpu, name):
     m.close()
 
 
-@pytest.mark.parametrize("max_ctx", [200, 400])
-@pytest.mark.parametrize("name", ["small-llama-q4", "small-openelm-q8"])
+def greedy_pick(logits):
+    """greedy_sample's scan (src/gten/sampler.cpp:30-38): max from -inf,
+    index 0, a value taken only when `val > max`."""
+    x = np.where(np.isnan(logits), -np.inf, logits)
+    return int(np.argmax(x)) if np.any(x > -np.inf) else 0
+
+
+@pytest.mark.parametrize("name", list(SMALL) + list(WIDE) + list(LONG) + FULL)
+def test_decode_steps_match_reference(gpu, name):
+    """The reference's greedy loop replayed through Model::logits (start_pos
+    = n - 1 after the prompt), every step a fused (or op-by-op) decode step
+    with direct launches: at the recorded steps the fp32 logits and every
+    layer's row at the step's position equal the reference's bit for bit,
+    and each step's greedy token is the reference's.  Then the same stream
+    through the captured step graph."""
+    w = ALL[name]
+    g = golden(name)
+    prompt = prompt_of(w)
+    assert prompt.tolist() == g["prompt"]
+    cfg = config_of(w)
+    m = gpu.Model(config_of(w, cls=gpu.ModelConfig))
+    m.init_synthetic(w["seed"])
+    logits = m.logits(prompt, 0)
+    assert sha(logits) == g["prefill_logits_sha256"], "prefill logits"
+    for l, digest in enumerate(g["layer_out_sha256"]):
+        assert sha(m.layer_out(l, len(prompt) - 1)) == digest, f"prefill layer {l}"
+    steps = {s["step"]: s for s in g["decode_steps"]}
+    toks = prompt.tolist()
+    ref = g["tokens"]
+    seen = set()
+    for i in range(w["gen"]):
+        if i > 0:
+            logits = m.logits(np.array(toks, np.int32), len(toks) - 1)
+        if i in steps:
+            s = steps[i]
+            assert s["pos"] == len(toks) - 1
+            assert sha(logits) == s["logits_sha256"], f"step {i} (position {s['pos']}): logits"
+            for l, digest in enumerate(s["layer_out_sha256"]):
+                assert sha(m.layer_out(l, len(toks) - 1)) == digest, f"step {i}: layer {l}"
+            seen.add(i)
+        t = greedy_pick(logits)
+        if i == len(ref):  # the reference stopped at eos here
+            assert t == cfg.eos
+            break
+        assert t == ref[i], f"step {i}: token {t}, reference {ref[i]}"
+        toks.append(t)
+    assert seen == set(steps)
+    m.close()
+    m = gpu.Model(config_of(w, cls=gpu.ModelConfig))
+    m.init_synthetic(w["seed"])
+    assert m.generate(prompt, w["gen"]).tolist() == ref
+    m.close()
+
+
+@pytest.mark.parametrize("max_ctx", [200, 1024, 4096])
+@pytest.mark.parametrize("name", ["small-llama-q8", "small-zephyr-q8", "small-zephyr-q4"])
 def test_small_model_stream_with_larger_cache(gpu, name, max_ctx):
-    """The decode attention sizes its register prefetch to the cache: the
-    cache sizes of no full workload (200, 400 positions) give the same
-    stream."""
+    """Caches larger than the sequence (the attention kernels size their
+    shared memory and prefetch by the cache) give the same varying streams,
+    up to the reference's default context (1024) and the longest (4096)."""
     w = SMALL[name]
     g = golden(name)
     m = gpu.Model(config_of(w, cls=gpu.ModelConfig, max_ctx=max_ctx))
     m.init_synthetic(w["seed"])
     assert m.generate(prompt_of(w), w["gen"]).tolist() == g["tokens"]
     m.close()
+
+
+def test_full_workload_at_default_context(gpu):
+    """TinyLlama-Q4 built with the reference's default inference context of
+    1024 positions (src/nanochat.cpp:40, sampler.cpp:13): the fused decode
+    step sized for it gives the workload's stream."""
+    w = ALL["tinyllama-q4"]
+    m = gpu.Model(config_of(w, cls=gpu.ModelConfig, max_ctx=1024))
+    m.init_synthetic(w["seed"])
+    assert m.generate(prompt_of(w), w["gen"]).tolist() == golden("tinyllama-q4")["tokens"]
+    m.close()
+
+
+def test_context_limit(gpu):
+    """max_ctx beyond the longest context of the reference's models is
+    refused at creation, not at the first decode step."""
+    w = SMALL["small-llama-q4"]
+    with pytest.raises(gpu.HipError, match="max_ctx"):
+        gpu.Model(config_of(w, cls=gpu.ModelConfig, max_ctx=gpu.MAX_CTX + 1))

@@ -205,6 +205,24 @@ ATTN_CASES = [
     (F16, 32, 32, 256, 255),
     (F16, 4, 4, 128, 0),
     (F16, 8, 2, 45, 20),
+    # contexts of the reference's models: 1024 (its default), 2048, 4096; the
+    # single-row softmax sum changes from one wavefront's loop to the exact
+    # workgroup sum above 1024 positions; n mod 8 / mod 32 edges; the prefill
+    # kernel's 8, 4 and 2 rows per workgroup (m <= 1024, <= 2048, beyond)
+    (Q8, 32, 4, 1024, 1023),
+    (Q8, 32, 4, 1025, 1024),
+    (Q8, 32, 4, 1031, 1030),
+    (Q8, 36, 36, 2048, 2047),
+    (Q8, 16, 4, 2053, 2040),
+    (Q8, 32, 4, 4096, 4095),
+    (Q8, 4, 1, 4093, 4080),
+    (Q8, 8, 2, 1100, 0),
+    (Q8, 4, 1, 3000, 0),
+    (F16, 32, 32, 1024, 1023),
+    (F16, 32, 32, 2049, 2048),
+    (F16, 32, 32, 4096, 4095),
+    (F16, 4, 4, 4090, 4081),
+    (F16, 4, 2, 1500, 0),
 ]
 
 

@@ -34,7 +34,43 @@ SMALL = {
 }
 
 
-ALL = dict(SMALL, **nc.WORKLOADS)
+# Models at the workloads' widths but two or three layers deep: their
+# single-row steps run the fused decode kernels (the gate|up kernel is built
+# for rows of 2048 and 2304 values), checked against the oracle.
+WIDE = {
+    "wide-llama-q4": dict(arch=nc.LLAMA, wdtype=nc.Q4, n_vocab=32000, n_embd=2048, n_layers=2, n_heads=32,
+                          n_kv_heads=4, n_ffn=5632, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0001),
+    "wide-llama-q8": dict(arch=nc.LLAMA, wdtype=nc.Q8, n_vocab=32000, n_embd=2048, n_layers=2, n_heads=32,
+                          n_kv_heads=4, n_ffn=5632, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0002),
+    # MiniCPM's own vocabulary: its tied lm head runs the row-chain kernel
+    "wide-minicpm-q4": dict(arch=nc.MINICPM, wdtype=nc.Q4, n_vocab=122753, n_embd=2304, n_layers=2, n_heads=36,
+                            n_kv_heads=36, n_ffn=5760, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0003),
+    "wide-openelm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=32000, n_embd=2048, n_layers=3,
+                            n_heads=[16, 16, 20], n_kv_heads=[4, 4, 5], n_ffn=[1024, 4608, 8192], eos=-1,
+                            rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0004),
+}
+
+# Long contexts: the reference's default inference context is 1024 positions
+# (src/nanochat.cpp:40) and its models allow up to 2048 (TinyLlama, MiniCPM)
+# or 4096 (Zephyr).  One-layer models whose prompts fill most of such a
+# context; their decode steps cross the 1024-position point where a softmax
+# sum changes from one wavefront's loop to the exact workgroup sum.  The
+# llama and openelm models run the fused decode kernels (full widths), the
+# other two the op-by-op kernels (Q8 and fp16 activations).  Fixtures come
+# from the reference build like the others.
+LONG = {
+    "long-llama-q4": dict(arch=nc.LLAMA, wdtype=nc.Q4, n_vocab=2000, n_embd=2048, n_layers=1, n_heads=32,
+                          n_kv_heads=4, n_ffn=256, eos=-1, rope_pct=1.0, prompt=1012, gen=24, seed=0x10C0001),
+    "long-openelm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=2000, n_embd=2048, n_layers=1, n_heads=[16],
+                            n_kv_heads=[4], n_ffn=[512], eos=-1, rope_pct=1.0, prompt=2036, gen=12,
+                            seed=0x10C0002),
+    "long-minicpm-q8": dict(arch=nc.MINICPM, wdtype=nc.Q8, n_vocab=1000, n_embd=256, n_layers=1, n_heads=4,
+                            n_kv_heads=4, n_ffn=512, eos=-1, rope_pct=1.0, prompt=1500, gen=40, seed=0x10C0003),
+    "long-zephyr-f16": dict(arch=nc.ZEPHYR, wdtype=nc.F16, n_vocab=1000, n_embd=256, n_layers=1, n_heads=4,
+                            n_kv_heads=4, n_ffn=512, eos=-1, rope_pct=0.25, prompt=4080, gen=16, seed=0x10C0004),
+}
+
+ALL = dict(SMALL, **WIDE, **LONG, **nc.WORKLOADS)
 
 
 def config_of(w, cls=OL.Config, max_ctx=None):
