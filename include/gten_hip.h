@@ -98,6 +98,17 @@ int nc_token_embed(const nc_tensor* table, const int32_t* tokens, nc_tensor* out
  * lane/block summation order; out dtype F32 gives the raw dot products,
  * an activation dtype stores them requantized. */
 int nc_matmul_2d(const nc_tensor* x, const nc_tensor* w, nc_tensor* out, int start, int n_ctx, void* stream);
+/* nc_matmul_2d without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  An
+ * activation-dtype output is staged in a fixed per-GPU array of
+ * NC_NOALLOC_STAGE_BYTES instead of library-allocated memory, so
+ * (n_ctx - start) * w->rows * 4 must not exceed it (else NC_ERR_ARG); an F32
+ * output needs no staging.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race. */
+#define NC_NOALLOC_STAGE_BYTES (8u << 20)
+int nc_matmul_2d_noalloc(const nc_tensor* x, const nc_tensor* w, nc_tensor* out, int start, int n_ctx,
+                         void* stream);
 /* rms_norm (ops.h:26): d_norm = cols for the 2-D op, the head size for the
  * per-head (3-D) op; w is fp16 [d_norm]. */
 int nc_rms_norm(const nc_tensor* x, const uint16_t* w, nc_tensor* out, int d_norm, int start, int n_ctx,

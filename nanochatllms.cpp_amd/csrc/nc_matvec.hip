@@ -401,6 +401,80 @@ int stage_buffer(size_t bytes, float** out)
 
 }  // namespace
 
+// nc_matmul_2d_noalloc's staging: a file-scope device array.  Every GPU the
+// library runs on holds its own copy, at its own address, until the process
+// ends.  In host code `scratch` only names a host-side stand-in; the device
+// address comes from hipGetSymbolAddress, taken once per device with that
+// device current (nc_init, or the entry point's first call on a device) and
+// kept in g_scratch.  Kernels get that address as an argument.
+static __device__ __align__(256) float scratch[NC_NOALLOC_STAGE_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr size_t kNoAllocStageBytes = NC_NOALLOC_STAGE_BYTES;
+constexpr int kMaxDevices = 64;
+float* g_scratch[kMaxDevices] = {};
+
+int scratch_for_current(float** out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    int s = noalloc_scratch_setup(dev);
+    if (s) return s;
+    *out = g_scratch[dev];
+    return NC_OK;
+}
+
+}  // namespace
+
+namespace nc {
+
+int noalloc_scratch_setup(int dev)
+{
+    if (dev < 0 || dev >= kMaxDevices) return fail(NC_ERR_ARG, "staging array: device %d", dev);
+    if (g_scratch[dev]) return NC_OK;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch[dev] = static_cast<float*>(p);
+    return NC_OK;
+}
+
+}  // namespace nc
+
+// The same as nc_matmul_2d, with an activation-dtype output staged in the
+// device's fixed array instead of library-allocated memory: no allocation
+// anywhere on this path.
+extern "C" int nc_matmul_2d_noalloc(const nc_tensor* x, const nc_tensor* w, nc_tensor* out, int start, int n_ctx,
+                                    void* stream)
+{
+    NC_CHECK_ARG(x && w && out && x->data && w->data && out->data, "matmul_2d_noalloc: null tensor");
+    NC_CHECK_ARG(x->cols == w->cols, "matmul_2d_noalloc: x has %d columns, w has %d", x->cols, w->cols);
+    NC_CHECK_ARG(out->cols == w->rows, "matmul_2d_noalloc: out has %d columns, w has %d rows", out->cols, w->rows);
+    NC_CHECK_ARG(start >= 0 && start <= n_ctx && n_ctx <= x->rows && n_ctx <= out->rows,
+                 "matmul_2d_noalloc: rows [%d, %d)", start, n_ctx);
+    const int rows = n_ctx - start;
+    if (rows == 0) return NC_OK;
+    hipStream_t st = stream_of(stream);
+    const uint8_t* xr = (const uint8_t*)x->data + (size_t)start * x->pitch;
+    if (out->dtype == NC_F32) {
+        NC_CHECK_ARG(out->pitch % 4 == 0, "matmul_2d_noalloc: fp32 pitch %d", out->pitch);
+        return matvec_raw(xr, x->dtype, x->pitch, rows, w, (float*)((uint8_t*)out->data + (size_t)start * out->pitch),
+                          out->pitch / 4, st);
+    }
+    const size_t need = (size_t)rows * w->rows * 4;
+    NC_CHECK_ARG(need <= kNoAllocStageBytes,
+                 "matmul_2d_noalloc: %d rows x %d outputs need %zu staging bytes, more than the %zu-byte array", rows,
+                 w->rows, need, kNoAllocStageBytes);
+    float* stage = nullptr;
+    int s = scratch_for_current(&stage);
+    if (s) return s;
+    if ((s = matvec_raw(xr, x->dtype, x->pitch, rows, w, stage, w->rows, st))) return s;
+    return write_rows(stage, w->rows, (uint8_t*)out->data + (size_t)start * out->pitch, out->pitch, out->dtype, w->rows,
+                      rows, st);
+}
+
 extern "C" int nc_matmul_2d(const nc_tensor* x, const nc_tensor* w, nc_tensor* out, int start, int n_ctx, void* stream)
 {
     NC_CHECK_ARG(x && w && out && x->data && w->data && out->data, "matmul_2d: null tensor");

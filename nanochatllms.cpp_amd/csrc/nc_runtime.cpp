@@ -52,6 +52,8 @@ int nc_init(int device)
     if (device < 0 || device >= n) return fail(NC_ERR_ARG, "nc_init: device %d of %d", device, n);
     if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
     if ((e = hipStreamCreate(&g_stream)) != hipSuccess) return hip_fail(e, "hipStreamCreate");
+    int s = noalloc_scratch_setup(device);
+    if (s) return s;
     g_device = device;
     return NC_OK;
 }

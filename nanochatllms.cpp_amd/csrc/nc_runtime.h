@@ -14,6 +14,10 @@ int hip_fail(hipError_t e, const char* what);
 hipStream_t stream_of(void* s);
 bool initialized();
 
+// Takes the device address of nc_matmul_2d_noalloc's staging array on
+// device `dev` (the current device); called by nc_init.
+int noalloc_scratch_setup(int dev);
+
 // Checks a kernel launch; returns NC_OK or the recorded failure.
 inline int launch_status(const char* what)
 {
