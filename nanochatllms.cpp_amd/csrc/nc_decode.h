@@ -62,7 +62,19 @@ struct DmvArgs {
     const float* rope_table = nullptr;  // [max_ctx][rope_half] (cos, sin) pairs
     float* rope_cur = nullptr;
     int rope_half = 0;
+    // Nonzero: wq / wd are an lm head in the head layout (head_layout_launch);
+    // only with PRO_RES_RMS and EPI_RAW / EPI_ARGMAX.
+    int head = 0;
 };
+
+// The lm-head copy of a Q4 / Q8 weight [N, K] read by the head kernel: rows
+// in groups of 16, per group and 16-byte chunk each (row, lane)'s codes in
+// (row, lane) order (one contiguous 1 KB load per wavefront), deltas per
+// group and 8 blocks in row order.  Supported for the model widths K = 2048
+// and 2304 and N >= 64.
+bool head_layout_supported(int wdtype, int N, int K);
+int head_layout_bytes(int wdtype, int N, int K, size_t* code_bytes, size_t* delta_bytes);
+int head_layout_launch(const nc_tensor* w, void* codes, void* deltas, hipStream_t st);
 
 constexpr int kDmvArgmaxWords = 320 + 4096;
 

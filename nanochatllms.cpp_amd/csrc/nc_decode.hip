@@ -104,8 +104,10 @@ __device__ __forceinline__ void load_f32_chunk(const float* p, int ch, float (&v
 // load_w() requests the workgroup's first weights, and the row is built
 // while the weights are in flight (LDS barriers do not wait for global
 // loads).  sq: K floats of LDS for the squares and the Act row.  Ends with
-// an LDS barrier.
-template <int PRO, int NCH, class LoadW>
+// an LDS barrier.  ROWS_FIRST (norm prologues): the weights are requested
+// only once the rows have arrived -- a launch that requests tens of MB
+// would otherwise queue its rows behind its own weights.
+template <int PRO, int NCH, bool ROWS_FIRST = false, class LoadW>
 __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, LoadW&& load_w)
 {
     const int tid = threadIdx.x;
@@ -153,6 +155,7 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
         __builtin_amdgcn_sched_barrier(0);
         int posv = 0;
         if (fixed && A.dpos) posv = load_pos(A.dpos);
+        if (ROWS_FIRST) wait_loads_done();
         __builtin_amdgcn_sched_barrier(0);
         load_w();
         __builtin_amdgcn_sched_barrier(0);
@@ -476,169 +479,201 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     }
 }
 
-// Tall Q4 launches (a lm head of ~100k rows): each thread runs one (row,
-// lane) chain of the reference's fold itself, acc_k += t_k(i) for blocks i
-// in order, from its lane's weight dword and the staged activation block,
-// so the fold needs no LDS terms and no workgroup barriers.  A wavefront
-// holds 16 rows x 4 lanes, a workgroup 64 rows (a group); workgroups walk
-// groups g, g + grid, ...  Weights stream in chunks of 8 blocks, kRwDepth
-// chunks ahead across group boundaries: the four threads of a row load the
-// chunk's 128 contiguous bytes (streaming loads, every line used whole),
-// pass them through a wavefront-private LDS slice so each takes its lane's
-// dword of every block, and share the chunk's deltas by quad broadcast.  The
-// four lanes of a row then combine as (a0 + a1) + (a2 + a3) (the two
-// _mm_hadd_ps of gten/ops.cpp:358-360).
-constexpr int kRwRows = 64;   // rows per group: 4 wavefronts x 16 rows
-constexpr int kRwChunk = 8;   // blocks per chunk (nb % 8 == 0)
-constexpr int kRwDepth = 4;   // chunks in flight per thread
+// LM heads (32000 - 122753 rows of 2048 / 2304 values) read a second copy of
+// the weight in the head layout (k_head_layout): rows in groups of 16, and
+// per group and chunk of E blocks (Q4: 4, Q8: 2) the 16 rows x 4 lanes'
+// 16 bytes in (row, lane) order -- lane k's code dwords of the chunk's
+// blocks.  A wavefront is one row group, thread (row r, lane k) one chain
+// of the reference's fold (acc_k += t_k(i) for blocks i in order), and one
+// 16-byte load per thread is one contiguous 1 KB per wavefront that hands
+// every thread its own next E blocks: no weights or terms through LDS, and
+// the staged activation block is a broadcast read.  Deltas: per group and
+// 8-block chunk the 16 rows' eight deltas (16 bytes).  Wavefronts walk
+// groups w, w + waves, ...; each keeps DEPTH chunks in flight across group
+// boundaries, the first DEPTH requested once the norm prologue's rows have
+// arrived.  Lanes 4r .. 4r + 3 then combine as (a0 + a1) + (a2 + a3) (the
+// two _mm_hadd_ps of gten/ops.cpp:358-360).  The kernel is instruction-
+// bound as much as memory-bound (per block and lane: three LDS reads, two
+// v_dot4 and the fold's fp32 operations), so every index is a constant.
+constexpr int kHdGroup = 16;  // rows per group (a wavefront)
 
-template <int WT, int PRO, int EPI, int NCH>
-__global__ __launch_bounds__(kDmvThreads) void k_dmv_rows(DmvArgs A)
+// Blocks per 16-byte head-layout load.
+template <int WT>
+__host__ __device__ constexpr int head_chunk_blocks()
 {
-    constexpr int WW = WT == Q4 ? 1 : 2;        // code dwords of one lane and block
-    constexpr int CV = WT == Q4 ? 2 : 4;        // 16-byte code loads per lane and chunk
-    constexpr int RS = WT == Q4 ? 36 : 68;      // LDS dwords per row of a chunk (32 / 64 used)
+    return WT == Q4 ? 4 : 2;
+}
+
+// Chunks a thread keeps in flight: a divisor of the chunks per row (so a
+// chunk's register slot is the same in every group) of 16-18.
+template <int WT, int NCK>
+__host__ __device__ constexpr int head_depth()
+{
+    return WT == Q4 ? NCK : NCK / 2;
+}
+
+// NCK: 16-byte chunks per row (K / 32 / E).  All chunk and slot indices are
+// compile-time after unrolling; a wavefront's group base is wave-uniform, so
+// a load's address is one scalar base plus a constant offset.
+template <int WT, int EPI, int NCH, int NCK>
+__global__ __launch_bounds__(kDmvThreads) void k_dmv_head(DmvArgs A)
+{
+    constexpr int E = head_chunk_blocks<WT>();
+    constexpr int NB = NCK * E;                // blocks per row
+    constexpr int DEPTH = head_depth<WT, NCK>();
+    constexpr int DW = E / 2;                  // delta dwords per chunk
+    static_assert(NCK % DEPTH == 0 && NB % 8 == 0, "head layout shape");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
     __shared__ unsigned long long s_key[4];
     __shared__ int s_tok;
-    const int nb = A.nb, K = nb * 32;
-    uint32_t* xs = lds;                                         // staged row: nb * kStage dwords
-    float* sq = reinterpret_cast<float*>(xs + nb * kStage);    // prologue scratch: K floats
-    uint32_t* wl = reinterpret_cast<uint32_t*>(sq + K);        // per wavefront: 16 rows x RS dwords
-    float* res = reinterpret_cast<float*>(wl + 4 * 16 * RS);   // row results: 64 per owned group
-    const int tid = threadIdx.x;
-    const int k = tid & 3;                                     // the thread's lane
-    const int rr = (tid & 63) >> 2;                            // its row within the wavefront
-    const int wrow = (tid >> 6) * 16 + rr;                     // its row within a group
-    uint32_t* wrow_lds = wl + (tid >> 6) * 16 * RS + rr * RS;  // its row's chunk in LDS
-    const int G = gridDim.x;
-    const int nch = nb / kRwChunk;                             // >= kRwDepth (launcher)
-    const int mine = (A.ngroups - (int)blockIdx.x + G - 1) / G;  // groups this workgroup owns
-    const int total = mine * nch;                              // its chunks, >= kRwDepth
+    uint32_t* xs = lds;                                      // staged row: NB * kStage dwords
+    float* sq = reinterpret_cast<float*>(xs + NB * kStage);  // prologue scratch: K floats
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int rr = lane >> 2, k = lane & 3;                  // row in the group, lane
+    // this wavefront, the wavefronts of the grid and its groups (>= 1: the
+    // grid has at most one wavefront per group), all wave-uniform
+    const int gw = (int)blockIdx.x * (kDmvThreads / kWave) + __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int GW = (int)gridDim.x * (kDmvThreads / kWave);
+    const int ngr = (A.N + kHdGroup - 1) / kHdGroup;
+    const int mine = (ngr - gw + GW - 1) / GW;
 
-    // a chunk of a row is 8 blocks: thread (row, k) loads blocks 2k and 2k+1
-    // (contiguous, so a row's chunk is one coalesced span) and the two
-    // deltas of those blocks
-    uint4 wc[kRwDepth][CV];
-    uint32_t wd[kRwDepth];
-    // chunk j of this workgroup's stream: rows past N read row 0 (their
-    // results are not stored).  Every call issues the same loads, and no
-    // other global access sits between the issues and the waits, so the
-    // waits for a chunk are exact counts.
-    auto issue = [&](int j, uint4(&q)[CV], uint32_t& d) {
-        const int gi = j / nch;
-        const int c = j - gi * nch;
-        const int row = ((int)blockIdx.x + gi * G) * kRwRows + wrow;
-        const size_t b0 = (size_t)(row < A.N ? row : 0) * nb + (size_t)c * kRwChunk + 2 * k;
-        const uint4* src = reinterpret_cast<const uint4*>(A.wq + b0 * (WT == Q4 ? 4 : 8));
-#pragma unroll
-        for (int v = 0; v < CV; v++) q[v] = load_stream(src + v);
-        // the deltas (a ninth of the bytes) keep the default policy: the
-        // chunks after this one read the rest of their line
-        d = *reinterpret_cast<const uint32_t*>(A.wd + b0);
+    uint4 wq[DEPTH];
+    uint32_t wd[DEPTH][DW];  // the chunk's E deltas
+    // Group g's codes and deltas as buffer resources (scalar registers):
+    // chunk c's codes at byte 1024 c (this thread's 16 at + 16 lane), its E
+    // deltas at half 128 (cE / 8) + 8 rr + cE % 8 ([8-block chunk][row][8]).
+    // Every load is then one VGPR offset shared by all chunks plus a
+    // constant.  A resource with no records (`live` false) turns its loads
+    // into zeros that read no memory: the prefetch past a wavefront's last
+    // group is issued unconditionally, so the loads per iteration are fixed
+    // and every wait is exact.
+    auto code_rsrc = [&](int g, bool live) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(A.wq) + (size_t)g * NCK * 256, (short)0,
+                                                 live ? NCK * 1024 : 0, kBufferFlags);
     };
-    const int pos = dmv_prologue<PRO, NCH>(A, xs, sq, ssh, [&] {
+    auto delta_rsrc = [&](int g, bool live) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A.wd) + (size_t)g * NB * kHdGroup, (short)0,
+                                                 live ? NB * kHdGroup * 2 : 0, kBufferFlags);
+    };
+    const int qoff = lane * 16, doff = rr * 16;
+    auto issue = [&](__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rd, int c, int b) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, c * 1024, kCacheStream);
+        wq[b] = make_uint4(q[0], q[1], q[2], q[3]);
+        const int dc = ((c * E / 8) * 128 + (c * E) % 8) * 2;
+        if (E == 4) {
+            const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rd, doff, dc, 0);
+            wd[b][0] = t2[0];
+            wd[b][DW - 1] = t2[1];
+        } else {
+            wd[b][0] = __builtin_amdgcn_raw_buffer_load_b32(rd, doff, dc, 0);
+        }
+    };
+    const int pos = dmv_prologue<PRO_RES_RMS, NCH, true>(A, xs, sq, ssh, [&] {
+        const auto rq = code_rsrc(gw, true);
+        const auto rd = delta_rsrc(gw, true);
 #pragma unroll
-        for (int b = 0; b < kRwDepth; b++) issue(b, wc[b], wd[b]);
+        for (int c = 0; c < DEPTH; c++) issue(rq, rd, c, c);
     });
 
     float acc = 0.0f;
-    // chunk j from buffer b: this lane's chain over the chunk's 8 blocks;
-    // at a group's last chunk lane 4r combines row r into res
-    auto consume = [&](int j, const uint4(&q)[CV], uint32_t d) {
-        const int gi = j / nch;
-        const int c = j - gi * nch;
-        // the row's chunk through this wavefront's LDS slice: lane k then
-        // reads its own dword(s) of each block (wavefront-private, and LDS
-        // operations of a wavefront complete in order)
+    unsigned long long best = 0;
+    // xo: zero, opaque to the compiler per group, so the staged row's LDS
+    // reads stay in the loop instead of being hoisted out of it into
+    // registers (all NB blocks' worth, which would halve occupancy)
+    int xo = 0;
+    auto consume = [&](int c, int b) {
+        const uint4 q = wq[b];
+        const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int v = 0; v < CV; v++) reinterpret_cast<uint4*>(wrow_lds + k * 4 * CV)[v] = q[v];
-        uint32_t qv[kRwChunk][WW];
-#pragma unroll
-        for (int e = 0; e < kRwChunk; e++) {
-            if (WW == 1) {
-                qv[e][0] = wrow_lds[e * 4 + k];
-            } else {
-                const uint2 t2 = *reinterpret_cast<const uint2*>(wrow_lds + e * 8 + 2 * k);
-                qv[e][0] = t2.x;
-                qv[e][WW - 1] = t2.y;
-            }
-        }
-        // the chunk's eight deltas: lane m holds those of blocks 2m, 2m + 1
-        const uint32_t dws[4] = {(uint32_t)dpp_i<0x00>((int)d), (uint32_t)dpp_i<0x55>((int)d),
-                                 (uint32_t)dpp_i<0xAA>((int)d), (uint32_t)dpp_i<0xFF>((int)d)};
-#pragma unroll
-        for (int e = 0; e < kRwChunk; e++) {
-            const uint32_t* st = xs + (c * kRwChunk + e) * kStage;
-            // this lane's staged codes, offset and the block's delta
-            const uint32_t xa = st[2 * k];
-            const uint32_t xb = st[2 * k + 1];
+        for (int e = 0; e < E; e++) {
+            // lane k of the staged block: xa, xb at dwords 2k, 2k + 1, the Q4
+            // offset at 8 + k, the delta at 12
+            const uint32_t* st = xs + xo + (c * E + e) * kStage;
+            const uint2 xv = *reinterpret_cast<const uint2*>(st + 2 * k);
             const int cx = (int)st[8 + k];
             const float dx = __uint_as_float(st[12]);
-            const float dd = dx * h2f((uint16_t)(dws[e >> 1] >> (16 * (e & 1))));
+            const float dd = dx * h2f((uint16_t)(wd[b][e >> 1] >> (16 * (e & 1))));
             int L;
             if (WT == Q4) {
-                const uint32_t P = qv[e][0];
-                L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)xa, cx, false);
-                L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)xb, L, false);
+                const uint32_t P = qd[e];
+                L = __builtin_amdgcn_sdot4((int)((P >> 4) & 0x0F0F0F0Fu), (int)xv.x, cx, false);
+                L = __builtin_amdgcn_sdot4((int)(P & 0x0F0F0F0Fu), (int)xv.y, L, false);
             } else {
-                L = __builtin_amdgcn_sdot4((int)qv[e][0], (int)xa, 0, false);
-                L = __builtin_amdgcn_sdot4((int)qv[e][WW - 1], (int)xb, L, false);
+                L = __builtin_amdgcn_sdot4((int)qd[2 * e], (int)xv.x, 0, false);
+                L = __builtin_amdgcn_sdot4((int)qd[2 * e + 1], (int)xv.y, L, false);
             }
             acc = acc + (float)L * dd;
         }
-        if (c == nch - 1) {
-            const float a1 = dpp_f<kDppQuadXor1>(acc);
-            const float a2 = dpp_f<kDppQuadXor2>(acc);
-            const float a3 = dpp_f<0x1B>(acc);
-            if (k == 0) res[gi * kRwRows + wrow] = (acc + a1) + (a2 + a3);
-            acc = 0.0f;
-        }
     };
-    int j0 = 0;
-    // steady state: each consumed chunk's buffer takes the chunk kRwDepth on
-    for (; j0 + 2 * kRwDepth <= total; j0 += kRwDepth) {
+    for (int gi = 0; gi < mine; gi++) {
+        const int g = gw + gi * GW;
+        const bool more = gi + 1 < mine;  // wave-uniform
+        asm volatile("" : "+v"(xo));
+        const auto rq = code_rsrc(g, true);
+        const auto rd = delta_rsrc(g, true);
+        const auto rqn = code_rsrc(g + GW, more);
+        const auto rdn = delta_rsrc(g + GW, more);
+        // each consumed chunk's slot takes the chunk DEPTH on in the stream
 #pragma unroll
-        for (int b = 0; b < kRwDepth; b++) {
-            consume(j0 + b, wc[b], wd[b]);
-            issue(j0 + b + kRwDepth, wc[b], wd[b]);
+        for (int c = 0; c < NCK; c++) {
+            consume(c, c % DEPTH);
+            if (c + DEPTH < NCK)
+                issue(rq, rd, c + DEPTH, c % DEPTH);
+            else
+                issue(rqn, rdn, c + DEPTH - NCK, c % DEPTH);
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
-    // the last kRwDepth .. 2 kRwDepth - 1 chunks
-    const int rest = total - j0 - kRwDepth;  // 0 .. kRwDepth - 1 still to issue
-#pragma unroll
-    for (int b = 0; b < kRwDepth; b++) {
-        consume(j0 + b, wc[b], wd[b]);
-        if (b < rest) issue(j0 + b + kRwDepth, wc[b], wd[b]);
-    }
-#pragma unroll
-    for (int b = 0; b < kRwDepth; b++)
-        if (b < rest) consume(j0 + kRwDepth + b, wc[b], wd[b]);
-
-    // the workgroup's row results out, and the greedy token
-    lds_barrier();
-    unsigned long long best = 0;
-    for (int t = tid; t < mine * kRwRows; t += kDmvThreads) {
-        const int row = ((int)blockIdx.x + (t / kRwRows) * G) * kRwRows + (t % kRwRows);
-        if (row < A.N) {
-            const float v = res[t];
-            A.raw[row] = v;
+        // the row is done: lane 4r reads the other three lanes' sums
+        const float a1 = dpp_f<kDppQuadXor1>(acc);
+        const float a2 = dpp_f<kDppQuadXor2>(acc);
+        const float a3 = dpp_f<0x1B>(acc);
+        const int row = g * kHdGroup + rr;
+        if (k == 0 && row < A.N) {
+            const float res = (acc + a1) + (a2 + a3);
+            A.raw[row] = res;
             if (EPI == EPI_ARGMAX) {
-                const unsigned long long key = greedy_key(v, row);
+                const unsigned long long key = greedy_key(res, row);
                 best = key > best ? key : best;
             }
         }
+        acc = 0.0f;
     }
+
     if (EPI == EPI_ARGMAX) {
-        // argmax_epilogue reduces keys held on lanes 4r: fold each quad first
-        // (keys of one quad's lanes are distinct rows here)
-        unsigned long long o = __shfl_xor(best, 1);
-        best = o > best ? o : best;
-        o = __shfl_xor(best, 2);
-        best = o > best ? o : best;
+        // row results sit on lanes 4r
         argmax_epilogue<WT, NCH>(A, best, pos, kDmvThreads / kWave, s_key, &s_tok);
     }
+}
+
+// Copies a Q4 / Q8 weight [N, nb blocks] (codes and deltas) into the head
+// layout of k_dmv_head; rows past N (up to the group of 16) are zeros.
+// Thread = one (row, block).
+template <int WT>
+__global__ void k_head_layout(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ wd, int N, int nb,
+                              uint32_t* __restrict__ hq, uint16_t* __restrict__ hd)
+{
+    constexpr int WD = WT == Q4 ? 4 : 8, E = head_chunk_blocks<WT>();
+    const int npad = (N + kHdGroup - 1) / kHdGroup * kHdGroup;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)npad * nb) return;
+    const int r = (int)(t / nb), i = (int)(t - (int64_t)r * nb);
+    const size_t g = (size_t)(r / kHdGroup);
+    const int rr = r % kHdGroup;
+    const bool in = r < N;
+    const int nck = nb / E;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        // lane k's dwords of block i: Q4 dword k, Q8 dwords 2k and 2k + 1
+        const size_t dst = (((g * nck + i / E) * kHdGroup + rr) * 4 + k) * 4;
+        if (WT == Q4) {
+            hq[dst + i % E] = in ? wq[((size_t)r * nb + i) * WD + k] : 0u;
+        } else {
+            hq[dst + 2 * (i % E)] = in ? wq[((size_t)r * nb + i) * WD + 2 * k] : 0u;
+            hq[dst + 2 * (i % E) + 1] = in ? wq[((size_t)r * nb + i) * WD + 2 * k + 1] : 0u;
+        }
+    }
+    hd[((g * (nb / 8) + i / 8) * kHdGroup + rr) * 8 + i % 8] = in ? wd[(size_t)r * nb + i] : (uint16_t)0;
 }
 
 // Gate|up matvec with the SwiGLU epilogue: a workgroup owns output block b
@@ -818,46 +853,30 @@ int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
     return launch_status("k_dmv_glu");
 }
 
-// Q4 launches with this many rows and a norm prologue (MiniCPM's tied lm
-// head, 122753 rows) run k_dmv_rows: 45% of HBM peak there against 35% for
-// k_dmv.  At 32000 rows the two kernels take the same time, and for Q8 (twice
-// the code bytes per chunk through LDS) k_dmv is faster.
-constexpr int kRwMinRows = 65536;
-
-template <int WT, int PRO, int EPI, int NCH>
-int rows_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+// LM heads in the head layout, rows of NCK chunks.
+template <int WT, int EPI, int NCH, int NCK>
+int head_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv_rows<WT, PRO, EPI, NCH>;
-    // staged row, prologue scratch, then the row results of the groups a
-    // workgroup owns (occupancy taken with room for 8 groups)
-    const size_t lds0 = (size_t)A.nb * kStage * 4 + (size_t)A.nb * 32 * 4 + 4 * 16 * (WT == Q4 ? 36 : 68) * 4;
-    static int max_grid = 0;
+    auto kern = k_dmv_head<WT, EPI, NCH, NCK>;
+    const size_t lds = (size_t)A.nb * kStage * 4 + (size_t)A.nb * 32 * 4;
+    static int max_grid = 0;  // workgroups resident at once
     if (!max_grid) {
         int per_cu = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kDmvThreads,
-                                                                    lds0 + 8 * kRwRows * 4);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kDmvThreads, lds);
         if (e != hipSuccess) return hip_fail(e, "decode matvec: occupancy");
         max_grid = std::min(kDmvMaxGrid, std::max(1, per_cu) * device_cus());
     }
-    A.rows = kRwRows;
-    A.ngroups = (A.N + kRwRows - 1) / kRwRows;
-    const int grid_n = std::min(A.ngroups, max_grid);  // every workgroup owns at least one group
-    const int per_wg = (A.ngroups + grid_n - 1) / grid_n;
-    const size_t lds = lds0 + (size_t)per_wg * kRwRows * 4;
-    if (lds > 64 * 1024) return fail(NC_ERR_ARG, "decode matvec: %d rows in too few workgroups", A.N);
-    const dim3 grid(grid_n);
+    if (A.nb != NCK * head_chunk_blocks<WT>() || A.N < kHdGroup * (kDmvThreads / kWave))
+        return fail(NC_ERR_ARG, "decode matvec: lm head of %d x %d blocks", A.N, A.nb);
+    A.rows = kHdGroup;
+    A.ngroups = (A.N + kHdGroup - 1) / kHdGroup;
+    // every wavefront owns at least one group of 16 rows
+    const dim3 grid(std::min(A.ngroups / (kDmvThreads / kWave), max_grid));
     if (ev0)
         hipExtLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, ev0, ev1, 0, A);
     else
         hipLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, A);
-    return launch_status("k_dmv_rows");
-}
-
-template <int WT, int PRO, int EPI>
-int rows_nch(const DmvArgs& A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
-{
-    if (A.nb * 32 > kDmvThreads * 8) return rows_go<WT, PRO, EPI, 2>(A, st, ev0, ev1);
-    return rows_go<WT, PRO, EPI, 1>(A, st, ev0, ev1);
+    return launch_status("k_dmv_head");
 }
 
 // Launch with the items per thread the group needs (1, 2, 4, 8 or 12).
@@ -896,15 +915,23 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
         if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72>(A, lds, st, ev0, ev1);
         return glu_go<WT, PRO_RES_RMS, 2, 72>(A, lds, st, ev0, ev1);
     }
-    if constexpr (WT == Q4) {
-        if (norm && epi != EPI_SWIGLU && A.N >= kRwMinRows && A.nb % kRwChunk == 0 && A.nb >= kRwChunk * kRwDepth) {
-            // tall launches (lm heads): one fold chain per thread
-            if (epi == EPI_ARGMAX)
-                return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_ARGMAX>(A, st, ev0, ev1)
-                                      : rows_nch<WT, PRO_RES_RMS, EPI_ARGMAX>(A, st, ev0, ev1);
-            return pro == PRO_RMS ? rows_nch<WT, PRO_RMS, EPI_RAW>(A, st, ev0, ev1)
-                                  : rows_nch<WT, PRO_RES_RMS, EPI_RAW>(A, st, ev0, ev1);
+    if (A.head) {
+        // an lm head in the head layout: one fold chain per thread, the
+        // weights streamed straight into registers
+        if (pro != PRO_RES_RMS || epi == EPI_SWIGLU)
+            return fail(NC_ERR_ARG, "decode matvec: head layout with prologue %d epilogue %d", pro, epi);
+        // rows of 2048 (one 8-value chunk per thread in the prologue) or
+        // 2304 values (two)
+        constexpr int E = head_chunk_blocks<WT>();
+        if (A.nb == 64) {
+            if (epi == EPI_ARGMAX) return head_go<WT, EPI_ARGMAX, 1, 64 / E>(A, st, ev0, ev1);
+            return head_go<WT, EPI_RAW, 1, 64 / E>(A, st, ev0, ev1);
         }
+        if (A.nb == 72) {
+            if (epi == EPI_ARGMAX) return head_go<WT, EPI_ARGMAX, 2, 72 / E>(A, st, ev0, ev1);
+            return head_go<WT, EPI_RAW, 2, 72 / E>(A, st, ev0, ev1);
+        }
+        return fail(NC_ERR_ARG, "decode matvec: head layout rows of %d blocks", A.nb);
     }
     if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
     if (epi == EPI_ARGMAX) {
@@ -933,6 +960,36 @@ bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi)
     if (epi == EPI_ARGMAX && !norm) return false;
     if (epi == EPI_SWIGLU && (N % 64 || (K != 2048 && K != 2304) || !norm)) return false;
     return true;
+}
+
+bool head_layout_supported(int wdtype, int N, int K)
+{
+    if (wdtype != NC_Q4 && wdtype != NC_Q8) return false;
+    return (K == 2048 || K == 2304) && N >= kHdGroup * (kDmvThreads / kWave);
+}
+
+int head_layout_bytes(int wdtype, int N, int K, size_t* code_bytes, size_t* delta_bytes)
+{
+    const size_t npad = (size_t)(N + kHdGroup - 1) / kHdGroup * kHdGroup, nb = (size_t)K / 32;
+    *code_bytes = npad * nb * (wdtype == NC_Q4 ? 16 : 32);
+    *delta_bytes = npad * nb * 2;
+    return NC_OK;
+}
+
+int head_layout_launch(const nc_tensor* w, void* codes, void* deltas, hipStream_t st)
+{
+    if (!head_layout_supported(w->dtype, w->rows, w->cols))
+        return fail(NC_ERR_ARG, "head layout: [%d x %d] dtype %d", w->rows, w->cols, w->dtype);
+    const int nb = w->cols / 32;
+    const int64_t n = (int64_t)(w->rows + kHdGroup - 1) / kHdGroup * kHdGroup * nb;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (w->dtype == NC_Q4)
+        hipLaunchKernelGGL(k_head_layout<Q4>, grid, dim3(256), 0, st, (const uint32_t*)w->data,
+                           (const uint16_t*)w->deltas, w->rows, nb, (uint32_t*)codes, (uint16_t*)deltas);
+    else
+        hipLaunchKernelGGL(k_head_layout<Q8>, grid, dim3(256), 0, st, (const uint32_t*)w->data,
+                           (const uint16_t*)w->deltas, w->rows, nb, (uint32_t*)codes, (uint16_t*)deltas);
+    return launch_status("k_head_layout");
 }
 
 int decode_matvec(const DmvArgs& A, int wdtype, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)

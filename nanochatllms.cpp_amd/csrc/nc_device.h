@@ -33,6 +33,12 @@ __device__ __forceinline__ uint2 load_stream(const uint2* p)
     return make_uint2(v.x, v.y);
 }
 
+// Raw buffer loads (__builtin_amdgcn_raw_buffer_load_*): the resource's
+// third dword for gfx9 untyped buffers, and the cache-policy operand of a
+// streaming (nontemporal) load, as load_stream issues it.
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kCacheStream = 2;
+
 // fp16 -> fp32, exact (gten/gten_types.h:129-133).
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
@@ -119,6 +125,10 @@ __device__ __forceinline__ unsigned long long greedy_key(float v, int idx)
 // ordering they need (no L2 write-back, which a release fence adds for plain
 // stores).
 __device__ __forceinline__ void wait_stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Waits until this thread's global loads so far have returned, so the loads
+// issued next do not queue ahead of their data.
+__device__ __forceinline__ void wait_loads_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
 // accesses, not for its global loads (which may stay in flight across it).

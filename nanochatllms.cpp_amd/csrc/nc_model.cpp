@@ -113,6 +113,10 @@ public:
     // before it returns (upload()), so no queued copy outlives its source.
     uint8_t* hstage = nullptr;
     size_t hstage_bytes = 0;
+    // The lm head (lm, or emb when tied) in the head layout, read by the
+    // fused step's lm-head kernel; rebuilt from the weight whenever it
+    // changes (refresh_head).  data == nullptr: no copy.
+    nc_tensor hl{};
 
     // Matvec launch timing: a start/end event pair recorded on the model's
     // stream around every matvec launch while profiling is on.
@@ -344,6 +348,16 @@ public:
             return s;
         fused = fused_supported();
         if (const char* f = std::getenv("NC_DECODE_FUSED")) fused = fused && std::atoi(f) != 0;
+        // the fused step's lm head reads a copy of its weight in the head layout
+        if (fused && head_layout_supported(c->wdtype, c->n_vocab, d)) {
+            size_t cb, db;
+            if ((s = head_layout_bytes(c->wdtype, c->n_vocab, d, &cb, &db)) || (s = alloc(&hl.data, cb)) ||
+                (s = alloc(&hl.deltas, db)))
+                return s;
+            hl.dtype = c->wdtype;
+            hl.rows = c->n_vocab;
+            hl.cols = d;
+        }
         // RoPE table from the host libm, the reference's expression
         d_half = static_cast<int>((float)c->d_head * c->rope_pct) / 2;
         std::vector<float> tab((size_t)mc * std::max(d_half, 1) * 2);
@@ -458,11 +472,29 @@ public:
         for (int l = 0; l < cfg.n_layers; l++)
             for (int slot = 0; slot <= NC_W_K_NORM; slot++)
                 if ((s = one(l, slot))) return s;
+        if ((s = refresh_head())) return s;
         hipError_t e = hipStreamSynchronize(st);
         return e == hipSuccess ? NC_OK : hip_fail(e, "init_synthetic");
     }
 
+    // The head-layout copy of the lm head, rebuilt from the weight.
+    int refresh_head()
+    {
+        if (!hl.data) return NC_OK;
+        return head_layout_launch(tied() ? &emb : &lm, hl.data, hl.deltas, st);
+    }
+
     int set_weight(int layer, int slot, const void* ref, size_t n_bytes)
+    {
+        const bool head = layer < 0 && (slot == NC_TID_LM || (slot == NC_TID_EMB && tied()));
+        int s = set_weight_only(layer, slot, ref, n_bytes);
+        if (s || !head) return s;
+        if ((s = refresh_head())) return s;
+        hipError_t e = hipStreamSynchronize(st);
+        return e == hipSuccess ? NC_OK : hip_fail(e, "set_weight: head layout");
+    }
+
+    int set_weight_only(int layer, int slot, const void* ref, size_t n_bytes)
     {
         Loc o;
         int s = locate(layer, slot, &o);
@@ -849,14 +881,18 @@ public:
         a.norm_w = norm_w;
         a.post_scale = minicpm ? 1.0f / 9 : 1.0f;  // minicpm.cpp:104-105
         a.raw = logits;
+        // the head-layout copy of the lm head when there is one
+        const nc_tensor* head = hl.data ? &hl : (tied() ? &emb : &lm);
+        a.head = hl.data ? 1 : 0;
         // a sampling step: logits only, the sampler picks the token
-        if (sample_head) return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_RAW, NC_PROF_LM_HEAD);
+        if (sample_head) return dmv(a, head, PRO_RES_RMS, EPI_RAW, NC_PROF_LM_HEAD);
         a.tokens = tokens;
         a.pos_out = dpos;
         a.amax = am_scratch;
-        // the next step's embedding and RoPE rows, from the greedy token
+        // the next step's embedding and RoPE rows, from the greedy token (the
+        // embedding rows in the embedding's own layout)
         if (dpos) next_input_fields(&a, dpos);
-        return dmv(a, tied() ? &emb : &lm, PRO_RES_RMS, EPI_ARGMAX, NC_PROF_LM_HEAD);
+        return dmv(a, head, PRO_RES_RMS, EPI_ARGMAX, NC_PROF_LM_HEAD);
     }
 
     // The fields of the next step's embedding and RoPE rows (the greedy
