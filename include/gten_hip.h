@@ -282,6 +282,32 @@ int nc_model_generate_topk(void* model, const int32_t* prompt, int n_prompt, int
  * calls (no host round trip between steps) and appends the tokens. */
 int nc_model_prefill(void* model, const int32_t* prompt, int n_prompt);
 int nc_model_decode(void* model, int n_steps, int32_t* out);
+/* The same split for topk_sample's loop (src/gten/sampler.cpp:78-135, with
+ * std::mt19937(seed)): nc_model_sample_begin runs the prompt and samples the
+ * first token; nc_model_sample_steps samples n_steps more and copies every
+ * token sampled since the prompt to out (when set). */
+int nc_model_sample_begin(void* model, const int32_t* prompt, int n_prompt, float temp, int top_k, uint32_t seed);
+int nc_model_sample_steps(void* model, int n_steps, int32_t* out);
+/* The configuration the model was created with. */
+int nc_model_get_config(void* model, nc_model_config* cfg);
+
+/* ---- the text path: greedy_sample / topk_sample (src/gten/sampler.cpp) ----
+ * Prompt text in, generated text out: the tokenizer's encode of the prompt
+ * (chat prefixes and suffixes included), the model's tokens up to
+ * n_predict - (prompt tokens) of them or the tokenizer's eos, and each
+ * token's decode(prev, token) passed to `sink` as it is produced (prev = 1
+ * for the first, as the reference's `(i == 0) ? 1 : tokens.back()`), then
+ * "\n" -- the text the reference writes to std::cerr.  n_predict <= 0 takes
+ * the model's max_ctx (the reference's min(inference ctx, train ctx) is the
+ * max_ctx its callers give the model).  *n_tokens = tokens produced (eos not
+ * counted).  Each call starts from position 0 like the reference's.
+ * topk_sample clamps top_k to 1000 and temp to 2 as the reference does and
+ * draws from std::mt19937(seed) in place of a random_device seed. */
+typedef void (*nc_text_sink)(const char* text, void* user);
+int nc_greedy_sample(void* model, void* tokenizer, const char* prompt, int n_predict, nc_text_sink sink, void* user,
+                     int* n_tokens);
+int nc_topk_sample(void* model, void* tokenizer, const char* prompt, int n_predict, float temp, int top_k,
+                   uint32_t seed, nc_text_sink sink, void* user, int* n_tokens);
 /* Timing of the model's matvec launches (the reference's Linear time,
  * print_perf in src/tinyllama/tinyllama.cpp:140-193, measured per launch):
  * between begin and end, HIP events on the model's stream bracket up to

@@ -101,6 +101,9 @@ def weight_bytes_ref(dtype, rows, cols):
 
 _lib = None
 
+# nc_text_sink: void (*)(const char* text, void* user)
+TEXT_SINK = C.CFUNCTYPE(None, C.c_char_p, C.c_void_p)
+
 
 def lib():
     """The loaded product library; raises if it has not been built."""
@@ -152,6 +155,11 @@ def lib():
         "nc_model_profile_end": (I, [VP, C.POINTER(I)] + [C.POINTER(C.c_double)] * 4),
         "nc_model_profile_launches": (I, [VP, I, VP, VP, VP, C.POINTER(I)]),
         "nc_copy_d2d": (I, [VP, VP, C.c_size_t, VP]),
+        "nc_model_sample_begin": (I, [VP, VP, I, F, I, C.c_uint32]),
+        "nc_model_sample_steps": (I, [VP, I, VP]),
+        "nc_model_get_config": (I, [VP, C.POINTER(ModelConfig)]),
+        "nc_greedy_sample": (I, [VP, VP, C.c_char_p, I, TEXT_SINK, VP, C.POINTER(I)]),
+        "nc_topk_sample": (I, [VP, VP, C.c_char_p, I, F, I, C.c_uint32, TEXT_SINK, VP, C.POINTER(I)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -382,3 +390,38 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+def _sample_text(call, on_text):
+    pieces = []
+
+    def sink(text, _user):
+        piece = text or b""
+        pieces.append(piece)
+        if on_text:
+            on_text(piece)
+
+    cb = TEXT_SINK(sink)
+    n = C.c_int()
+    check(call(cb, C.byref(n)), "sample")
+    return b"".join(pieces), n.value
+
+
+def greedy_sample(model, tokenizer, prompt, n_predict=0, on_text=None):
+    """greedy_sample (src/gten/sampler.cpp:11-60) end to end: prompt text
+    (str or bytes) in, the text the reference writes out (bytes, closing
+    newline included) and the number of tokens generated.  on_text(piece)
+    sees each decoded piece as it is produced.  n_predict <= 0: the model's
+    max_ctx."""
+    p = prompt.encode() if isinstance(prompt, str) else bytes(prompt)
+    return _sample_text(lambda cb, n: lib().nc_greedy_sample(model.h, tokenizer.h, p, n_predict, cb, None, n),
+                        on_text)
+
+
+def topk_sample(model, tokenizer, prompt, temp=0.9, top_k=50, seed=0, n_predict=0, on_text=None):
+    """topk_sample (src/gten/sampler.cpp:63-143) end to end, with
+    std::mt19937(seed) in place of the random_device seed."""
+    p = prompt.encode() if isinstance(prompt, str) else bytes(prompt)
+    return _sample_text(
+        lambda cb, n: lib().nc_topk_sample(model.h, tokenizer.h, p, n_predict, temp, top_k, seed, cb, None, n),
+        on_text)

@@ -950,6 +950,7 @@ public:
         NC_CHECK_ARG(toks && out && n > 0 && n <= cfg.max_ctx && sp >= 0 && sp < n,
                      "logits: %d tokens from %d with max_ctx %d", n, sp, cfg.max_ctx);
         NC_CHECK_ARG(sp == 0 || sp <= n_cur, "logits: start_pos %d beyond the %d cached rows", sp, n_cur);
+        topk_on = false;
         Drain drain{st};
         int s = upload(tokens, toks, (size_t)n * 4, "token upload");
         if (s || (s = forward(sp, n))) return s;
@@ -962,6 +963,7 @@ public:
     int prefill(const int32_t* prompt, int np)
     {
         NC_CHECK_ARG(prompt && np > 0 && np < cfg.max_ctx + 1, "prefill: %d prompt tokens, max_ctx %d", np, cfg.max_ctx);
+        topk_on = false;
         int s = upload(tokens, prompt, (size_t)np * 4, "token upload");
         if (s || (s = forward(0, np))) return s;
         if (s) return s;
@@ -1056,10 +1058,26 @@ public:
     // device.  top_k and temp are clamped as the reference clamps them.
     int generate_topk(const int32_t* prompt, int np, int n_gen, float temp, int top_k, uint32_t seed)
     {
-        const int k = 1000 < top_k ? 1000 : top_k;
-        const float t = 2.0f < temp ? 2.0f : temp;
         NC_CHECK_ARG(prompt && np > 0 && n_gen > 0 && np + n_gen - 1 <= cfg.max_ctx,
                      "generate_topk: %d prompt + %d tokens, max_ctx %d", np, n_gen, cfg.max_ctx);
+        int s = topk_begin(prompt, np, temp, top_k, seed);
+        return s ? s : topk_steps(n_gen - 1);
+    }
+
+    // The sampled loop in parts: the prompt and its sampled token, then
+    // more sampled steps (each reading the setting and generator state the
+    // first part left on the device).
+    bool topk_on = false, topk_graph = false;
+    float topk_t = 0.0f;
+    int topk_k = 0;
+
+    int topk_begin(const int32_t* prompt, int np, float temp, int top_k, uint32_t seed)
+    {
+        const int k = 1000 < top_k ? 1000 : top_k;
+        const float t = 2.0f < temp ? 2.0f : temp;
+        topk_on = false;
+        NC_CHECK_ARG(prompt && np > 0 && np <= cfg.max_ctx, "generate_topk: %d prompt tokens, max_ctx %d", np,
+                     cfg.max_ctx);
         NC_CHECK_ARG(k >= 1 && k <= cfg.n_vocab && t > 0.0f, "generate_topk: top_k %d, temperature %g", top_k,
                      (double)temp);
         int s;
@@ -1080,20 +1098,34 @@ public:
         const int first = np - 1;
         if (graph && (s = upload(step_pos, &first, 4, "generate_topk: position upload"))) return s;
         if ((s = sample_after(t, k, graph ? step_pos : nullptr, first))) return s;
+        topk_on = true;
+        topk_graph = graph;
+        topk_t = t;
+        topk_k = k;
+        return NC_OK;
+    }
+
+    int topk_steps(int n_steps)
+    {
+        NC_CHECK_ARG(topk_on, "sample_steps: no sampled prompt");
+        NC_CHECK_ARG(n_steps >= 0 && n_cur + n_steps <= cfg.max_ctx, "sample_steps: %d + %d steps exceed max_ctx %d",
+                     n_cur, n_steps, cfg.max_ctx);
+        int s;
         hipError_t e = hipSuccess;
-        if (graph) {
+        // the first part chose the graph (device position) or direct path
+        if (topk_graph) {
             if (!sample_graph && (s = capture_sample_graph())) return s;
-            for (int i = 1; i < n_gen; i++)
+            for (int i = 0; i < n_steps; i++)
                 if ((e = hipGraphLaunch(sample_graph, st)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
-            n_cur += n_gen - 1;
+            n_cur += n_steps;
             return NC_OK;
         }
-        for (int i = 1; i < n_gen; i++) {
+        for (int i = 0; i < n_steps; i++) {
             const int n = n_cur + 1;
             sample_head = true;
             s = forward(n - 1, n);
             sample_head = false;
-            if (s || (s = sample_after(t, k, nullptr, n - 1))) return s;
+            if (s || (s = sample_after(topk_t, topk_k, nullptr, n - 1))) return s;
             n_cur = n;
         }
         return NC_OK;
@@ -1232,6 +1264,29 @@ int nc_model_generate(void* model, const int32_t* prompt, int n_prompt, int n_ge
     if (!s) s = m->decode(n_gen - 1);
     if (!s) s = m->fetch_generated(out, n_gen, n_out);
     return s;
+}
+
+int nc_model_sample_begin(void* model, const int32_t* prompt, int n_prompt, float temp, int top_k, uint32_t seed)
+{
+    NC_CHECK_ARG(model, "model: null");
+    return static_cast<Decoder*>(model)->topk_begin(prompt, n_prompt, temp, top_k, seed);
+}
+
+int nc_model_sample_steps(void* model, int n_steps, int32_t* out)
+{
+    NC_CHECK_ARG(model, "model: null");
+    auto* m = static_cast<Decoder*>(model);
+    int s = m->topk_steps(n_steps);
+    if (s || !out) return s;
+    int n;
+    return m->fetch_generated(out, m->n_cur + 1 - m->n_prompt, &n);
+}
+
+int nc_model_get_config(void* model, nc_model_config* cfg)
+{
+    NC_CHECK_ARG(model && cfg, "model_get_config: null");
+    *cfg = static_cast<Decoder*>(model)->cfg;
+    return NC_OK;
 }
 
 int nc_model_generate_topk(void* model, const int32_t* prompt, int n_prompt, int n_gen, float temp, int top_k,

@@ -309,9 +309,11 @@ int nc_tokenizer_load_for_model(const char* model, const char* path, void** toke
 {
     NC_CHECK_ARG(model && path && tokenizer, "tokenizer_load_for_model: bad arguments");
     const std::string m = model;
+    // TinyLlama and OpenELM: vocab n_vocab - 3 = 32000 and eos
+    // tinyllama_cfg.eos = 32002 (tinyllama/tinyllama.h:13,20)
     if (m == "tinyllama") {
         const int32_t pre[] = {1, 32001}, suf[] = {32002, 29871, 13, 32001, 20255, 13};
-        return nc_tokenizer_load_bpe(path, 32000, 2, "user\n", "", pre, 2, suf, 6, tokenizer);
+        return nc_tokenizer_load_bpe(path, 32000, 32002, "user\n", "", pre, 2, suf, 6, tokenizer);
     }
     if (m == "zephyr") {
         const int32_t pre[] = {27, 91, 882, 91, 29, 397}, suf[] = {100257, 198, 27, 91, 78191, 91, 397};
@@ -320,7 +322,7 @@ int nc_tokenizer_load_for_model(const char* model, const char* path, void** toke
     if (m == "minicpm") return nc_tokenizer_load_bpe(path, 122753, 2, "<用户>", "<AI>", nullptr, 0, nullptr, 0, tokenizer);
     if (m == "openelm_sm" || m == "openelm_md" || m == "openelm_lg") {
         const int32_t pre[] = {1};
-        return nc_tokenizer_load_bpe(path, 32000, 2, "", "", pre, 1, nullptr, 0, tokenizer);
+        return nc_tokenizer_load_bpe(path, 32000, 32002, "", "", pre, 1, nullptr, 0, tokenizer);
     }
     return nc::fail(NC_ERR_ARG, "tokenizer_load_for_model: unknown model `%s`", model);
 }

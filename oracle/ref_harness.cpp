@@ -21,12 +21,15 @@
 #include <cstdint>
 #include <cstring>
 #include <fstream>
+#include <iostream>
 #include <memory>
 #include <random>
+#include <sstream>
 #include <utility>
 #include <vector>
 
 #include "gten/gten.h"
+#include "gten/sampler.h"
 #include "gten/tokenizer.h"
 #include "minicpm/minicpm.h"
 #include "tinyllama/tinyllama.h"
@@ -582,5 +585,48 @@ const char* ref_tok_decode(void* p, int prev_token, int token)
 }
 
 void ref_tok_free(void* p) { delete static_cast<RefTokenizer*>(p); }
+
+}  // extern "C"
+
+namespace {
+
+// A harness model behind the reference's Model interface (gten/abc.h), so
+// that the reference's own greedy_sample drives it.
+class HarnessModel : public gten::Model {
+public:
+    HarnessModel(void* m, int inference_ctx, int train_ctx) : Model(inference_ctx, train_ctx), m_(m) {}
+    Tensor logits(const Tensor& tokens, const int start_pos) override
+    {
+        Tensor out({static_cast<RefModel*>(m_)->cfg.n_vocab}, kFloat32);
+        ref_model_logits(m_, tokens.data_ptr<int32_t>(), tokens.numel(), start_pos, out.data_ptr<float>());
+        return out;
+    }
+    void load_from_ckpt(std::ifstream&) override {}
+    void print_perf(const int) override {}
+
+private:
+    void* m_;
+};
+
+}  // namespace
+
+extern "C" {
+
+// gten::greedy_sample (gten/sampler.cpp:11-60) itself, prompt text in, the
+// text it writes to std::cerr out (`cap` bytes at most; returns the full
+// length).
+int ref_greedy_sample_text(void* model, void* tok, const char* prompt, int inference_ctx, int train_ctx, char* out,
+                           int cap)
+{
+    HarnessModel hm(model, inference_ctx, train_ctx);
+    std::ostringstream os;
+    std::streambuf* old = std::cerr.rdbuf(os.rdbuf());
+    std::string p(prompt);
+    gten::greedy_sample(p, &hm, static_cast<RefTokenizer*>(tok)->t, false);
+    std::cerr.rdbuf(old);
+    const std::string s = os.str();
+    std::memcpy(out, s.data(), std::min<size_t>(s.size(), (size_t)cap));
+    return (int)s.size();
+}
 
 }  // extern "C"

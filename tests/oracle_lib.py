@@ -158,6 +158,15 @@ class Reference(_Lib):
         self.tok_encode = b("ref_tok_encode", _I, [_VP, C.c_char_p, _VP, _I])
         self.tok_decode = b("ref_tok_decode", C.c_char_p, [_VP, _I, _I])
         self.tok_free = b("ref_tok_free", None, [_VP])
+        self.greedy_sample_text_ = b("ref_greedy_sample_text", _I, [_VP, _VP, C.c_char_p, _I, _I, C.c_char_p, _I])
+
+    def greedy_sample_text(self, model, tok, prompt, inference_ctx, train_ctx):
+        """gten::greedy_sample's output text (bytes) for a prompt (bytes)."""
+        cap = 1 << 16
+        buf = C.create_string_buffer(cap)
+        n = self.greedy_sample_text_(model, tok, prompt, inference_ctx, train_ctx, buf, cap)
+        assert n <= cap
+        return buf.raw[:n]
 
     def token_embed(self, table, wdt, tokens, out, adt, d, vocab, start, n_ctx):
         self.token_embed_(table, wdt, tokens, out, adt, d, vocab, start, n_ctx)

@@ -60,10 +60,10 @@ def test_tokenizer_errors():
 
 # nanochat.cpp:189-229: vocabulary file, then the reference tokenizer's constructor arguments
 MODELS = {
-    "tinyllama": ("tinyllama_tokenizer.bin", "llama", (32000, 2, b"user\n", b"", [1, 32001],
+    "tinyllama": ("tinyllama_tokenizer.bin", "llama", (32000, 32002, b"user\n", b"", [1, 32001],
                                                        [32002, 29871, 13, 32001, 20255, 13])),
     "minicpm": ("minicpm_tokenizer.bin", "llama", (122753, 2, "<用户>".encode(), "<AI>".encode(), [], [])),
-    "openelm_sm": ("tinyllama_tokenizer.bin", "llama", (32000, 2, b"", b"", [1], [])),
+    "openelm_sm": ("tinyllama_tokenizer.bin", "llama", (32000, 32002, b"", b"", [1], [])),
     "zephyr": ("zephyr_tokenizer.bin", "gpt2", (100352, 100257)),
 }
 

@@ -70,6 +70,25 @@ LONG = {
                             n_kv_heads=4, n_ffn=512, eos=-1, rope_pct=0.25, prompt=4080, gen=16, seed=0x10C0004),
 }
 
+# The text path (greedy_sample: prompt text -> tokens -> model -> text):
+# small models over the synthetic vocabulary of tests/golden/tok/ (482
+# pieces, ids up to 511 decode to nothing), the inference context is
+# prompt + generated tokens.
+CHAT_TOKENIZER = "bpe_chat"
+CHAT_PROMPTS = ["Tell me a story about the quick brown fox.", "hello world", "abc " * 12]
+CHAT_TOPK = dict(temp=0.9, top_k=50, seed=7)
+CHAT = {
+    "chat-llama-q8": dict(arch=nc.LLAMA, wdtype=nc.Q8, n_vocab=512, n_embd=256, n_layers=2, n_heads=4,
+                          n_kv_heads=2, n_ffn=512, eos=2, rope_pct=1.0, prompt=0, gen=96, seed=2101),
+    "chat-minicpm-q4": dict(arch=nc.MINICPM, wdtype=nc.Q4, n_vocab=512, n_embd=256, n_layers=2, n_heads=4,
+                            n_kv_heads=4, n_ffn=512, eos=2, rope_pct=1.0, prompt=0, gen=96, seed=2102),
+    "chat-zephyr-f16": dict(arch=nc.ZEPHYR, wdtype=nc.F16, n_vocab=512, n_embd=256, n_layers=2, n_heads=4,
+                            n_kv_heads=4, n_ffn=512, eos=2, rope_pct=0.25, prompt=0, gen=96, seed=2103),
+    "chat-openelm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=512, n_embd=256, n_layers=3,
+                            n_heads=[2, 2, 3], n_kv_heads=[1, 1, 1], n_ffn=[256, 512, 768], eos=2,
+                            rope_pct=1.0, prompt=0, gen=96, seed=2104),
+}
+
 ALL = dict(SMALL, **WIDE, **LONG, **nc.WORKLOADS)
 
 
