@@ -41,7 +41,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // on the same rows, side by side in columns), MR groups of 4 rows (one MFMA
 // row operand each) per workgroup; the first 4 MR x kGmChunk threads stage
 // the activation blocks.
-template <int WT, int NG, int NW, int MR>
+template <int WT, int NG, int NW, int MR, int PF, bool MF = false>
 __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
                                                       const uint32_t* __restrict__ wq,
                                                       const uint16_t* __restrict__ wd, float* __restrict__ out,
@@ -95,77 +95,128 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
 #pragma unroll
             for (int k = 0; k < 4; k++) acc[m][n][k] = 0.0f;
 
-    uint32_t wc[kGmChunk][kGmNg][WV];
-    uint16_t dc[kGmChunk][kGmNg];
-    {
-        XRaw xr{};
-        if (tid < kStagers) xr = stage_load(0);
-        w_load(0, wc, dc);
-        if (tid < kStagers) stage_x_block(xr, xs[0][sblk][srow]);
+    // weights and activation blocks: a ring of PF chunks in registers;
+    // chunk ch sits in slot ch % PF from its request (PF chunks ahead) until
+    // it is used, so HBM latency hides behind PF chunks of work, and a slot
+    // is refilled straight after use (no register copies, which would wait
+    // for the loads).  Both are requested together because the vector
+    // memory counter completes in order: the activation blocks staged at
+    // the end of chunk ch (chunk ch + 1's) were requested PF - 1 chunks
+    // earlier, so waiting for them waits only for loads that old.  Every
+    // request is issued (chunks past the end re-read the last blocks), so
+    // the waits are exact counts.
+    uint32_t wr[PF][kGmChunk][kGmNg][WV];
+    uint16_t dr[PF][kGmChunk][kGmNg];
+    XRaw xq[PF];
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+        w_load(p, wr[p], dr[p]);
+        xq[p] = stage_load(min(p, nch - 1));
     }
+    if (tid < kStagers) stage_x_block(xq[0], xs[0][sblk][srow]);
     lds_barrier();
-    for (int ch = 0; ch < nch; ch++) {
-        const int buf = ch & 1;
-        const bool more = ch + 1 < nch;
-        XRaw xn{};
-        uint32_t wn[kGmChunk][kGmNg][WV];
-        uint16_t dn[kGmChunk][kGmNg];
-        if (more) {
-            if (tid < kStagers) xn = stage_load(ch + 1);
-            w_load(ch + 1, wn, dn);
-        }
+    for (int cb = 0; cb < nch; cb += PF) {
 #pragma unroll
-        for (int j = 0; j < kGmChunk; j++) {
-            if (ch * kGmChunk + j >= nb) break;  // uniform
-            // weight operands: column lc of group n, lane lg's eight codes
-            long B[kGmNg];
-            float dw[kGmNg];
+        for (int p = 0; p < PF; p++) {
+            const int ch = cb + p;
+            if (ch >= nch) break;  // uniform
+            const int buf = ch & 1;
+            if constexpr (MF) {
+                // the chunk's MFMAs first (nb % kGmChunk == 0), then its folds
+                // in block order: no fold waits on the MFMA just issued
+                v4i L[kGmChunk][MR][kGmNg];
+                float dd[kGmChunk][MR][kGmNg];
 #pragma unroll
-            for (int n = 0; n < kGmNg; n++) {
-                if (WT == Q4) {
-                    const uint32_t P = wc[j][n][0];
-                    // high nibbles pair with codes {2k,2k+1,2k+8,2k+9}, low
-                    // nibbles with those + 16 (the staged xa_k, xb_k order)
-                    B[n] = (long)(uint64_t)(((P >> 4) & 0x0F0F0F0Fu) | ((uint64_t)(P & 0x0F0F0F0Fu) << 32));
-                } else {
-                    B[n] = (long)(uint64_t)(wc[j][n][0] | ((uint64_t)wc[j][n][1] << 32));
+                for (int j = 0; j < kGmChunk; j++) {
+                    long B[kGmNg];
+                    float dw[kGmNg];
+#pragma unroll
+                    for (int n = 0; n < kGmNg; n++) {
+                        if (WT == Q4) {
+                            const uint32_t P = wr[p][j][n][0];
+                            B[n] = (long)(uint64_t)(((P >> 4) & 0x0F0F0F0Fu) | ((uint64_t)(P & 0x0F0F0F0Fu) << 32));
+                        } else {
+                            B[n] = (long)(uint64_t)(wr[p][j][n][0] | ((uint64_t)wr[p][j][n][1] << 32));
+                        }
+                        dw[n] = h2f(dr[p][j][n]);
+                    }
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        const uint32_t* sa = xs[buf][j][4 * m + (lc >> 2)];
+                        const uint2 v = *reinterpret_cast<const uint2*>(sa + 2 * lg);
+                        const bool own = lg == (lc & 3);
+                        const long A = (long)(uint64_t)((own ? v.x : 0u) | ((uint64_t)(own ? v.y : 0u) << 32));
+                        const uint32_t* sr = xs[buf][j][4 * m + lg];
+                        const uint4 cs = *reinterpret_cast<const uint4*>(sr + 8);
+                        const v4i cinit = WT == Q4 ? v4i{(int)cs.x, (int)cs.y, (int)cs.z, (int)cs.w} : v4i{0, 0, 0, 0};
+                        const float dx = __uint_as_float(sr[12]);
+#pragma unroll
+                        for (int n = 0; n < kGmNg; n++) {
+                            L[j][m][n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B[n], cinit, 0, 0, 0);
+                            dd[j][m][n] = dx * dw[n];
+                        }
+                    }
                 }
-                dw[n] = h2f(dc[j][n]);
-            }
 #pragma unroll
-            for (int m = 0; m < MR; m++) {
-                // activation operand: matrix row lc = 4 r' + k of row group m
-                // holds row (4m + r')'s lane-k codes in K group k only
-                const uint32_t* sa = xs[buf][j][4 * m + (lc >> 2)];
-                const uint2 v = *reinterpret_cast<const uint2*>(sa + 2 * lg);
-                const bool own = lg == (lc & 3);
-                const long A = (long)(uint64_t)((own ? v.x : 0u) | ((uint64_t)(own ? v.y : 0u) << 32));
-                // this thread's outputs: row 4m + lg, lane sums k = 0..3
-                const uint32_t* sr = xs[buf][j][4 * m + lg];
-                const uint4 cs = *reinterpret_cast<const uint4*>(sr + 8);
-                const v4i cinit = WT == Q4 ? v4i{(int)cs.x, (int)cs.y, (int)cs.z, (int)cs.w} : v4i{0, 0, 0, 0};
-                const float dx = __uint_as_float(sr[12]);
+                for (int j = 0; j < kGmChunk; j++)
+#pragma unroll
+                    for (int m = 0; m < MR; m++)
+#pragma unroll
+                        for (int n = 0; n < kGmNg; n++)
+#pragma unroll
+                            for (int k = 0; k < 4; k++)
+                                acc[m][n][k] = acc[m][n][k] + (float)L[j][m][n][k] * dd[j][m][n];
+            } else {
+#pragma unroll
+            for (int j = 0; j < kGmChunk; j++) {
+                if (ch * kGmChunk + j >= nb) break;  // uniform
+                // weight operands: column lc of group n, lane lg's eight codes
+                long B[kGmNg];
+                float dw[kGmNg];
 #pragma unroll
                 for (int n = 0; n < kGmNg; n++) {
-                    const v4i L = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B[n], cinit, 0, 0, 0);
-                    const float dd = dx * dw[n];
+                    if (WT == Q4) {
+                        const uint32_t P = wr[p][j][n][0];
+                        // high nibbles pair with codes {2k,2k+1,2k+8,2k+9},
+                        // low nibbles with those + 16 (the staged xa_k, xb_k
+                        // order)
+                        B[n] = (long)(uint64_t)(((P >> 4) & 0x0F0F0F0Fu) | ((uint64_t)(P & 0x0F0F0F0Fu) << 32));
+                    } else {
+                        B[n] = (long)(uint64_t)(wr[p][j][n][0] | ((uint64_t)wr[p][j][n][1] << 32));
+                    }
+                    dw[n] = h2f(dr[p][j][n]);
+                }
 #pragma unroll
-                    for (int k = 0; k < 4; k++) acc[m][n][k] = acc[m][n][k] + (float)L[k] * dd;
+                for (int m = 0; m < MR; m++) {
+                    // activation operand: matrix row lc = 4 r' + k of row
+                    // group m holds row (4m + r')'s lane-k codes in K group
+                    // k only
+                    const uint32_t* sa = xs[buf][j][4 * m + (lc >> 2)];
+                    const uint2 v = *reinterpret_cast<const uint2*>(sa + 2 * lg);
+                    const bool own = lg == (lc & 3);
+                    const long A = (long)(uint64_t)((own ? v.x : 0u) | ((uint64_t)(own ? v.y : 0u) << 32));
+                    // this thread's outputs: row 4m + lg, lane sums k = 0..3
+                    const uint32_t* sr = xs[buf][j][4 * m + lg];
+                    const uint4 cs = *reinterpret_cast<const uint4*>(sr + 8);
+                    const v4i cinit = WT == Q4 ? v4i{(int)cs.x, (int)cs.y, (int)cs.z, (int)cs.w} : v4i{0, 0, 0, 0};
+                    const float dx = __uint_as_float(sr[12]);
+#pragma unroll
+                    for (int n = 0; n < kGmNg; n++) {
+                        const v4i L = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B[n], cinit, 0, 0, 0);
+                        const float dd = dx * dw[n];
+#pragma unroll
+                        for (int k = 0; k < 4; k++) acc[m][n][k] = acc[m][n][k] + (float)L[k] * dd;
+                    }
                 }
             }
+            }
+            // the slot's next chunk, then chunk ch + 1's activation blocks
+            // into the other staging buffer
+            w_load(ch + PF, wr[p], dr[p]);
+            xq[p] = stage_load(min(ch + PF, nch - 1));
+            if (ch + 1 < nch && tid < kStagers) stage_x_block(xq[(p + 1) % PF], xs[buf ^ 1][sblk][srow]);
+            lds_barrier();
         }
-        if (more) {
-#pragma unroll
-            for (int j = 0; j < kGmChunk; j++)
-#pragma unroll
-                for (int n = 0; n < kGmNg; n++) {
-#pragma unroll
-                    for (int v = 0; v < WV; v++) wc[j][n][v] = wn[j][n][v];
-                    dc[j][n] = dn[j][n];
-                }
-            if (tid < kStagers) stage_x_block(xn, xs[buf ^ 1][sblk][srow]);
-        }
-        lds_barrier();
     }
 #pragma unroll
     for (int m = 0; m < MR; m++) {
@@ -179,15 +230,21 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
     }
 }
 
-// Workgroup shape (measured on MI355X, prefill of 64 and 512 rows, exact
-// results in every shape): one wavefront per workgroup (a workgroup of four
-// on the same rows is slower: it shares the staging but waits at every
-// chunk's barrier), four row groups (16 rows) per wavefront -- one or two
-// row groups are slower (7.4K, 10.9K tok/s against 11.2K for TinyLlama):
-// the weights a wavefront loads serve fewer rows -- and two 16-wide column
-// groups per wavefront for long prompts (MiniCPM, 512 rows: 12.3K against
-// 11.3K tok/s), one for short ones (TinyLlama, 64 rows: 11.2K against 9.9K).
+// Workgroup shapes, measured on MI355X with Q4 weights (us per launch,
+// exact results in every shape): NG 16-wide column groups per wavefront,
+// NW wavefronts per workgroup sharing one staging of 4 MR rows, PF weight
+// chunks in flight, MF MFMAs first.
+//   64 rows:   q|k|v (2560 x 2048) 30.6 -> 22.1 with (1, 1, 4, 3, MF);
+//              o 28.5 -> 21.2, down (2048 x 5632) 67.0 -> 49.8 the same;
+//              gate|up (11264 x 2048) 81.6 -> 56.4 with (1, 2, 8, 4)
+//   512 rows:  (1, 2, 8, 4): q|k|v 138 -> 74, o 93 -> 62, down 196 -> 138;
+//              gate|up 503 -> 265 with (2, 2, 8, 3)
+// Wider shapes re-read the staged rows from LDS fewer times per weight
+// column but leave fewer wavefronts for short prompts; MFMAs first lets a
+// chunk's folds run without waiting on each MFMA result, and needs the
+// chunk's four blocks to exist (nb % 4 == 0).
 constexpr int kGemmWideRows = 256;
+constexpr int kGemmTallCols = 8192;
 
 int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
                hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop)
@@ -196,20 +253,22 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
     if (w->cols % 32 || w->cols <= 0 || w->rows <= 0 || n_rows <= 0)
         return fail(NC_ERR_ARG, "gemm: [%d x %d] weights, %d rows", w->rows, w->cols, n_rows);
     const int N = w->rows, nb = w->cols / 32;
-    auto go = [&](auto kern, int mr, int ng) {
-        const dim3 grid((N + 16 * ng - 1) / (16 * ng), (n_rows + 4 * mr - 1) / (4 * mr));
+    auto go = [&](auto kern, int mr, int ng, int nw) {
+        const dim3 grid((N + 16 * ng * nw - 1) / (16 * ng * nw), (n_rows + 4 * mr - 1) / (4 * mr));
         if (ev_start)
-            hipExtLaunchKernelGGL(kern, grid, dim3(64), 0, st, ev_start, ev_stop, 0, x, x_pitch, n_rows,
+            hipExtLaunchKernelGGL(kern, grid, dim3(64 * nw), 0, st, ev_start, ev_stop, 0, x, x_pitch, n_rows,
                                   (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
         else
-            hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, x, x_pitch, n_rows, (const uint32_t*)w->data,
+            hipLaunchKernelGGL(kern, grid, dim3(64 * nw), 0, st, x, x_pitch, n_rows, (const uint32_t*)w->data,
                                (const uint16_t*)w->deltas, out, out_pitch, N, nb);
     };
-    const bool wide = n_rows >= kGemmWideRows;
+    const bool wide = n_rows >= kGemmWideRows, tall = N >= kGemmTallCols;
     auto by_type = [&](auto wt) {
         constexpr int WT = decltype(wt)::value;
-        if (wide) go(k_gemm_q<WT, 2, 1, 4>, 4, 2);
-        else go(k_gemm_q<WT, 1, 1, 4>, 4, 1);
+        if (wide && tall) go(k_gemm_q<WT, 2, 2, 8, 3>, 8, 2, 2);
+        else if (wide || (tall && n_rows >= 32)) go(k_gemm_q<WT, 1, 2, 8, 4>, 8, 1, 2);
+        else if (nb % kGmChunk == 0) go(k_gemm_q<WT, 1, 1, 4, 3, true>, 4, 1, 1);
+        else go(k_gemm_q<WT, 1, 1, 4, 3>, 4, 1, 1);
     };
     if (w->dtype == NC_Q4) by_type(std::integral_constant<int, Q4>{});
     else by_type(std::integral_constant<int, Q8>{});
