@@ -64,7 +64,8 @@ FUSED_KERNEL = {"qkv": "k_dmv (qkv, residual add + rms_norm prologue)",
                 "o": "k_dmv (o)",
                 "gate_up": "k_dmv_glu (gate|up, residual add + rms_norm prologue, SwiGLU epilogue)",
                 "down": "k_dmv (down)",
-                "lm_head": "k_dmv (lm head, residual add + final norm prologue, greedy-token epilogue)"}
+                "lm_head": "k_dmv_head (lm head in the head layout, residual add + final norm prologue, "
+                           "greedy-token epilogue; k_dmv for widths other than 2048 / 2304)"}
 
 
 def prompt_tokens(w):
