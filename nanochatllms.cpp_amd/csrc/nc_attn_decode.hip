@@ -39,7 +39,7 @@ __device__ __forceinline__ void static_for(F&& f)
     }
 }
 
-constexpr int kAdThreads = 256;
+constexpr int kAdThreads = 512;
 constexpr int kAdMaxK = 2;      // K rows per thread requested at kernel start, at most
 constexpr int kAdVB = 80;       // LDS bytes per staged V position: 64 codes, 2 fp16 deltas, pad
 constexpr int kAdVc = 128;      // positions per staged V chunk (2 16-byte parts per thread)
@@ -115,11 +115,13 @@ __device__ __forceinline__ float score_of(const uint4 (&qv)[4], const float (&dq
     return head_dot_q8(qv, dq, k.q, dk);
 }
 
-// The V parts of one chunk a thread carries: 16-byte parts tid and tid + 256
-// (position = part / 4 within the chunk), and the delta dword of position tid
-// (threads below kAdVc).
+// The V parts of one chunk a thread carries: 16-byte parts tid + i
+// kAdThreads (position = part / 4 within the chunk), and the delta dword of
+// position tid (threads below kAdVc).
+constexpr int kAdVParts = kAdVc * 4 / kAdThreads;
+static_assert(kAdVParts >= 1 && kAdVParts * kAdThreads == kAdVc * 4 && kAdVc <= kAdThreads, "V chunk parts");
 struct VChunk {
-    uint32_t p[2][4];  // plain words: an array of the uint4 union type stays in scratch memory
+    uint32_t p[kAdVParts][4];  // plain words: an array of the uint4 union type stays in scratch memory
     uint32_t d;
 };
 
@@ -130,7 +132,7 @@ __device__ __forceinline__ void load_vchunk(VChunk& v, const uint8_t* vslice, co
 {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < kAdVParts; i++) {
         const int idx = tid + i * kAdThreads;
         const int c = min(ch * kAdVc + (idx >> 2), kv_rows - 1);
         const uint4 t4 = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[idx & 3];
@@ -149,7 +151,7 @@ __device__ __forceinline__ void store_vchunk(const VChunk& v, uint8_t* buf, int 
 {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < kAdVParts; i++) {
         const int idx = tid + i * kAdThreads;
         const int cl = idx >> 2, part = idx & 3;
         uint4 t4 = make_uint4(v.p[i][0], v.p[i][1], v.p[i][2], v.p[i][3]);
@@ -180,7 +182,8 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     extern __shared__ __align__(16) float sm[];
     __shared__ __align__(16) uint8_t s_q[kAdVB], s_k[kAdVB], s_v[kAdVB];
     __shared__ __align__(16) float s_nrm[2][64];
-    __shared__ float red[8];
+    __shared__ float red[kAdThreads / kWave];
+    __shared__ float s_sum;
     __shared__ SsShared ssh;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     // workgroup i runs on XCD i % 8: with hq % 8 == 0, XCD x takes heads
@@ -299,7 +302,9 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     mx = wave_max(mx);
     if (lane == 0) red[w] = mx;
     lds_barrier();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int q = 1; q < kAdThreads / kWave; q++) mx = fmaxf(mx, red[q]);
     const bool long_row = n > kAdSeqMax;
     const int npad = (n + kSsThreads - 1) & ~(kSsThreads - 1);
     for (int c = tid; c < (long_row ? npad : n); c += kAdThreads) S[c] = c < n ? expf_ref(S[c] - mx) : 0.0f;
@@ -312,10 +317,10 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     } else {
         if (w == 0) {
             const float ss = seq_sum(S, n);
-            if (lane == 0) red[4] = ss;
+            if (lane == 0) s_sum = ss;
         }
         lds_barrier();
-        sum = red[4];
+        sum = s_sum;
     }
     for (int c0 = 0; c0 < n; c0 += kAdThreads) {
         const int c = c0 + tid;
@@ -326,54 +331,43 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     }
     lds_barrier();
 
-    // ---- P.V: thread = (lane l = tid / 32, columns 2m and 2m + 1 with
-    // m = tid % 32): the chains (l, 2m) and (l, 2m + 1) over positions l,
-    // l + 8, ... in order, both column codes of a position in one load.
-    // Chunk ch sits in buffer ch & 1 while chunk ch + 1 is parked in the
-    // other and chunk ch + 2 is requested.
-    const int l = tid >> 5, m = tid & 31;
+    // ---- P.V: thread = (lane l = tid / 64, column m = tid % 64): the chain
+    // (l, m) over positions l, l + 8, ... in order.  Chunk ch sits in buffer
+    // ch & 1 while chunk ch + 1 is parked in the other and chunk ch + 2 is
+    // requested.
+    static_assert(kAdThreads == 8 * 64, "one P.V chain per thread");
+    const int l = tid >> 6, m = tid & 63;
     const int n8 = n & ~7;
-    float a0 = 0.0f, a1 = 0.0f;
+    float a0 = 0.0f;
     for (int ch = 0; ch < nch; ch++) {
         const uint8_t* B = Vb + (ch & 1) * (kAdVc * kAdVB);
         const int c0 = ch * kAdVc;
         const int cend = min(c0 + kAdVc, n8);
-        auto vpair = [&](int c, float& v0, float& v1) {
+        auto vone = [&](int c) {
             const uint8_t* vrow = B + (c - c0) * kAdVB;
-            const uint32_t codes = reinterpret_cast<const uint16_t*>(vrow)[m];
-            const float d = h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[m >> 4]);  // block of column 2m
-            v0 = (float)(int8_t)(codes & 0xFFu) * d;
-            v1 = (float)(int8_t)(codes >> 8) * d;
+            const float d = h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[m >> 5]);  // block of column m
+            return (float)reinterpret_cast<const int8_t*>(vrow)[m] * d;
         };
         int c = c0;
         for (; c + 64 <= cend; c += 64) {
-            // eight positions of both chains: loads first, then the adds in order
-            float p[8], v0[8], v1[8];
+            // eight positions of the chain: loads first, then the adds in order
+            float p[8], v[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 p[u] = S[c + 8 * u + l];
-                vpair(c + 8 * u + l, v0[u], v1[u]);
+                v[u] = vone(c + 8 * u + l);
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                a0 = p[u] * v0[u] + a0;
-                a1 = p[u] * v1[u] + a1;
-            }
+            for (int u = 0; u < 8; u++) a0 = p[u] * v[u] + a0;
         }
-        for (; c < cend; c += 8) {
-            float v0, v1;
-            vpair(c + l, v0, v1);
-            const float p = S[c + l];
-            a0 = p * v0 + a0;
-            a1 = p * v1 + a1;
-        }
+        for (; c < cend; c += 8) a0 = S[c + l] * vone(c + l) + a0;
         if (ch + 1 < nch) {
             store_vchunk(vch, Vb + ((ch + 1) & 1) * (kAdVc * kAdVB), ch + 1, pos, s_v);
             if (ch + 2 < nch) load_vchunk(vch, vslice, vc + kvd, ch + 2, kv_pitch, g, kv_rows);
         }
         lds_barrier();
     }
-    *reinterpret_cast<float2*>(acc + l * 64 + 2 * m) = make_float2(a0, a1);
+    acc[l * 64 + m] = a0;
     lds_barrier();
     if (w == 0) {
         // lanes left to right, then the tail positions [n8, n) in order (all
@@ -419,8 +413,8 @@ int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, 
         hipLaunchKernelGGL(kern, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w, (const float2*)table,
                            d_half, pos, dpos, kc, vc, kv_pitch, out, scale, (const float2*)rope_cur, max_ctx);
     };
-    // K rows requested at the start: one per thread for caches of up to 256
-    // positions, two beyond
+    // K rows requested at the start: one per thread for caches of up to
+    // kAdThreads positions, two beyond
     auto by_ctx = [&](auto qk) {
         constexpr bool QK = decltype(qk)::value;
         if (max_ctx <= kAdThreads) go(k_attn_dec<QK, 1>);
