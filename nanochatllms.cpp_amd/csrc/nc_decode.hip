@@ -107,7 +107,7 @@ __device__ __forceinline__ void load_f32_chunk(const float* p, int ch, float (&v
 // an LDS barrier.  ROWS_FIRST (norm prologues): the weights are requested
 // only once the rows have arrived -- a launch that requests tens of MB
 // would otherwise queue its rows behind its own weights.
-template <int PRO, int NCH, bool ROWS_FIRST = false, class LoadW>
+template <int PRO, int NCH, bool ROWS_FIRST = false, int NT = kDmvThreads, class LoadW>
 __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, LoadW&& load_w)
 {
     const int tid = threadIdx.x;
@@ -143,7 +143,7 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
         }
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * kDmvThreads;
+            const int ch = tid + j * NT;
             const int cc = ch < nch ? ch : 0;
             load_act_chunk(arow, K, cc, av[j]);
             if (PRO == PRO_RES_RMS) load_f32_chunk(A.raw_in, cc, ov[j]);
@@ -162,9 +162,9 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
         if (fixed && A.dpos) pos = posv;
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * kDmvThreads;
+            const int ch = tid + j * NT;
             const bool valid = ch < nch;
-            if (j * kDmvThreads >= nch) break;  // uniform
+            if (j * NT >= nch) break;  // uniform
             if (PRO == PRO_RES_RMS) {
                 quad_roundtrip(ov[j]);
                 if (A.bscale != 1.0f) {
@@ -200,8 +200,8 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
         // the normalized row as stored (codes, then deltas) over sq's bytes
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * kDmvThreads;
-            if (j * kDmvThreads >= nch) break;  // uniform
+            const int ch = tid + j * NT;
+            if (j * NT >= nch) break;  // uniform
             float y[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) y[i] = h[j][i] / denom * gain[j][i];
@@ -681,15 +681,16 @@ __global__ void k_head_layout(const uint32_t* __restrict__ wq, const uint16_t* _
 // rows (f + 32b + r) -- all of their weights requested up front -- in two
 // halves through the fold, then m = Act(Act(silu(Act(g))) * Act(u)) for the
 // block (tinyllama/tinyllama.cpp:88-97).  No workgroup waits for another.
-constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / 256 threads, NB <= 72
+constexpr int kGluThreads = 512;  // gate|up workgroup: 64 rows' block terms over 8 wavefronts
+constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / threads, NB <= 72
 
 template <int WT, int PRO, int NCH, int NB>
-__global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
+__global__ __launch_bounds__(kGluThreads) void k_dmv_glu(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
     constexpr int WV = WD / 4;
     constexpr int TP = ((NB + 3) & ~3) + 4;
-    constexpr int IT = NB / 4;    // weight blocks per thread (64 rows)
+    constexpr int IT = NB * 64 / kGluThreads;  // weight blocks per thread (64 rows)
     static_assert(NB % 8 == 0 && IT <= kGluMaxItems, "gate|up block shape");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
@@ -705,7 +706,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     auto load_block = [&](int b) {
 #pragma unroll
         for (int it = 0; it < IT; it++) {
-            const int j = tid + it * kDmvThreads;
+            const int j = tid + it * kGluThreads;
             const int r = j / NB, i = j - r * NB;
             const int row = r < 32 ? 32 * b + r : f + 32 * b + (r - 32);
             const size_t bi = (size_t)row * NB + i;
@@ -718,19 +719,19 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
     int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks
     DmvArgs P = A;
     P.nb = NB;
-    dmv_prologue<PRO, NCH>(P, xs, sq, ssh, [&] { load_block(b); });
+    dmv_prologue<PRO, NCH, false, kGluThreads>(P, xs, sq, ssh, [&] { load_block(b); });
 
     // the terms of all 64 rows, then the gate rows' folds (waves 0-1) and
     // the up rows' folds (waves 2-3) side by side
     auto pass = [&]() {
         // NB dividing the workgroup: every item of a thread is block
         // tid % NB, read from LDS once
-        constexpr bool kOneBlock = kDmvThreads % NB == 0;
+        constexpr bool kOneBlock = kGluThreads % NB == 0;
         StagedX x0{};
         if (kOneBlock) x0 = load_staged(xs + (tid % NB) * kStage);
 #pragma unroll
         for (int it = 0; it < IT; it++) {
-            const int j = tid + it * kDmvThreads;
+            const int j = tid + it * kGluThreads;
             const int r = j / NB, i = j - r * NB;
             float tv[4];
             if (kOneBlock)
@@ -742,8 +743,8 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_glu(DmvArgs A)
             for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
         }
         lds_barrier();
-        {
-            // thread 4r + k folds lane k of row r in block order
+        if (tid < 64 * 4) {
+            // thread 4r + k folds lane k of row r in block order (waves 0-3)
             const float acc = seq_sum<16>(T + tid * TP, NB);
             const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
             if ((tid & 3) == 0) {
@@ -841,15 +842,15 @@ int glu_go(DmvArgs A, size_t lds, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1
     static int max_grid = 0;
     if (!max_grid) {
         int per_cu = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kDmvThreads, lds);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kGluThreads, lds);
         if (e != hipSuccess) return hip_fail(e, "decode matvec: occupancy");
         max_grid = std::min(kDmvMaxGrid, std::max(1, per_cu) * device_cus());
     }
     const dim3 grid(std::min(A.N / 64, max_grid));
     if (ev0)
-        hipExtLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, ev0, ev1, 0, A);
+        hipExtLaunchKernelGGL(kern, grid, dim3(kGluThreads), lds, st, ev0, ev1, 0, A);
     else
-        hipLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, A);
+        hipLaunchKernelGGL(kern, grid, dim3(kGluThreads), lds, st, A);
     return launch_status("k_dmv_glu");
 }
 
@@ -912,8 +913,8 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
             if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64>(A, lds, st, ev0, ev1);
             return glu_go<WT, PRO_RES_RMS, 1, 64>(A, lds, st, ev0, ev1);
         }
-        if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 2, 72>(A, lds, st, ev0, ev1);
-        return glu_go<WT, PRO_RES_RMS, 2, 72>(A, lds, st, ev0, ev1);
+        if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 72>(A, lds, st, ev0, ev1);
+        return glu_go<WT, PRO_RES_RMS, 1, 72>(A, lds, st, ev0, ev1);
     }
     if (A.head) {
         // an lm head in the head layout: one fold chain per thread, the
