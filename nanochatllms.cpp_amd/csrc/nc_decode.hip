@@ -389,8 +389,8 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
     }
 }
 
-template <int WT, int IT, int PRO, int EPI, int NCH>
-__global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
+template <int WT, int IT, int PRO, int EPI, int NCH, int NT = kDmvThreads>
+__global__ __launch_bounds__(NT) void k_dmv(DmvArgs A)
 {
     constexpr int WD = WT == Q4 ? 4 : 8;
     constexpr int WV = WD / 4;
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     const int tid = threadIdx.x;
     const int nitems = R * nb;
 
-    // IT: weight blocks per thread (R rows x nb blocks <= IT x 256)
+    // IT: weight blocks per thread (R rows x nb blocks <= IT x NT)
     uint4 wc[IT][WV];
     uint16_t dc[IT];
     auto load_group = [&](int g, uint4(&w)[IT][WV], uint16_t(&dw)[IT]) {
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
         for (int it = 0; it < IT; it++) {
             // every slot loads (items past the group and rows past N: block
             // 0), so the waits for these loads are exact counts
-            const int j = tid + it * kDmvThreads;
+            const int j = tid + it * NT;
             const int r = j / nb, i = j - r * nb;
             const size_t b = j < nitems && g * R + r < A.N ? (size_t)(g * R + r) * nb + i : 0;
             const uint4* src = reinterpret_cast<const uint4*>(A.wq + b * WD);
@@ -425,7 +425,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
     };
     const int G = gridDim.x;
     int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
-    const int pos = dmv_prologue<PRO, NCH>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
+    const int pos = dmv_prologue<PRO, NCH, false, NT>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
 
     // EPI_ARGMAX: each row's lane-0 thread keeps the best key of its rows
     unsigned long long best = 0;
@@ -436,7 +436,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv(DmvArgs A)
         if (gn < A.ngroups) load_group(gn, wn, dn);
 #pragma unroll
         for (int it = 0; it < IT; it++) {
-            const int j = tid + it * kDmvThreads;
+            const int j = tid + it * NT;
             if (j >= nitems) continue;
             const int r = j / nb, i = j - r * nb;
             float tv[4];
@@ -814,14 +814,14 @@ DmvShape dmv_shape(int nb, int N, bool norm)
     return {best, false};
 }
 
-template <int WT, int IT, int PRO, int EPI, int NCH>
+template <int WT, int IT, int PRO, int EPI, int NCH, int NT = kDmvThreads>
 int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv<WT, IT, PRO, EPI, NCH>;
+    auto kern = k_dmv<WT, IT, PRO, EPI, NCH, NT>;
     static int max_grid = 0;  // per instantiation: workgroups resident at once
     if (!max_grid) {
         int per_cu = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kDmvThreads, lds);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NT, lds);
         if (e != hipSuccess) return hip_fail(e, "decode matvec: occupancy");
         max_grid = std::min(kDmvMaxGrid, std::max(1, per_cu) * device_cus());
     }
@@ -829,9 +829,9 @@ int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, h
     // spread: ngroups <= CUs, one workgroup each
     const dim3 grid(spread ? A.ngroups : std::min(A.ngroups, max_grid));
     if (ev0)
-        hipExtLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, ev0, ev1, 0, A);
+        hipExtLaunchKernelGGL(kern, grid, dim3(NT), lds, st, ev0, ev1, 0, A);
     else
-        hipLaunchKernelGGL(kern, grid, dim3(kDmvThreads), lds, st, A);
+        hipLaunchKernelGGL(kern, grid, dim3(NT), lds, st, A);
     return launch_status("k_dmv");
 }
 
@@ -895,6 +895,28 @@ int dmv_r(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t ev0, h
     return dmv_go<WT, 12, PRO, EPI, NCH>(A, lds, sh.spread, st, ev0, ev1);
 }
 
+// Norm-prologue launches spread one group per CU whose groups hold more than
+// four blocks per thread at 256 threads (MiniCPM's q|k|v: 32 rows x 72
+// blocks) run 512 threads: the block terms and the prologue's elementwise
+// work take half as long per thread, one 8-value chunk per thread up to 4096
+// values.  At four blocks or fewer (TinyLlama's, OpenELM's q|k|v) the wider
+// workgroup measured slower.
+constexpr int kDmvWideThreads = 512;
+
+template <int WT, int PRO>
+int dmv_r_wide(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    constexpr int NT = kDmvWideThreads;
+    const int tp = ((A.nb + 3) & ~3) + 4;
+    const size_t lds = lds0 + (size_t)sh.rows * 4 * tp * 4;
+    A.rows = sh.rows;
+    const int items = (sh.rows * A.nb + NT - 1) / NT;
+    if (items <= 1) return dmv_go<WT, 1, PRO, EPI_RAW, 1, NT>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 2) return dmv_go<WT, 2, PRO, EPI_RAW, 1, NT>(A, lds, sh.spread, st, ev0, ev1);
+    if (items <= 4) return dmv_go<WT, 4, PRO, EPI_RAW, 1, NT>(A, lds, sh.spread, st, ev0, ev1);
+    return dmv_go<WT, 6, PRO, EPI_RAW, 1, NT>(A, lds, sh.spread, st, ev0, ev1);
+}
+
 template <int WT>
 int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
@@ -941,6 +963,10 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
                        : dmv_r<WT, PRO_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
         return two ? dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
                    : dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
+    }
+    if (R.spread && R.rows * A.nb > kDmvThreads * 4 && R.rows * A.nb <= kDmvWideThreads * 6) {
+        if (pro == PRO_RMS) return dmv_r_wide<WT, PRO_RMS>(A, lds0, R, st, ev0, ev1);
+        return dmv_r_wide<WT, PRO_RES_RMS>(A, lds0, R, st, ev0, ev1);
     }
     if (pro == PRO_RMS)
         return two ? dmv_r<WT, PRO_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
