@@ -211,7 +211,11 @@ def kernel_table(ms, nbytes, kind, wdtype):
         fused = bool(k & nc.PROF_FUSED)
         avg_ms = float(ms[sel].mean())
         avg_b = float(nbytes[sel].mean())
-        unfused = "k_matvec_f16_row (fp16 decode matvec)" if wdtype == nc.F16 else "k_matvec_q"
+        if wdtype == nc.F16:
+            unfused = ("k_dmv_f16<GLU> (fp16 gate|up + SwiGLU decode matvec)" if role == "gate_up"
+                       else "k_dmv_f16 (fp16 decode matvec)")
+        else:
+            unfused = "k_matvec_q"
         out.append({"role": role, "kernel": FUSED_KERNEL[role] if fused else unfused,
                     "launches": int(sel.sum()), "total_ms": round(float(ms[sel].sum()), 4),
                     "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(avg_b),

@@ -18,6 +18,13 @@ int write_rows(const float* in, int in_pitch, uint8_t* out, int out_pitch, int d
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
                hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 
+// One fp16 row times the fused fp16 gate|up weight [2f, K] with the SwiGLU
+// epilogue: the fp16 row m[f] out.  Built for f a multiple of 4 and the
+// K the unrolled decode kernel covers (matvec_f16_glu_supported).
+bool matvec_f16_glu_supported(const nc_tensor* w);
+int matvec_f16_glu(const uint8_t* x, const nc_tensor* w, uint8_t* m_out, hipStream_t st,
+                   hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+
 // x rows times Q4/Q8 weight rows -> fp32 dots on the matrix cores (the
 // reference's block dot product, exact); used by matvec_raw for multi-row
 // (prefill) products.

@@ -313,6 +313,105 @@ __global__ __launch_bounds__(64) void k_matvec_f16_row(const uint8_t* __restrict
     if (j == 0 && row < N) out[row] = s;
 }
 
+// F16, one activation row (decode), for the group counts G = K / 64 it is
+// built for: the same lane chains as k_matvec_f16_row, fully unrolled over
+// the G groups so that each fold waits for its own loads only.  Weights come
+// through a ring of D loads per thread (the load for group g + D is issued
+// once group g is folded); the activation row is staged in LDS as fp16 in
+// the [G][8 lanes][8] order and read P groups ahead of its fold (the fp16 x
+// fp16 products go through v_fma_mix exactly as through fp32).
+// GLU: w is a fused gate|up [2f, K] weight; workgroup b takes gate rows
+// 4b .. 4b+3 and up rows f+4b .. f+4b+3 and, instead of the fp32 outputs,
+// writes the fp16 SwiGLU values m[4b + i] = Act(Act(silu(Act(g))) * Act(u))
+// as k_silu_mul does them (tinyllama/tinyllama.cpp:88-97 in the fp16 dtype).
+template <int G, int D, int P, bool GLU>
+__global__ __launch_bounds__(64) void k_dmv_f16(const uint8_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                               float* __restrict__ out, int N, uint16_t* __restrict__ m_out)
+{
+    constexpr int K = G * 64, XC = K / 8, XPT = (XC + 63) / 64;
+    static_assert(D <= G && P <= G && P <= 15, "ring depths");
+    __shared__ __align__(16) uint16_t xs[K];  // [G][8 lanes][8] halves
+    const int lane = threadIdx.x;
+    const int j = lane & 7, sub = lane >> 3;
+    const int row = GLU ? (sub < 4 ? 4 * (int)blockIdx.x + sub : N / 2 + 4 * (int)blockIdx.x + sub - 4)
+                        : (int)blockIdx.x * 8 + sub;
+    const int rowc = row < N ? row : N - 1;  // rows past N read a valid row and store nothing
+    const size_t gstride = (size_t)((N + 7) & ~7) * 8;  // uint4s per group
+    const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;
+    // the activation row first, then the weight ring, so staging waits for the row only
+    uint4 xv[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int c = lane + i * 64;  // 8-value chunk: group c >> 3, m = c & 7
+        xv[i] = (XC % 64 == 0 || c < XC) ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0, 0, 0, 0);
+    }
+    uint4 wv[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) wv[i] = load_stream(wrow + (size_t)i * gstride);
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int c = lane + i * 64;
+        if (XC % 64 == 0 || c < XC) {
+            const uint32_t q[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                xs[((c >> 3) * 8 + t) * 8 + (c & 7)] = (uint16_t)(t & 1 ? q[t >> 1] >> 16 : q[t >> 1] & 0xFFFFu);
+        }
+    }
+    __syncthreads();
+    const uint4* xrow = reinterpret_cast<const uint4*>(xs) + j;  // group g at xrow[g * 8]
+    uint4 xr[P];
+#pragma unroll
+    for (int i = 0; i < P; i++) xr[i] = xrow[i * 8];
+    float acc = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const uint4 xc = xr[g % P];
+        if (g + P < G) xr[g % P] = xrow[(g + P) * 8];
+        const uint4 wc = wv[g % D];
+        if (g + D < G) wv[g % D] = load_stream(wrow + (size_t)(g + D) * gstride);
+        const uint32_t wq[4] = {wc.x, wc.y, wc.z, wc.w}, xq[4] = {xc.x, xc.y, xc.z, xc.w};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const float a = h2f((uint16_t)(m & 1 ? xq[m >> 1] >> 16 : xq[m >> 1] & 0xFFFFu));
+            const float b = h2f((uint16_t)(m & 1 ? wq[m >> 1] >> 16 : wq[m >> 1] & 0xFFFFu));
+            acc = __builtin_fmaf(a, b, acc);  // exact product: same as mul then add
+        }
+        // keep the ring order: the reads for g + P and g + D stay ahead of later folds
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // lanes 0..7 of the row summed left to right
+    const int base = lane & ~7;
+    float s = __shfl(acc, base);
+#pragma unroll
+    for (int l = 1; l < 8; l++) s = s + __shfl(acc, base + l);
+    if (!GLU) {
+        if (j == 0 && row < N) out[row] = s;
+        return;
+    }
+    const float gsum = __shfl(s, (lane & 3) * 8), usum = __shfl(s, ((lane & 3) + 4) * 8);
+    if (lane < 4) {
+        const float g = f16_roundtrip(gsum);
+        const float gs = f16_roundtrip(g / (1.0f + expf_ref(-g)));
+        const float u = f16_roundtrip(usum);
+        m_out[4 * blockIdx.x + lane] = f2h(gs * u);
+    }
+}
+
+// The group counts k_dmv_f16 is built for (d_model and d_ffn of the fp16
+// models: 2048 / 5632 and 2304 / 5760), with the ring depths measured best.
+template <bool GLU, class Launch>
+bool dmv_f16_dispatch(int G, Launch&& go)
+{
+    switch (G) {
+    case 32: go(k_dmv_f16<32, 32, 8, GLU>); return true;
+    case 36: go(k_dmv_f16<36, 36, 8, GLU>); return true;
+    case 88: go(k_dmv_f16<88, 32, 8, GLU>); return true;
+    case 90: go(k_dmv_f16<90, 32, 8, GLU>); return true;
+    default: return false;
+    }
+}
+
 // out[r, c] = dot(x[r], w[c]) for x rows [0, n_rows) (pointers already at
 // the first row), fp32 out with `out_pitch` floats per row.
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
@@ -350,6 +449,17 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
         if (K % 64) return fail(NC_ERR_ARG, "matmul: F16 path needs K %% 64 == 0, K=%d", K);
         const size_t lds = (size_t)K * 4;
         if (lds > 64 * 1024) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);
+        if (n_rows == 1) {
+            const dim3 grid((N + 7) / 8);
+            auto go = [&](auto kern) {
+                if (ev_start)
+                    hipExtLaunchKernelGGL(kern, grid, dim3(64), 0, st, ev_start, ev_stop, 0, x,
+                                          (const uint16_t*)w->data, out, N, nullptr);
+                else
+                    hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, x, (const uint16_t*)w->data, out, N, nullptr);
+            };
+            if (dmv_f16_dispatch<false>(K / 64, go)) return launch_status("k_dmv_f16");
+        }
         if (n_rows == 1 && K <= 8192) {
             if (ev_start)
                 hipExtLaunchKernelGGL(k_matvec_f16_row, dim3((N + 7) / 8), dim3(64), lds, st, ev_start, ev_stop, 0, x,
@@ -370,6 +480,31 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
     }
     return fail(NC_ERR_ARG, "matmul: weight dtype %d", w->dtype);
 #undef NC_MV_LAUNCH
+}
+
+bool matvec_f16_glu_supported(const nc_tensor* w)
+{
+    return w->dtype == NC_F16 && w->rows % 8 == 0 && w->cols % 64 == 0 &&
+           dmv_f16_dispatch<true>(w->cols / 64, [](auto) {});
+}
+
+int matvec_f16_glu(const uint8_t* x, const nc_tensor* w, uint8_t* m_out, hipStream_t st, hipEvent_t ev_start,
+                   hipEvent_t ev_stop)
+{
+    const int N = w->rows, K = w->cols;
+    if (!matvec_f16_glu_supported(w))
+        return fail(NC_ERR_ARG, "gate|up SwiGLU matvec: [%d x %d] dtype %d", N, K, w->dtype);
+    const dim3 grid(N / 8);
+    auto go = [&](auto kern) {
+        if (ev_start)
+            hipExtLaunchKernelGGL(kern, grid, dim3(64), 0, st, ev_start, ev_stop, 0, x, (const uint16_t*)w->data,
+                                  nullptr, N, (uint16_t*)m_out);
+        else
+            hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, x, (const uint16_t*)w->data, nullptr, N,
+                               (uint16_t*)m_out);
+    };
+    dmv_f16_dispatch<true>(K / 64, go);
+    return launch_status("k_dmv_f16<GLU>");
 }
 
 }  // namespace nc

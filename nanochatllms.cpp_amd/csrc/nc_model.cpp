@@ -171,6 +171,22 @@ public:
         return wb + rows * (xb + 4.0 * N);
     }
 
+    // fp16 decode row: gate|up product with the SwiGLU epilogue in one
+    // launch, fp16 m row out.
+    int mv_glu(const uint8_t* x, const nc_tensor* w, uint8_t* m_out)
+    {
+        const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
+        int s = timed ? matvec_f16_glu(x, w, m_out, st, prof.ev[prof.used], prof.ev[prof.used + 1])
+                      : matvec_f16_glu(x, w, m_out, st);
+        if (s) return s;
+        if (timed) {
+            prof.used += 2;
+            prof.bytes.push_back(matvec_bytes(w, 1));
+            prof.kind.push_back(NC_PROF_GATE_UP);
+        }
+        return NC_OK;
+    }
+
     int mv(const uint8_t* x, int x_pitch, int rows, const nc_tensor* w, float* out, int out_pitch, int role)
     {
         const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
@@ -736,8 +752,12 @@ public:
             if ((s = norm_launch(norm_kind(), adt, true, xin + off, pd, o_raw, d, bs, y.res1 + off, pd, y.mlp_norm,
                                  y.mlp_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
                 return s;
-            if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f, NC_PROF_GATE_UP))) return s;
-            if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
+            if (R == 1 && adt == NC_F16 && matvec_f16_glu_supported(&y.gu)) {
+                if ((s = mv_glu(xn, &y.gu, m_act))) return s;
+            } else {
+                if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f, NC_PROF_GATE_UP))) return s;
+                if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
+            }
             if ((s = mv(m_act, pf, R, &y.down, down_raw, d, NC_PROF_DOWN))) return s;
             // out = h + mlp, then the next layer's attention norm (or the final norm)
             const bool last = l + 1 == cfg.n_layers;

@@ -61,6 +61,10 @@ MATMUL_CASES = [
     (F16, F16, 2048, 2048, 1, 0),
     (F16, F16, 5632, 2048, 1, 0),
     (F16, F16, 128, 44, 4, 1),
+    (F16, F16, 2304, 250, 1, 0),
+    (F16, F16, 5760, 2304, 1, 0),
+    (F16, F16, 2048, 100, 1, 0),
+    (F16, F16, 1280, 96, 1, 0),
 ]
 
 

@@ -45,6 +45,10 @@ WIDE = {
     # MiniCPM's own vocabulary: its tied lm head runs the row-chain kernel
     "wide-minicpm-q4": dict(arch=nc.MINICPM, wdtype=nc.Q4, n_vocab=122753, n_embd=2304, n_layers=2, n_heads=36,
                             n_kv_heads=36, n_ffn=5760, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0003),
+    # fp16 at MiniCPM's widths: the unrolled fp16 decode matvec for rows of
+    # 2304 and 5760 values, its SwiGLU epilogue, and the tied 122753-row head
+    "wide-minicpm-f16": dict(arch=nc.MINICPM, wdtype=nc.F16, n_vocab=122753, n_embd=2304, n_layers=2, n_heads=36,
+                             n_kv_heads=36, n_ffn=5760, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0005),
     "wide-openelm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=32000, n_embd=2048, n_layers=3,
                             n_heads=[16, 16, 20], n_kv_heads=[4, 4, 5], n_ffn=[1024, 4608, 8192], eos=-1,
                             rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0004),
