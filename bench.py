@@ -67,6 +67,9 @@ FUSED_KERNEL = {"qkv": "k_dmv (qkv, residual add + rms_norm prologue)",
                 "lm_head": "k_dmv_head (lm head in the head layout, residual add + final norm prologue, "
                            "greedy-token epilogue; k_dmv for widths other than 2048 / 2304)"}
 
+FUSED_F16_KERNEL = {"qkv": "k_dmv_f16_ln (q|k|v, residual add + layer_norm prologue)",
+                    "gate_up": "k_dmv_f16_ln<GLU> (gate|up, residual add + layer_norm prologue, SwiGLU epilogue)"}
+
 
 def prompt_tokens(w):
     """The workload prompt (same generator as the tests), computed here
@@ -216,7 +219,11 @@ def kernel_table(ms, nbytes, kind, wdtype):
                        else "k_dmv_f16 (fp16 decode matvec)")
         else:
             unfused = "k_matvec_q"
-        out.append({"role": role, "kernel": FUSED_KERNEL[role] if fused else unfused,
+        if fused and wdtype == nc.F16:
+            kname = FUSED_F16_KERNEL[role]
+        else:
+            kname = FUSED_KERNEL[role] if fused else unfused
+        out.append({"role": role, "kernel": kname,
                     "launches": int(sel.sum()), "total_ms": round(float(ms[sel].sum()), 4),
                     "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(avg_b),
                     "achieved_gbs": round(avg_b / (avg_ms * 1e-3) / 1e9, 1)})

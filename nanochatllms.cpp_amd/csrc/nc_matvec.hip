@@ -30,6 +30,7 @@
 
 #include "nc_kernels.h"
 #include "nc_qdot.h"
+#include "nc_seqsum.h"
 
 namespace nc {
 
@@ -313,52 +314,19 @@ __global__ __launch_bounds__(64) void k_matvec_f16_row(const uint8_t* __restrict
     if (j == 0 && row < N) out[row] = s;
 }
 
-// F16, one activation row (decode), for the group counts G = K / 64 it is
-// built for: the same lane chains as k_matvec_f16_row, fully unrolled over
-// the G groups so that each fold waits for its own loads only.  Weights come
-// through a ring of D loads per thread (the load for group g + D is issued
-// once group g is folded); the activation row is staged in LDS as fp16 in
-// the [G][8 lanes][8] order and read P groups ahead of its fold (the fp16 x
-// fp16 products go through v_fma_mix exactly as through fp32).
-// GLU: w is a fused gate|up [2f, K] weight; workgroup b takes gate rows
-// 4b .. 4b+3 and up rows f+4b .. f+4b+3 and, instead of the fp32 outputs,
-// writes the fp16 SwiGLU values m[4b + i] = Act(Act(silu(Act(g))) * Act(u))
-// as k_silu_mul does them (tinyllama/tinyllama.cpp:88-97 in the fp16 dtype).
-template <int G, int D, int P, bool GLU>
-__global__ __launch_bounds__(64) void k_dmv_f16(const uint8_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                               float* __restrict__ out, int N, uint16_t* __restrict__ m_out)
+// Fold of one wavefront's 64 lane chains (8 rows x 8 lanes, thread (row,
+// lane j) folds lane j's chain over the G 64-column groups in order, as
+// k_matvec_f16_row does), fully unrolled so that each fold waits for its
+// own loads only.  The weights come through the ring wv of D loads per
+// thread (its first D loads issued by the caller; the load for group g + D
+// is issued once group g is folded); the activation row is the fp16 copy xs
+// in LDS in the [G][8 lanes][8] order, read P groups ahead of its fold (the
+// fp16 x fp16 products go through v_fma_mix exactly as through fp32).
+template <int G, int D, int P>
+__device__ __forceinline__ float dmv_f16_fold(const uint16_t* xs, uint4 (&wv)[D], const uint4* wrow, size_t gstride,
+                                              int j)
 {
-    constexpr int K = G * 64, XC = K / 8, XPT = (XC + 63) / 64;
     static_assert(D <= G && P <= G && P <= 15, "ring depths");
-    __shared__ __align__(16) uint16_t xs[K];  // [G][8 lanes][8] halves
-    const int lane = threadIdx.x;
-    const int j = lane & 7, sub = lane >> 3;
-    const int row = GLU ? (sub < 4 ? 4 * (int)blockIdx.x + sub : N / 2 + 4 * (int)blockIdx.x + sub - 4)
-                        : (int)blockIdx.x * 8 + sub;
-    const int rowc = row < N ? row : N - 1;  // rows past N read a valid row and store nothing
-    const size_t gstride = (size_t)((N + 7) & ~7) * 8;  // uint4s per group
-    const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;
-    // the activation row first, then the weight ring, so staging waits for the row only
-    uint4 xv[XPT];
-#pragma unroll
-    for (int i = 0; i < XPT; i++) {
-        const int c = lane + i * 64;  // 8-value chunk: group c >> 3, m = c & 7
-        xv[i] = (XC % 64 == 0 || c < XC) ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0, 0, 0, 0);
-    }
-    uint4 wv[D];
-#pragma unroll
-    for (int i = 0; i < D; i++) wv[i] = load_stream(wrow + (size_t)i * gstride);
-#pragma unroll
-    for (int i = 0; i < XPT; i++) {
-        const int c = lane + i * 64;
-        if (XC % 64 == 0 || c < XC) {
-            const uint32_t q[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-#pragma unroll
-            for (int t = 0; t < 8; t++)
-                xs[((c >> 3) * 8 + t) * 8 + (c & 7)] = (uint16_t)(t & 1 ? q[t >> 1] >> 16 : q[t >> 1] & 0xFFFFu);
-        }
-    }
-    __syncthreads();
     const uint4* xrow = reinterpret_cast<const uint4*>(xs) + j;  // group g at xrow[g * 8]
     uint4 xr[P];
 #pragma unroll
@@ -377,25 +345,170 @@ __global__ __launch_bounds__(64) void k_dmv_f16(const uint8_t* __restrict__ x, c
             const float b = h2f((uint16_t)(m & 1 ? wq[m >> 1] >> 16 : wq[m >> 1] & 0xFFFFu));
             acc = __builtin_fmaf(a, b, acc);  // exact product: same as mul then add
         }
-        // keep the ring order: the reads for g + P and g + D stay ahead of later folds
+        // keep the ring order: this group's adds are done and the reads for
+        // g + P and g + D issued here (otherwise the adds sink below every
+        // read, which then hold all their registers at once)
+        asm volatile("" : "+v"(acc)::"memory");
         __builtin_amdgcn_sched_barrier(0);
     }
-    // lanes 0..7 of the row summed left to right
+    return acc;
+}
+
+// Row of wavefront quad q's lane-row sub (8 rows per wavefront): plain, rows
+// 8q .. 8q+7; GLU (w a fused gate|up [2f, K] weight, N = 2f), gate rows
+// 4q .. 4q+3 and up rows f+4q .. f+4q+3.
+template <bool GLU>
+__device__ __forceinline__ int dmv_f16_row(int q, int sub, int N)
+{
+    return GLU ? (sub < 4 ? 4 * q + sub : N / 2 + 4 * q + sub - 4) : 8 * q + sub;
+}
+
+// Lanes 0..7 of each row summed left to right.  Plain: the fp32 dots to
+// out.  GLU: the fp16 SwiGLU values m[4q + i] = Act(Act(silu(Act(g))) *
+// Act(u)) as k_silu_mul does them (tinyllama/tinyllama.cpp:88-97 in the
+// fp16 dtype).
+template <bool GLU>
+__device__ __forceinline__ void dmv_f16_finish(float acc, int lane, int q, int row, int N, float* out,
+                                               uint16_t* m_out)
+{
     const int base = lane & ~7;
     float s = __shfl(acc, base);
 #pragma unroll
     for (int l = 1; l < 8; l++) s = s + __shfl(acc, base + l);
     if (!GLU) {
-        if (j == 0 && row < N) out[row] = s;
+        if ((lane & 7) == 0 && row < N) out[row] = s;
         return;
     }
     const float gsum = __shfl(s, (lane & 3) * 8), usum = __shfl(s, ((lane & 3) + 4) * 8);
-    if (lane < 4) {
+    if (lane < 4 && 4 * q + lane < N / 2) {
         const float g = f16_roundtrip(gsum);
         const float gs = f16_roundtrip(g / (1.0f + expf_ref(-g)));
         const float u = f16_roundtrip(usum);
-        m_out[4 * blockIdx.x + lane] = f2h(gs * u);
+        m_out[4 * q + lane] = f2h(gs * u);
     }
+}
+
+// F16, one activation row (decode), for the group counts G = K / 64 it is
+// built for: one wavefront per 8 rows (dmv_f16_fold); the row is staged
+// into LDS as fp16 in the fold's order while the weight ring is in flight.
+template <int G, int D, int P, bool GLU>
+__global__ __launch_bounds__(64) void k_dmv_f16(const uint8_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                               float* __restrict__ out, int N, uint16_t* __restrict__ m_out)
+{
+    constexpr int K = G * 64, XC = K / 8, XPT = (XC + 63) / 64;
+    __shared__ __align__(16) uint16_t xs[K];  // [G][8 lanes][8] halves
+    const int lane = threadIdx.x;
+    const int j = lane & 7, q = blockIdx.x;
+    const int row = dmv_f16_row<GLU>(q, lane >> 3, N);
+    const int rowc = row < N ? row : N - 1;  // rows past N read a valid row and store nothing
+    const size_t gstride = (size_t)((N + 7) & ~7) * 8;  // uint4s per group
+    const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;
+    // the activation row first, then the weight ring, so staging waits for the row only
+    uint4 xv[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int c = lane + i * 64;  // 8-value chunk: group c >> 3, m = c & 7
+        xv[i] = (XC % 64 == 0 || c < XC) ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0, 0, 0, 0);
+    }
+    uint4 wv[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) wv[i] = load_stream(wrow + (size_t)i * gstride);
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int c = lane + i * 64;
+        if (XC % 64 == 0 || c < XC) {
+            const uint32_t q4[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                xs[((c >> 3) * 8 + t) * 8 + (c & 7)] = (uint16_t)(t & 1 ? q4[t >> 1] >> 16 : q4[t >> 1] & 0xFFFFu);
+        }
+    }
+    __syncthreads();
+    const float acc = dmv_f16_fold<G, D, P>(xs, wv, wrow, gstride, j);
+    dmv_f16_finish<GLU>(acc, lane, q, row, N, out, m_out);
+}
+
+// Zephyr's layer norm fused into the fp16 decode matvec that consumes it:
+// every workgroup (8 wavefronts, 64 rows) computes the norm of the row
+// itself while its weight loads are in flight, as
+// k_norm<F16, layer norm> does (gten/ops.cpp:669-698): ADD, the residual sum
+// h = a + Act(braw) (stored to h_out by workgroup 0, the Act row the next
+// residual reads); the mean as the sequential sum on wavefront 0, the
+// variance as the exact workgroup sum of the squared deviations, then
+// y = ((x - mean) / (sqrt(var) + 1e-5)) * w + b rounded to fp16 into the
+// fold's LDS order.  Under graph replay (dpos) the a and h_out rows sit at
+// the device-held position.
+constexpr int kLnThreads = 512;
+template <int G, int D, int P, bool ADD, bool GLU>
+__global__ __launch_bounds__(kLnThreads) void k_dmv_f16_ln(
+    const uint8_t* __restrict__ a, int a_pitch, const float* __restrict__ braw, uint8_t* __restrict__ h_out,
+    int h_pitch, const uint16_t* __restrict__ nw, const uint16_t* __restrict__ nb, const uint16_t* __restrict__ w,
+    float* __restrict__ out, uint16_t* __restrict__ m_out, int N, const int* __restrict__ dpos)
+{
+    constexpr int K = G * 64, PER = K / kLnThreads;
+    static_assert(K % kLnThreads == 0 && K % kSsThreads == 0, "row width");
+    __shared__ __align__(16) float buf[K];
+    __shared__ __align__(16) uint16_t xs[K];
+    __shared__ float s_mean;
+    __shared__ SsShared ssh;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int j = lane & 7, q = (int)blockIdx.x * (kLnThreads / kWave) + tid / kWave;
+    const int row = dmv_f16_row<GLU>(q, lane >> 3, N);
+    const int rowc = row < N ? row : N - 1;  // rows past N read a valid row and store nothing
+    const size_t gstride = (size_t)((N + 7) & ~7) * 8;
+    const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;
+    const size_t prow = dpos ? (size_t)dpos[0] : 0;
+    const uint16_t* arow = reinterpret_cast<const uint16_t*>(a + prow * a_pitch);
+    // the row's inputs and the norm's weights first
+    float av[PER], bv[PER], nwv[PER], nbv[PER];
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int e = tid + m * kLnThreads;
+        av[m] = h2f(arow[e]);
+        bv[m] = ADD ? braw[e] : 0.0f;
+        nwv[m] = h2f(nw[e]);
+        nbv[m] = h2f(nb[e]);
+    }
+    float xv[PER];
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int e = tid + m * kLnThreads;
+        float x = av[m];
+        if (ADD) {
+            const float s = x + f16_roundtrip(bv[m]);  // the Linear output as an fp16 Act, then the add
+            x = f16_roundtrip(s);
+            if (blockIdx.x == 0) reinterpret_cast<uint16_t*>(h_out + prow * h_pitch)[e] = f2h(s);
+        }
+        xv[m] = x;
+        buf[e] = x;
+    }
+    __syncthreads();
+    if (tid < kWave) {
+        const float s1 = seq_sum(buf, K);
+        if (tid == 0) s_mean = s1 / (float)K;
+    }
+    // the weight ring: wavefronts 1.. issue theirs while wavefront 0 runs
+    // the mean's chain (a wavefront issuing a large transfer waits at the
+    // issue until the memory system takes it), wavefront 0 after the chain
+    uint4 wv[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) wv[i] = load_stream(wrow + (size_t)i * gstride);
+    __syncthreads();
+    const float mean = s_mean;
+#pragma unroll
+    for (int m = 0; m < PER; m++) buf[tid + m * kLnThreads] = (xv[m] - mean) * (xv[m] - mean);
+    __syncthreads();
+    const float ssq = block_seq_sum_nonneg(buf, K, ssh);
+    const float denom = sqrtf(ssq / (float)K) + 1e-05f;
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int e = tid + m * kLnThreads;
+        const float y = ((xv[m] - mean) / denom) * nwv[m] + nbv[m];
+        xs[((e >> 6) * 8 + (e & 7)) * 8 + ((e >> 3) & 7)] = f2h(y);
+    }
+    __syncthreads();
+    const float acc = dmv_f16_fold<G, D, P>(xs, wv, wrow, gstride, j);
+    dmv_f16_finish<GLU>(acc, lane, q, row, N, out, m_out);
 }
 
 // The group counts k_dmv_f16 is built for (d_model and d_ffn of the fp16
@@ -505,6 +618,36 @@ int matvec_f16_glu(const uint8_t* x, const nc_tensor* w, uint8_t* m_out, hipStre
     };
     dmv_f16_dispatch<true>(K / 64, go);
     return launch_status("k_dmv_f16<GLU>");
+}
+
+bool dmv_f16_ln_supported(const nc_tensor* w, int d, bool glu)
+{
+    return w->dtype == NC_F16 && w->cols == d && d == 2048 && (!glu || w->rows % 8 == 0);
+}
+
+int dmv_f16_ln_launch(const uint8_t* a, int a_pitch, const float* braw, uint8_t* h_out, int h_pitch,
+                      const uint16_t* nw, const uint16_t* nb, const nc_tensor* w, float* out, uint8_t* m_out,
+                      bool glu, hipStream_t st, const int* dpos, hipEvent_t ev_start, hipEvent_t ev_stop)
+{
+    const int N = w->rows, K = w->cols;
+    if (!dmv_f16_ln_supported(w, K, glu))
+        return fail(NC_ERR_ARG, "layer norm + fp16 matvec: [%d x %d] dtype %d", N, K, w->dtype);
+    const int quads = glu ? N / 8 : (N + 7) / 8;  // wavefronts: 8 rows each
+    const dim3 grid((quads + kLnThreads / kWave - 1) / (kLnThreads / kWave));
+    auto go = [&](auto kern) {
+        if (ev_start)
+            hipExtLaunchKernelGGL(kern, grid, dim3(kLnThreads), 0, st, ev_start, ev_stop, 0, a, a_pitch, braw, h_out,
+                                  h_pitch, nw, nb, (const uint16_t*)w->data, out, (uint16_t*)m_out, N, dpos);
+        else
+            hipLaunchKernelGGL(kern, grid, dim3(kLnThreads), 0, st, a, a_pitch, braw, h_out, h_pitch, nw, nb,
+                               (const uint16_t*)w->data, out, (uint16_t*)m_out, N, dpos);
+    };
+    const bool add = braw != nullptr;
+    if (add && glu) go(k_dmv_f16_ln<32, 32, 8, true, true>);
+    else if (add) go(k_dmv_f16_ln<32, 32, 8, true, false>);
+    else if (glu) go(k_dmv_f16_ln<32, 32, 8, false, true>);
+    else go(k_dmv_f16_ln<32, 32, 8, false, false>);
+    return launch_status("k_dmv_f16_ln");
 }
 
 }  // namespace nc

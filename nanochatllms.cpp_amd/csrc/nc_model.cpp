@@ -171,6 +171,36 @@ public:
         return wb + rows * (xb + 4.0 * N);
     }
 
+    // Zephyr decode row: layer norm (after the residual add when braw) fused
+    // into the fp16 matvec that consumes it; glu: the gate|up product with
+    // the SwiGLU epilogue, m row out.
+    int mv_ln(const uint8_t* a, const float* braw, uint8_t* h_out, const uint16_t* nw, const uint16_t* nb,
+              const nc_tensor* w, float* out, uint8_t* m_out, bool glu, int role, const int* dpos)
+    {
+        const int pd = pitch(d);
+        const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
+        int s = timed ? dmv_f16_ln_launch(a, pd, braw, h_out, pd, nw, nb, w, out, m_out, glu, st, dpos,
+                                          prof.ev[prof.used], prof.ev[prof.used + 1])
+                      : dmv_f16_ln_launch(a, pd, braw, h_out, pd, nw, nb, w, out, m_out, glu, st, dpos);
+        if (s) return s;
+        if (timed) {
+            prof.used += 2;
+            prof.bytes.push_back(matvec_bytes(w, 1));
+            prof.kind.push_back(role | NC_PROF_FUSED);
+        }
+        return NC_OK;
+    }
+
+    // The layer norms of Zephyr's single-row steps run inside the q|k|v and
+    // gate|up matvecs (all but the final norm).
+    bool ln_fused(int R) const
+    {
+        if (R != 1 || adt != NC_F16 || norm_kind() != kNormLayer) return false;
+        for (int l = 0; l < cfg.n_layers; l++)
+            if (!dmv_f16_ln_supported(&L[l].qkv, d, false) || !dmv_f16_ln_supported(&L[l].gu, d, true)) return false;
+        return true;
+    }
+
     // fp16 decode row: gate|up product with the SwiGLU epilogue in one
     // launch, fp16 m row out.
     int mv_glu(const uint8_t* x, const nc_tensor* w, uint8_t* m_out)
@@ -731,16 +761,27 @@ public:
         if ((s = embed_launch(&emb, dpos ? tokens : tokens + sp, x0 + off, pd, adt, R, minicpm ? 12.0f : 1.0f, st,
                               dpos)))
             return s;
+        const bool lnf = ln_fused(R);
         // first attention norm on the embeddings
-        if ((s = norm_launch(norm_kind(), adt, false, x0 + off, pd, nullptr, 0, 1.0f, nullptr, 0, L[0].attn_norm,
-                             L[0].attn_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
+        if (!lnf && (s = norm_launch(norm_kind(), adt, false, x0 + off, pd, nullptr, 0, 1.0f, nullptr, 0,
+                                     L[0].attn_norm, L[0].attn_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
             return s;
         const uint8_t* xin = x0;
         for (int l = 0; l < cfg.n_layers; l++) {
             Layer& y = L[l];
             const int pq = pitch(y.qd), pkv = pitch(y.kvd), pf = pitch(y.f);
             const int nqkv = y.qd + 2 * y.kvd;
-            if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv, NC_PROF_QKV))) return s;
+            if (lnf) {
+                // this layer's attention norm; from the second layer on after
+                // the previous layer's residual add (out = h + mlp)
+                const bool first = l == 0;
+                if ((s = mv_ln(first ? x0 + off : L[l - 1].res1 + off, first ? nullptr : down_raw,
+                               first ? nullptr : L[l - 1].res2 + off, y.attn_norm, y.attn_norm_b, &y.qkv, qkv_raw,
+                               nullptr, false, NC_PROF_QKV, dpos)))
+                    return s;
+            } else if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv, NC_PROF_QKV))) {
+                return s;
+            }
             if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, sp, R,
                                      q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
                 return s;
@@ -748,15 +789,21 @@ public:
                                  cfg.max_ctx)))
                 return s;
             if ((s = mv(attn, pq, R, &y.o, o_raw, d, NC_PROF_O))) return s;
-            // h = x + attn (MiniCPM: attn scaled first), then the MLP norm
-            if ((s = norm_launch(norm_kind(), adt, true, xin + off, pd, o_raw, d, bs, y.res1 + off, pd, y.mlp_norm,
-                                 y.mlp_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
-                return s;
-            if (R == 1 && adt == NC_F16 && matvec_f16_glu_supported(&y.gu)) {
-                if ((s = mv_glu(xn, &y.gu, m_act))) return s;
+            // h = x + attn (MiniCPM: attn scaled first), then the MLP norm and gate|up
+            if (lnf) {
+                if ((s = mv_ln(xin + off, o_raw, y.res1 + off, y.mlp_norm, y.mlp_norm_b, &y.gu, nullptr, m_act, true,
+                               NC_PROF_GATE_UP, dpos)))
+                    return s;
             } else {
-                if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f, NC_PROF_GATE_UP))) return s;
-                if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
+                if ((s = norm_launch(norm_kind(), adt, true, xin + off, pd, o_raw, d, bs, y.res1 + off, pd,
+                                     y.mlp_norm, y.mlp_norm_b, xn, pd, d, d, R, 1.0f, st, dpos)))
+                    return s;
+                if (R == 1 && adt == NC_F16 && matvec_f16_glu_supported(&y.gu)) {
+                    if ((s = mv_glu(xn, &y.gu, m_act))) return s;
+                } else {
+                    if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f, NC_PROF_GATE_UP))) return s;
+                    if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
+                }
             }
             if ((s = mv(m_act, pf, R, &y.down, down_raw, d, NC_PROF_DOWN))) return s;
             // out = h + mlp, then the next layer's attention norm (or the final norm)
@@ -764,8 +811,9 @@ public:
             const uint16_t* nw = last ? norm_w : L[l + 1].attn_norm;
             const uint16_t* nb = last ? norm_b : L[l + 1].attn_norm_b;
             const float post = last && minicpm ? 1.0f / 9 : 1.0f;  // minicpm.cpp:104-105
-            if ((s = norm_launch(norm_kind(), adt, true, y.res1 + off, pd, down_raw, d, bs, y.res2 + off, pd, nw, nb,
-                                 xn, pd, d, d, R, post, st, dpos)))
+            // (fused: the next layer's q|k|v launch does this add and norm)
+            if ((!lnf || last) && (s = norm_launch(norm_kind(), adt, true, y.res1 + off, pd, down_raw, d, bs,
+                                                   y.res2 + off, pd, nw, nb, xn, pd, d, d, R, post, st, dpos)))
                 return s;
             xin = y.res2;
         }
