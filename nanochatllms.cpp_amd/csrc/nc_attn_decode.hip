@@ -1,5 +1,5 @@
 // nc_attn_decode.hip -- single-row decode attention with the q/k/v post-
-// processing fused in (Q8 activations).
+// processing fused in (Q8 activations; the fp16 kernel below).
 //
 // One workgroup per query head h (group g = h / (hq / hkv)) does what
 // k_qkv_post + k_attn do for the decode row, with the same arithmetic:
@@ -385,6 +385,287 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         }
         act_store<Q8>(out, h * 64 + j, act_delta_offset(hq * 64), s, true);
     }
+}
+
+// ---- fp16 activations -------------------------------------------------------
+//
+// k_attn_dec's structure for fp16 rows (Zephyr, and the fp16 variants of the
+// other models), with the arithmetic of k_qkv_post<F16> and k_attn<F16>: the
+// Linear outputs rounded to fp16 (+ fp16 bias, rounded: bias_add_inplace,
+// gten/ops.cpp:639-666), OpenELM's QK norm, RoPE, stored as fp16; scores as
+// the fp16 dot (eight fp32 lanes = element mod 8, summed left to right,
+// gten/ops.cpp:208-242), softmax as above with P rounded to fp16, P.V and
+// the output as k_attn_dec.  K rows and q are fp16 pairs (the products go
+// through v_fma_mix, exact like the fp32 products of fp16 values).
+constexpr int kAdVB16 = 128;  // LDS bytes per staged V position: 64 fp16 values
+constexpr int kAdVParts16 = kAdVc * 8 / kAdThreads;
+static_assert(kAdVParts16 >= 1 && kAdVParts16 * kAdThreads == kAdVc * 8, "fp16 V chunk parts");
+
+struct KRow16 {
+    uint4 q[8];
+};
+
+__device__ __forceinline__ KRow16 load_krow16(const uint8_t* kslice, int c, int kv_pitch)
+{
+    KRow16 r;
+    const uint4* p = reinterpret_cast<const uint4*>(kslice + (size_t)c * kv_pitch);
+#pragma unroll
+    for (int v = 0; v < 8; v++) r.q[v] = p[v];
+    return r;
+}
+
+__device__ __forceinline__ float score16(const uint4 (&qv)[8], const KRow16& k, float scale)
+{
+    float a8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int v = 0; v < 8; v++) {
+        const uint32_t wq[4] = {qv[v].x, qv[v].y, qv[v].z, qv[v].w};
+        const uint32_t wk[4] = {k.q[v].x, k.q[v].y, k.q[v].z, k.q[v].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            a8[2 * e] = __builtin_fmaf(h2f((uint16_t)(wq[e] & 0xFFFFu)), h2f((uint16_t)(wk[e] & 0xFFFFu)), a8[2 * e]);
+            a8[2 * e + 1] = __builtin_fmaf(h2f((uint16_t)(wq[e] >> 16)), h2f((uint16_t)(wk[e] >> 16)), a8[2 * e + 1]);
+        }
+    }
+    const float s = a8[0] + a8[1] + a8[2] + a8[3] + a8[4] + a8[5] + a8[6] + a8[7];
+    return s * scale;
+}
+
+struct VChunk16 {
+    uint32_t p[kAdVParts16][4];
+};
+
+// 16-byte parts tid + i kAdThreads of chunk ch (position = part / 8).
+__device__ __forceinline__ void load_vchunk16(VChunk16& v, const uint8_t* vslice, int ch, int kv_pitch, int kv_rows)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kAdVParts16; i++) {
+        const int idx = tid + i * kAdThreads;
+        const int c = min(ch * kAdVc + (idx >> 3), kv_rows - 1);
+        const uint4 t4 = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[idx & 7];
+        v.p[i][0] = t4.x;
+        v.p[i][1] = t4.y;
+        v.p[i][2] = t4.z;
+        v.p[i][3] = t4.w;
+    }
+}
+
+__device__ __forceinline__ void store_vchunk16(const VChunk16& v, uint8_t* buf, int ch, int pos, const uint16_t* s_v)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kAdVParts16; i++) {
+        const int idx = tid + i * kAdThreads;
+        const int cl = idx >> 3, part = idx & 7;
+        uint4 t4 = make_uint4(v.p[i][0], v.p[i][1], v.p[i][2], v.p[i][3]);
+        if (ch * kAdVc + cl == pos) t4 = reinterpret_cast<const uint4*>(s_v)[part];
+        reinterpret_cast<uint4*>(buf + cl * kAdVB16)[part] = t4;
+    }
+}
+
+template <bool BIAS, bool QKNORM, int MK>
+__global__ __launch_bounds__(kAdThreads) void k_attn_dec_f16(
+    const float* __restrict__ raw, int hq, int hkv, const uint16_t* __restrict__ bq, const uint16_t* __restrict__ bk,
+    const uint16_t* __restrict__ bv, const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w,
+    const float2* __restrict__ table, int d_half, int pos_host, const int* __restrict__ dpos, uint8_t* __restrict__ kc,
+    uint8_t* __restrict__ vc, int kv_pitch, uint8_t* __restrict__ out, float scale, int kv_rows)
+{
+    extern __shared__ __align__(16) float sm[];
+    __shared__ __align__(16) uint16_t s_q[64], s_k[64], s_v[64];
+    __shared__ __align__(16) float s_nrm[2][64];
+    __shared__ float red[kAdThreads / kWave];
+    __shared__ float s_sum;
+    __shared__ SsShared ssh;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // heads of one kv group on one XCD, as k_attn_dec
+    const int h = hq % 8 == 0 ? (int)(blockIdx.x % 8) * (hq / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int gs = hq / hkv, g = h / gs;
+    const int col = w == 0 ? h * 64 : (w == 1 ? hq * 64 + g * 64 : hq * 64 + hkv * 64 + g * 64);
+    const float raw_x = w < 3 ? raw[col + lane] : 0.0f;
+    float bias = 0.0f;
+    if (BIAS && w < 3) bias = h2f((w == 0 ? bq + h * 64 : (w == 1 ? bk + g * 64 : bv + g * 64))[lane]);
+    const int pair = lane < d_half ? lane : lane - d_half;
+    const bool rope_lane_in = w < 2 && lane < 2 * d_half;
+    const uint8_t* kslice = kc + g * 128;
+    const uint8_t* vslice = vc + g * 128;
+    VChunk16 vch;
+    load_vchunk16(vch, vslice, 0, kv_pitch, kv_rows);
+    const int pos = dpos ? load_pos(dpos) : pos_host;
+    float2 rp = make_float2(0.0f, 0.0f);
+    if (rope_lane_in) rp = table[(size_t)pos * d_half + pair];
+    __builtin_amdgcn_sched_barrier(0);
+    const int n = pos + 1;
+    const int spad = (kv_rows + kSsThreads - 1) & ~(kSsThreads - 1);
+    float* S = sm;
+    float* acc = S + spad;
+    uint8_t* Vb = reinterpret_cast<uint8_t*>(acc + 512);
+
+    // ---- K rows (positions < pos) into registers
+    KRow16 kr[MK];
+    static_for<0, MK>([&](auto I) {
+        const int c = tid + I * kAdThreads;
+        kr[I] = load_krow16(kslice, c < pos ? c : 0, kv_pitch);
+    });
+
+    // ---- q_h (wave 0), k_g (wave 1), v_g (wave 2) of the new position
+    if (w < 3) {
+        float x = f16_roundtrip(raw_x);  // the Linear output as stored
+        if (BIAS) x = f16_roundtrip(x + bias);
+        if (w < 2) {
+            if (QKNORM) {
+                float* buf = s_nrm[w];
+                buf[lane] = x * x;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+                const float rms = sqrtf(seq_sum(buf, 64) / 64.0f);
+                x = f16_roundtrip(x / (rms + 1e-6f) * h2f((w == 0 ? qn_w : kn_w)[lane]));
+            }
+            x = rope_lane_pair(x, lane, d_half, rp);
+        }
+        const uint16_t hx = f2h(x);
+        uint16_t* st = w == 0 ? s_q : (w == 1 ? s_k : s_v);
+        st[lane] = hx;
+        if (w > 0 && h % gs == 0)
+            reinterpret_cast<uint16_t*>((w == 1 ? kc : vc) + (size_t)pos * kv_pitch)[g * 64 + lane] = hx;
+    }
+    lds_barrier();
+
+    const int nch = (n + kAdVc - 1) / kAdVc;
+    store_vchunk16(vch, Vb, 0, pos, s_v);
+    if (nch > 1) load_vchunk16(vch, vslice, 1, kv_pitch, kv_rows);
+
+    // ---- scores of positions c <= pos (thread = position)
+    {
+        uint4 qv[8];
+#pragma unroll
+        for (int v = 0; v < 8; v++) qv[v] = reinterpret_cast<const uint4*>(s_q)[v];
+        static_for<0, MK>([&](auto I) {
+            const int c = tid + I * kAdThreads;
+            if (c < pos) S[c] = score16(qv, kr[I], scale);
+        });
+        int c = tid + MK * kAdThreads;
+        if (c < pos) {
+            KRow16 cur = load_krow16(kslice, c, kv_pitch);
+            for (;;) {
+                const int cn = c + kAdThreads;
+                KRow16 nxt = cur;
+                if (cn < pos) nxt = load_krow16(kslice, cn, kv_pitch);
+                S[c] = score16(qv, cur, scale);
+                if (cn >= pos) break;
+                cur = nxt;
+                c = cn;
+            }
+        }
+        if (tid == (pos & (kAdThreads - 1))) {
+            KRow16 kk;
+#pragma unroll
+            for (int v = 0; v < 8; v++) kk.q[v] = reinterpret_cast<const uint4*>(s_k)[v];
+            S[pos] = score16(qv, kk, scale);
+        }
+    }
+    lds_barrier();
+
+    // ---- softmax: max (order-free), expf, sequential sum, divide, fp16
+    float mx = -INFINITY;
+    for (int c = tid; c < n; c += kAdThreads) mx = fmaxf(mx, S[c]);
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    lds_barrier();
+    mx = red[0];
+#pragma unroll
+    for (int q = 1; q < kAdThreads / kWave; q++) mx = fmaxf(mx, red[q]);
+    const bool long_row = n > kAdSeqMax;
+    const int npad = (n + kSsThreads - 1) & ~(kSsThreads - 1);
+    for (int c = tid; c < (long_row ? npad : n); c += kAdThreads) S[c] = c < n ? expf_ref(S[c] - mx) : 0.0f;
+    lds_barrier();
+    float sum;
+    if (long_row) {
+        sum = block_seq_sum_nonneg(S, npad, ssh);
+    } else {
+        if (w == 0) {
+            const float ss = seq_sum(S, n);
+            if (lane == 0) s_sum = ss;
+        }
+        lds_barrier();
+        sum = s_sum;
+    }
+    for (int c = tid; c < n; c += kAdThreads) S[c] = f16_roundtrip(S[c] / sum);  // P stored as an fp16 row
+    lds_barrier();
+
+    // ---- P.V: as k_attn_dec, the chain (l, m) over positions l, l + 8, ...
+    const int l = tid >> 6, m = tid & 63;
+    const int n8 = n & ~7;
+    float a0 = 0.0f;
+    for (int ch = 0; ch < nch; ch++) {
+        const uint8_t* B = Vb + (ch & 1) * (kAdVc * kAdVB16);
+        const int c0 = ch * kAdVc;
+        const int cend = min(c0 + kAdVc, n8);
+        auto vone = [&](int c) { return h2f(reinterpret_cast<const uint16_t*>(B + (c - c0) * kAdVB16)[m]); };
+        int c = c0;
+        for (; c + 64 <= cend; c += 64) {
+            float p[8], v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                p[u] = S[c + 8 * u + l];
+                v[u] = vone(c + 8 * u + l);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) a0 = p[u] * v[u] + a0;
+        }
+        for (; c < cend; c += 8) a0 = S[c + l] * vone(c + l) + a0;
+        if (ch + 1 < nch) {
+            store_vchunk16(vch, Vb + ((ch + 1) & 1) * (kAdVc * kAdVB16), ch + 1, pos, s_v);
+            if (ch + 2 < nch) load_vchunk16(vch, vslice, ch + 2, kv_pitch, kv_rows);
+        }
+        lds_barrier();
+    }
+    acc[l * 64 + m] = a0;
+    lds_barrier();
+    if (w == 0) {
+        const int j = lane;
+        float s = acc[j];
+#pragma unroll
+        for (int q = 1; q < 8; q++) s = s + acc[q * 64 + j];
+        const uint8_t* B = Vb + ((nch - 1) & 1) * (kAdVc * kAdVB16);
+        const int c0 = (nch - 1) * kAdVc;
+        for (int c = n8; c < n; c++) s = s + S[c] * h2f(reinterpret_cast<const uint16_t*>(B + (c - c0) * kAdVB16)[j]);
+        reinterpret_cast<uint16_t*>(out)[h * 64 + j] = f2h(s);
+    }
+}
+
+int attn_decode_f16_launch(const float* raw, int hq, int hkv, const uint16_t* bq, const uint16_t* bk,
+                           const uint16_t* bv, const uint16_t* qn_w, const uint16_t* kn_w, const float* table,
+                           int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc, int kv_pitch, uint8_t* out,
+                           int max_ctx, hipStream_t st)
+{
+    if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "attention: %d query heads over %d kv heads", hq, hkv);
+    if (max_ctx <= 0 || max_ctx > kAttnMaxCtx)
+        return fail(NC_ERR_ARG, "attention: context %d (at most %d positions)", max_ctx, kAttnMaxCtx);
+    if (!dpos && (pos < 0 || pos >= max_ctx)) return fail(NC_ERR_ARG, "attention: position %d of %d", pos, max_ctx);
+    if ((bq != nullptr) != (bk != nullptr) || (bq != nullptr) != (bv != nullptr))
+        return fail(NC_ERR_ARG, "attention: q, k and v biases come together");
+    const size_t spad = ((size_t)max_ctx + kSsThreads - 1) & ~(size_t)(kSsThreads - 1);
+    const size_t lds = (spad + 512) * 4 + 2 * (size_t)kAdVc * kAdVB16;
+    const float scale = 1.0f / sqrtf(64.0f);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, bq, bk, bv, qn_w, kn_w,
+                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale, max_ctx);
+    };
+    auto by_ctx = [&](auto bias, auto qk) {
+        constexpr bool B = decltype(bias)::value, QK = decltype(qk)::value;
+        if (max_ctx <= kAdThreads) go(k_attn_dec_f16<B, QK, 1>);
+        else go(k_attn_dec_f16<B, QK, kAdMaxK>);
+    };
+    if (bq) {
+        if (qn_w) by_ctx(std::true_type{}, std::true_type{});
+        else by_ctx(std::true_type{}, std::false_type{});
+    } else {
+        if (qn_w) by_ctx(std::false_type{}, std::true_type{});
+        else by_ctx(std::false_type{}, std::false_type{});
+    }
+    return launch_status("k_attn_dec_f16");
 }
 
 // Shared memory of k_attn_dec for a cache of max_ctx rows.

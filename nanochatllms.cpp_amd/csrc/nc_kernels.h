@@ -109,5 +109,12 @@ bool attn_decode_supported(int hq, int hkv, int max_ctx);
 int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
                        const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
                        int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur = nullptr);
+// The same for fp16 rows, with optional q / k / v biases (bias_add_inplace
+// after the Linear outputs) and the RoPE pair read from the table at the
+// (device-held) position.
+int attn_decode_f16_launch(const float* raw, int hq, int hkv, const uint16_t* bq, const uint16_t* bk,
+                           const uint16_t* bv, const uint16_t* qn_w, const uint16_t* kn_w, const float* table,
+                           int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc, int kv_pitch, uint8_t* out,
+                           int max_ctx, hipStream_t st);
 
 }  // namespace nc

@@ -782,12 +782,19 @@ public:
             } else if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv, NC_PROF_QKV))) {
                 return s;
             }
-            if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, sp, R,
-                                     q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
-                return s;
-            if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, sp, n, st, dpos,
-                                 cfg.max_ctx)))
-                return s;
+            if (R == 1 && adt == NC_F16 && attn_decode_supported(y.hq, y.hkv, cfg.max_ctx)) {
+                // fp16 decode row: q/k/v post-processing and attention in one launch
+                if ((s = attn_decode_f16_launch(qkv_raw, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, sp,
+                                                dpos, y.kc, y.vc, pkv, attn, cfg.max_ctx, st)))
+                    return s;
+            } else {
+                if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half,
+                                         sp, R, q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
+                    return s;
+                if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, sp, n, st, dpos,
+                                     cfg.max_ctx)))
+                    return s;
+            }
             if ((s = mv(attn, pq, R, &y.o, o_raw, d, NC_PROF_O))) return s;
             // h = x + attn (MiniCPM: attn scaled first), then the MLP norm and gate|up
             if (lnf) {
