@@ -88,14 +88,17 @@ constexpr int kSsThreads = 256;   // workgroup size the block sum is written for
 constexpr int kSsMaxPer = 16;     // terms per thread: n <= 4096
 constexpr int kSsMaxCross = 63;   // crossings handled before the fallback
 constexpr int kSsMaxRec = 4;      // crossings one thread's chunk may hold before the fallback
+constexpr int kSsHead = 8;        // chunks in the head
 
 struct SsShared {
+    // the wave arrays are read as one 16-byte vector each: keep them first
     float wf[kSsThreads / kWave];
     int wc0[kSsThreads / kWave], wc1[kSsThreads / kWave], wfl[kSsThreads / kWave], wcnt[kSsThreads / kWave];
     int4 rec[kSsMaxCross + 1];  // crossing records: map (c0, c1), binade (0: no check), term bits
     int m;
     int ok;
     float result;
+    float head;  // the exact sum of the head chunks
 };
 
 // Segmented scan element: a parity map and flags (bit 0: nz, bit 1: the
@@ -150,10 +153,11 @@ __device__ __forceinline__ SsSeg wave_scan_seg(SsSeg x)
 // 0's view) tells whether the parallel path was taken.  Synchronizes the
 // workgroup through LDS barriers only (global loads may stay in flight).
 //
-// Thread j owns terms [j c, j c + c).  Thread 0 adds its chunk directly
-// (the exact start of everything after it, and the region where the running
-// sum crosses binades most often); every other thread walks its chunk once,
-// branch-free: binade predicted from an approximate prefix, step maps
+// Thread j owns the j-th chunk of c terms.  The first kSsHead chunks (the
+// region where the running sum crosses binades most often) form the head:
+// their threads only feed the prediction, and the last thread adds the head
+// exactly (the start of everything after it).  Every later thread walks its
+// chunk once: binade predicted from an approximate prefix, step maps
 // composed, and up to four crossings recorded (more fall back).  A segmented
 // scan joins the chunks, and wave 0 replays the few records in order.
 template <int C>
@@ -175,6 +179,7 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
     const int c = C ? C : n / kSsThreads;
     const int i0 = tid * c;
+    const int nh = kSsHead * c;  // head terms
     float v[kSsMaxPer];
     if (c % 4 == 0) {
 #pragma unroll
@@ -192,8 +197,7 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
         for (int k = 0; k < kSsMaxPer; k++)
             if (k < c) v[k] = t[i0 + k];
     }
-    // chunk sum in order: for thread 0 this is the exact running sum after
-    // its chunk
+    // chunk sum in order (a prediction only)
     float cs = 0.0f;
 #pragma unroll
     for (int k = 0; k < kSsMaxPer; k++)
@@ -208,7 +212,14 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
     if (lane == kWave - 1) sh.wf[w] = I;
     lds_barrier();
     float WP = 0.0f;
-    for (int q = 0; q < w; q++) WP = WP + sh.wf[q];
+    {
+        const float4 F = *reinterpret_cast<const float4*>(sh.wf);  // every wave's total at once
+        const float f[4] = {F.x, F.y, F.z, F.w};
+        static_assert(kSsThreads / kWave == 4, "four wave totals");
+#pragma unroll
+        for (int q = 0; q < 3; q++)
+            if (q < w) WP = WP + f[q];
+    }
     I = I + WP;
     float A = dpp_f<kDppWaveShr1>(I);  // the previous lane's I
     if (lane == 0) A = WP;
@@ -222,7 +233,7 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
     int4 rec[kSsMaxRec];  // (c0, c1, binade or 0, term bits) of this chunk's crossings
 #pragma unroll
     for (int q = 0; q < kSsMaxRec; q++) rec[q] = make_int4(0, 0, 0, 0);
-    if (tid > 0) {
+    if (tid >= kSsHead) {
         float P = A;
         int Eb = ss_binade(A);
         float top = ss_top(Eb);
@@ -272,6 +283,8 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
         c1 = __builtin_bit_cast(int, r1) - (b0 | 1);
         nz = nzb ? 1 : 0;
     }
+    // the head's exact sum, by the last thread (after its own chunk)
+    if (tid == kSsThreads - 1) sh.head = seq_sum(t, nh);
     // ---- segmented scan of (open map, has-crossing) and scan of the counts
     SsSeg x{c0, c1, nz | (ncross > 0 ? 2 : 0), ncross};
     x = wave_scan_seg(x);
@@ -286,9 +299,18 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
     }
     lds_barrier();
     SsSeg pre{0, 0, 0, 0};
-    int any_over = 0;
-    for (int q = 0; q < w; q++) pre = ss_seg(pre, SsSeg{sh.wc0[q], sh.wc1[q], sh.wfl[q], sh.wcnt[q] & 0xFFFF});
-    for (int q = 0; q < kSsThreads / kWave; q++) any_over |= sh.wcnt[q] >> 30;
+    int any_over;
+    {
+        // every wave's scan total at once, then the earlier waves' composed in order
+        const int4 W0 = *reinterpret_cast<const int4*>(sh.wc0), W1 = *reinterpret_cast<const int4*>(sh.wc1);
+        const int4 WF = *reinterpret_cast<const int4*>(sh.wfl), WN = *reinterpret_cast<const int4*>(sh.wcnt);
+        const int a0[4] = {W0.x, W0.y, W0.z, W0.w}, a1[4] = {W1.x, W1.y, W1.z, W1.w};
+        const int af[4] = {WF.x, WF.y, WF.z, WF.w}, an[4] = {WN.x, WN.y, WN.z, WN.w};
+#pragma unroll
+        for (int q = 0; q < 3; q++)
+            if (q < w) pre = ss_seg(pre, SsSeg{a0[q], a1[q], af[q], an[q] & 0xFFFF});
+        any_over = (an[0] | an[1] | an[2] | an[3]) >> 30;
+    }
     x = ss_seg(pre, x);
     const int cnt = x.n;
     // the open segment entering this chunk, and the crossings before it
@@ -324,7 +346,7 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
         // holds record r; the chain reads them with readlane, in vector
         // registers (the empty asm marks the state lane-varying, so it does
         // not bounce through scalar registers).
-        int sb = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs));
+        int sb = __builtin_bit_cast(int, sh.head);
         if (ok) {
             const int4 R = lane <= mm ? sh.rec[lane] : make_int4(0, 0, 0, 0);
             int okl = R.z == 0 || R.z < 255;
