@@ -352,9 +352,9 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
             int okl = R.z == 0 || R.z < 255;
             asm volatile("" : "+v"(sb));
             int sbl = 0, nbl = 0;  // the chain's value entering / leaving record `lane` (for the checks)
-            for (int r0 = 0; r0 <= mm; r0 += 4) {
+            for (int r0 = 0; r0 <= mm; r0 += 2) {
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
+                for (int k = 0; k < 2; k++) {
                     // past the last record: lane 63, which holds the identity
                     // (mm < kSsMaxCross = 63); readlane indices stay below 64
                     const int r = min(r0 + k, kWave - 1);
