@@ -227,12 +227,130 @@ __global__ __launch_bounds__(kMvThreads) void k_matvec_f16_tile(const uint8_t* _
     }
 }
 
+// F16, prefill (several activation rows): the lane chains of
+// k_matvec_f16_row with register tiles.  A 256-thread workgroup owns 32 R
+// weight rows and P activation rows; thread (row group rr, lane j) runs lane
+// j's chain for its R weight rows and the P activation rows (R x P chains),
+// over the 64-column groups in order.  Per chunk of GC groups it holds the
+// R weight rows' lane-j values in registers (the next chunk's requested
+// before this one is folded) and reads the P rows' lane-j values of each
+// group from LDS (fp32, staged per chunk, double-buffered): R P 8 fused
+// multiply-adds per 2 P LDS reads.  The products of two fp16 values are
+// exact in fp32, so each fused multiply-add is the reference's multiply
+// then add.  Workgroups of one weight block sit on one XCD when the grid's
+// x extent is a multiple of 8.
+template <int R, int P, int GC>
+__global__ __launch_bounds__(256) void k_mm_f16(const uint8_t* __restrict__ x, int x_pitch, int n_xrows,
+                                              const uint16_t* __restrict__ w, float* __restrict__ out, int out_pitch,
+                                              int N, int K)
+{
+    static_assert(P * GC * 8 <= 256, "one staged chunk per thread at most");
+    __shared__ __align__(16) float xs[2][P][GC][8][8];  // [buffer][row][group][lane j][m]
+    const int tid = threadIdx.x, j = tid & 7, rr = tid >> 3;
+    const int G = K / 64, nck = (G + GC - 1) / GC;
+    const size_t gstride = (size_t)((N + 7) & ~7) * 8;  // uint4s per group
+    const int wr0 = (int)blockIdx.x * (32 * R) + rr * R;
+    const int p0 = (int)blockIdx.y * P;
+    const uint4* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int rowc = min(wr0 + r, N - 1);  // rows past N read a valid row and store nothing
+        wrow[r] = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;
+    }
+    // staging: thread q < P GC 8 converts the 8 values of (row q / (8 GC),
+    // group (q / 8) % GC, m = q % 8) of a chunk
+    auto stage = [&](int ck, int buf) {
+        if (tid < P * GC * 8) {
+            const int p = tid / (GC * 8), gl = (tid >> 3) % GC, m = tid & 7;
+            const int g = ck * GC + gl;
+            float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (p0 + p < n_xrows && g < G) {
+                const uint4 u =
+                    *reinterpret_cast<const uint4*>(x + (size_t)(p0 + p) * x_pitch + ((size_t)g * 64 + 8 * m) * 2);
+                const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int t = 0; t < 8; t++) v[t] = h2f((uint16_t)(t & 1 ? h[t >> 1] >> 16 : h[t >> 1] & 0xFFFFu));
+            }
+#pragma unroll
+            for (int t = 0; t < 8; t++) xs[buf][p][gl][t][m] = v[t];
+        }
+    };
+    auto wload = [&](int ck, uint4 (&dst)[GC][R]) {
+#pragma unroll
+        for (int gl = 0; gl < GC; gl++) {
+            const int g = min(ck * GC + gl, G - 1);
+#pragma unroll
+            for (int r = 0; r < R; r++) dst[gl][r] = load_stream(wrow[r] + (size_t)g * gstride);
+        }
+    };
+    float acc[R][P];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int p = 0; p < P; p++) acc[r][p] = 0.0f;
+    auto fold = [&](int ck, int buf, const uint4 (&wv)[GC][R]) {
+#pragma unroll
+        for (int gl = 0; gl < GC; gl++) {
+            if (ck * GC + gl >= G) break;  // uniform
+            float wf[R][8];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t q[4] = {wv[gl][r].x, wv[gl][r].y, wv[gl][r].z, wv[gl][r].w};
+#pragma unroll
+                for (int m = 0; m < 8; m++) wf[r][m] = h2f((uint16_t)(m & 1 ? q[m >> 1] >> 16 : q[m >> 1] & 0xFFFFu));
+            }
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                const float4 xa = *reinterpret_cast<const float4*>(&xs[buf][p][gl][j][0]);
+                const float4 xb = *reinterpret_cast<const float4*>(&xs[buf][p][gl][j][4]);
+                const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                for (int m = 0; m < 8; m++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) acc[r][p] = __builtin_fmaf(xv[m], wf[r][m], acc[r][p]);
+            }
+        }
+    };
+    uint4 wa[GC][R], wb[GC][R];
+    wload(0, wa);
+    stage(0, 0);
+    __syncthreads();
+    // chunks in pairs, so the two weight sets keep compile-time names
+    for (int ck = 0; ck < nck; ck += 2) {
+        if (ck + 1 < nck) {
+            wload(ck + 1, wb);
+            stage(ck + 1, 1);
+        }
+        fold(ck, 0, wa);
+        __syncthreads();
+        if (ck + 1 >= nck) break;  // uniform
+        if (ck + 2 < nck) {
+            wload(ck + 2, wa);
+            stage(ck + 2, 0);
+        }
+        fold(ck + 1, 1, wb);
+        __syncthreads();
+    }
+    // lanes 0..7 of each (weight row, activation row) summed left to right
+    const int base = tid & ~7;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            float s = __shfl(acc[r][p], base);
+#pragma unroll
+            for (int l = 1; l < 8; l++) s = s + __shfl(acc[r][p], base + l);
+            if (j == 0 && wr0 + r < N && p0 + p < n_xrows) out[(size_t)(p0 + p) * out_pitch + wr0 + r] = s;
+        }
+}
+
 // F16, one activation row (decode): a 64-thread workgroup owns 8 rows, thread
 // (row, lane j) folds lane j's chain over the 64-column groups in order
 // exactly as k_matvec_f16 does, but keeps two batches of kF16Batch weight
 // runs in flight (the next batch is requested before the current one is
 // folded), so the fold is not serialised behind one load per group.
 constexpr int kF16Batch = 16;
+constexpr int kMmF16Rows = 8;  // activation rows per k_mm_f16 workgroup; matvec_raw takes it from this many rows
 
 __global__ __launch_bounds__(64) void k_matvec_f16_row(const uint8_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                       float* __restrict__ out, int N, int K)
@@ -581,6 +699,18 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
                 hipLaunchKernelGGL(k_matvec_f16_row, dim3((N + 7) / 8), dim3(64), lds, st, x, (const uint16_t*)w->data,
                                    out, N, K);
             return launch_status("k_matvec_f16_row");
+        }
+        if (n_rows >= kMmF16Rows) {
+            // 64 weight rows x 8 activation rows per workgroup (measured best of R x P x GC
+            // in {1, 2, 4, 8} x {4, 8, 16} x {1, 2, 4} on Zephyr's 128-row prefill)
+            const dim3 grid2((N + 63) / 64, (n_rows + kMmF16Rows - 1) / kMmF16Rows);
+            if (ev_start)
+                hipExtLaunchKernelGGL((k_mm_f16<2, kMmF16Rows, 2>), grid2, dim3(256), 0, st, ev_start, ev_stop, 0, x,
+                                      x_pitch, n_rows, (const uint16_t*)w->data, out, out_pitch, N, K);
+            else
+                hipLaunchKernelGGL((k_mm_f16<2, kMmF16Rows, 2>), grid2, dim3(256), 0, st, x, x_pitch, n_rows,
+                                   (const uint16_t*)w->data, out, out_pitch, N, K);
+            return launch_status("k_mm_f16");
         }
         const dim3 grid((N + 31) / 32);
         if (n_rows >= 4) {

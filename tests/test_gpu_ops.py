@@ -65,6 +65,10 @@ MATMUL_CASES = [
     (F16, F16, 5760, 2304, 1, 0),
     (F16, F16, 2048, 100, 1, 0),
     (F16, F16, 1280, 96, 1, 0),
+    (F16, F16, 2048, 2048, 64, 0),
+    (F16, F16, 5632, 2048, 16, 3),
+    (F16, F16, 2048, 300, 13, 0),
+    (F16, F16, 256, 768, 9, 1),
 ]
 
 
