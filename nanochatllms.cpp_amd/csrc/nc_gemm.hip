@@ -23,7 +23,9 @@
 //
 // Three quarters of each activation operand are zeros: the matrix cores do
 // four times the necessary integer work, which is cheap next to the
-// vector-unit fold (13 fp32 operations per output and block).
+// vector-unit fold (13 fp32 operations per output and block).  k_gemm_qh
+// (below) takes the same lane sums on the fp16 matrix cores and reads the
+// weights' chunk-major copy when the caller has one.
 #include <hip/hip_ext.h>
 
 #include <type_traits>
@@ -230,49 +232,370 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same products with the lane sums taken on the fp16 matrix cores
+// (v_mfma_f32_16x16x32_f16): codes enter as fp16 integers (activation codes
+// -127..127, Q4 weights code - 7 in -7..8, Q8 weights -127..127), so each
+// product is an integer below 2^14 and each lane sum of eight products an
+// integer below 2^17.  Every partial sum the matrix core forms is then an
+// integer exactly representable in fp32, and the fp32 result is exactly
+// float(L_k): the conversion the integer path needs per lane and block is
+// gone, and the fold is 9 fp32 operations per (row, column, block) instead
+// of 13.
+//
+// The activation operand is staged once per workgroup already expanded: for
+// block j and row group m, lane l = (4r + k) + 16 g holds row 4m + r's lane-k
+// codes as fp16 when g == k, and zeros otherwise (the zero entries are written
+// once at kernel start and never touched again).  A lane reads its 16 bytes
+// with one LDS load; rows of a group share them across the NW wavefronts.
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// Four bytes b0..b3 of `u` (each below 256) as fp16 1024 + b, two per dword:
+// [b0, b1] and [b2, b3] (v_perm_b32 with the exponent byte 0x64 from a
+// constant), then plus `bias` (fp16, both halves): exact integers.
+__device__ __forceinline__ void bytes_to_h(uint32_t u, uint32_t bias2, uint32_t& lo, uint32_t& hi)
+{
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2_t bb = __builtin_bit_cast(h2_t, bias2);
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, a) + bb);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, b) + bb);
+}
+constexpr uint32_t kHm1152 = 0xE480E480u;  // fp16 -1152, twice: (1024 + c + 128) - 1152 = c
+constexpr uint32_t kHm1031 = 0xE407E407u;  // fp16 -1031, twice: (1024 + n) - 1031 = n - 7
+
+// Four signed int8 codes -> four fp16 values (two dwords).
+__device__ __forceinline__ void s8x4_to_h(uint32_t v, uint32_t& lo, uint32_t& hi)
+{
+    bytes_to_h(v ^ 0x80808080u, kHm1152, lo, hi);
+}
+
+// NW wavefronts per workgroup share the staged activation blocks of 4 MR
+// rows and own 16 weight columns each; a chunk is CH blocks (one LDS barrier
+// per chunk), and PF chunks of weights and activation blocks are in flight.
+// Within a chunk the MFMAs of block j + 1 are issued before the folds of
+// block j, so no fold waits on the MFMA just issued.  CL: the weights are
+// read from their chunk-major copy (k_chunk_layout), where a wavefront's
+// codes of four blocks are one contiguous 1 KB (Q4) and a thread's are one
+// 16-byte load, instead of four 4-byte loads from 16 rows each.
+template <int WT, int MR, int NW, int CH, int PF, bool CL>
+__global__ __launch_bounds__(64 * NW) void k_gemm_qh(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
+                                                       const uint32_t* __restrict__ wq,
+                                                       const uint16_t* __restrict__ wd, float* __restrict__ out,
+                                                       int out_pitch, int N, int nb)
+{
+    constexpr int WV = WT == Q4 ? 1 : 2;  // code dwords of one lane of a weight block
+    constexpr int WD = WT == Q4 ? 4 : 8;  // code dwords per weight block
+    constexpr int kRows = 4 * MR;         // rows per workgroup
+    constexpr int kThreads = 64 * NW;
+    static_assert(CH == 4 || CH == 8, "chunk of 4 or 8 blocks (one 8- or 16-byte delta load)");
+    // expanded activation operands [buffer][block][row group][lane] and the
+    // rows' deltas [buffer][block][row]
+    __shared__ __align__(16) uint4 xa[2][CH][MR][64];
+    __shared__ float xd[2][CH][kRows];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int lc = lane & 15, lg = lane >> 4;
+    const int r0 = blockIdx.y * kRows;
+    const int col = min(blockIdx.x * 16 * NW + wv * 16 + lc, N - 1);  // this thread's weight column
+    const int nch = nb / CH;
+
+    // zero entries: lane l = lc + 16 lg with lg != lc % 4, never staged
+    for (int e = tid; e < 2 * CH * MR * 64; e += kThreads)
+        if (((e & 15) & 3) != ((e >> 4) & 3)) (&xa[0][0][0][0])[e] = make_uint4(0, 0, 0, 0);
+
+    // staging: thread t < CH kRows stages (row t % kRows, block t / kRows)
+    // of each chunk; rows past the end repeat the last row (their outputs
+    // are not stored); other threads stage nothing
+    constexpr int kStagers = kRows * CH;
+    static_assert(kStagers <= kThreads, "every staged (row, block) needs its own thread");
+    const bool stager = tid < kStagers;
+    const int srow = tid % kRows, sblk = (tid / kRows) % CH;
+    const uint8_t* xrow = x + (size_t)min(r0 + srow, n_rows - 1) * x_pitch;
+    auto stage = [&](const XRaw& q, int buf) {
+        const uint32_t X[8] = {q.a.x, q.a.y, q.a.z, q.a.w, q.b.x, q.b.y, q.b.z, q.b.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t a = pick_pair(X[k >> 1], X[2 + (k >> 1)], k & 1);
+            const uint32_t b = pick_pair(X[4 + (k >> 1)], X[6 + (k >> 1)], k & 1);
+            uint4 h;
+            s8x4_to_h(a, h.x, h.y);
+            s8x4_to_h(b, h.z, h.w);
+            xa[buf][sblk][srow >> 2][(srow & 3) * 4 + k + 16 * k] = h;
+        }
+        xd[buf][sblk][srow] = h2f(q.d16);
+    };
+    auto x_load = [&](int ch) {
+        XRaw q{};
+        if (stager) q = load_x_block(xrow, nb, min(ch, nch - 1) * CH + sblk);
+        return q;
+    };
+
+    const uint32_t* wcol = wq + (size_t)col * nb * WD + WV * lg;
+    const uint16_t* dcol = wd + (size_t)col * nb;
+    struct WChunk {
+        uint32_t c[CH][WV];
+        uint32_t d[CH / 2];  // the chunk's fp16 deltas, two per dword
+    };
+    auto w_load = [&](int ch, WChunk& w) {
+        const int b0 = min(ch, nch - 1) * CH;
+        if constexpr (CL) {
+            // codes [nb/4][N][4 lanes][4 blocks x WV dwords], deltas [nb/4][N][4]
+#pragma unroll
+            for (int h = 0; h < CH / 4; h++) {
+                const size_t c4 = (size_t)(b0 / 4 + h) * N + col;
+                const uint4* src = reinterpret_cast<const uint4*>(wq + (c4 * 4 + lg) * 4 * WV);
+#pragma unroll
+                for (int q = 0; q < WV; q++) {
+                    const uint4 t = src[q];
+                    const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) w.c[4 * h + (4 * q + e) / WV][(4 * q + e) % WV] = tv[e];
+                }
+                const uint2 d = *reinterpret_cast<const uint2*>(wd + c4 * 4);
+                w.d[2 * h] = d.x;
+                w.d[2 * h + 1] = d.y;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CH; j++)
+#pragma unroll
+                for (int v = 0; v < WV; v++) w.c[j][v] = wcol[(size_t)(b0 + j) * WD + v];
+            if constexpr (CH == 4) {
+                const uint2 d = *reinterpret_cast<const uint2*>(dcol + b0);
+                w.d[0] = d.x;
+                w.d[1] = d.y;
+            } else {
+                const uint4 d = *reinterpret_cast<const uint4*>(dcol + b0);
+                w.d[0] = d.x;
+                w.d[1] = d.y;
+                w.d[2] = d.z;
+                w.d[3] = d.w;
+            }
+        }
+    };
+
+    float acc[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[m][k] = 0.0f;
+
+    // one block's B operand (fp16 codes) and delta
+    auto b_operand = [&](const WChunk& w, int j, h8_t& Bh, float& dw) {
+        uint4 B;
+        if (WT == Q4) {
+            // high nibbles pair with the lane's codes {2k,2k+1,2k+8,2k+9},
+            // low nibbles with those + 16
+            const uint32_t P = w.c[j][0];
+            bytes_to_h((P >> 4) & 0x0F0F0F0Fu, kHm1031, B.x, B.y);
+            bytes_to_h(P & 0x0F0F0F0Fu, kHm1031, B.z, B.w);
+        } else {
+            s8x4_to_h(w.c[j][0], B.x, B.y);
+            s8x4_to_h(w.c[j][1], B.z, B.w);
+        }
+        Bh = __builtin_bit_cast(h8_t, B);
+        dw = h2f((uint16_t)(w.d[j >> 1] >> (16 * (j & 1))));
+    };
+
+    // weights and activation blocks in a ring of PF chunks (requested PF
+    // chunks ahead, every request issued so the waits are exact counts)
+    WChunk wr[PF];
+    XRaw xq[PF];
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+        w_load(p, wr[p]);
+        xq[p] = x_load(p);
+    }
+    if (stager) stage(xq[0], 0);
+    lds_barrier();
+    for (int cb = 0; cb < nch; cb += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int ch = cb + p;
+            if (ch >= nch) break;  // uniform
+            const int buf = ch & 1;
+            // the chunk's activation operands and row deltas, read at once
+            // (one LDS wait per chunk)
+            uint4 Ar[CH][MR];
+            float dxr[CH][MR];
+#pragma unroll
+            for (int j = 0; j < CH; j++)
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    Ar[j][m] = xa[buf][j][m][lane];
+                    dxr[j][m] = xd[buf][j][4 * m + lg];
+                }
+            f4_t L[2][MR];
+            float dw[2];
+            {
+                h8_t Bh;
+                b_operand(wr[p], 0, Bh, dw[0]);
+#pragma unroll
+                for (int m = 0; m < MR; m++)
+                    L[0][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, Ar[0][m]), Bh,
+                                                                      f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < CH; j++) {
+                const int cur = j & 1;
+                if (j + 1 < CH) {
+                    h8_t Bh;
+                    b_operand(wr[p], j + 1, Bh, dw[cur ^ 1]);
+#pragma unroll
+                    for (int m = 0; m < MR; m++)
+                        L[cur ^ 1][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(h8_t, Ar[j + 1][m]), Bh, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                }
+                // block j's folds in block order: row 4m + lg, lane sums k
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const float dd = dxr[j][m] * dw[cur];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[m][k] = acc[m][k] + L[cur][m][k] * dd;
+                }
+            }
+            w_load(ch + PF, wr[p]);
+            xq[p] = x_load(ch + PF);
+            if (ch + 1 < nch && stager) stage(xq[(p + 1) % PF], buf ^ 1);
+            lds_barrier();
+        }
+    }
+    const int oc = blockIdx.x * 16 * NW + wv * 16 + lc;
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        const int row = r0 + 4 * m + lg;
+        if (row < n_rows && oc < N)
+            out[(size_t)row * out_pitch + oc] = (acc[m][0] + acc[m][1]) + (acc[m][2] + acc[m][3]);
+    }
+}
+
+// The chunk-major copy of a Q4 / Q8 weight [N, K] (K % 128 == 0) that the
+// prefill matmul reads: codes [K/128][N][4 lanes][4 blocks][WV dwords] --
+// for each group of four blocks, each row's lane-k code dwords of the four
+// blocks side by side -- and deltas [K/128][N][4].
+template <int WT>
+__global__ void k_chunk_layout(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ wd, int N, int nb,
+                               uint32_t* __restrict__ cq, uint16_t* __restrict__ cd)
+{
+    constexpr int WV = WT == Q4 ? 1 : 2, WD = WV * 4;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one (row, block) each
+    if (t >= (int64_t)N * nb) return;
+    const int n = (int)(t / nb), b = (int)(t - (int64_t)n * nb);
+    const size_t c4 = (size_t)(b >> 2) * N + n;
+    const uint32_t* src = wq + t * WD;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int v = 0; v < WV; v++) cq[((c4 * 4 + k) * 4 + (b & 3)) * WV + v] = src[WV * k + v];
+    cd[c4 * 4 + (b & 3)] = wd[t];
+}
+
+bool chunk_layout_supported(const nc_tensor* w)
+{
+    return (w->dtype == NC_Q4 || w->dtype == NC_Q8) && w->cols > 0 && w->cols % 128 == 0 && w->rows > 0;
+}
+
+int chunk_layout_launch(const nc_tensor* w, void* codes, void* deltas, hipStream_t st)
+{
+    if (!chunk_layout_supported(w)) return fail(NC_ERR_ARG, "chunk layout: [%d x %d] dtype %d", w->rows, w->cols, w->dtype);
+    const int nb = w->cols / 32;
+    const int64_t n = (int64_t)w->rows * nb;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (w->dtype == NC_Q4)
+        hipLaunchKernelGGL(k_chunk_layout<Q4>, grid, dim3(256), 0, st, (const uint32_t*)w->data,
+                           (const uint16_t*)w->deltas, w->rows, nb, (uint32_t*)codes, (uint16_t*)deltas);
+    else
+        hipLaunchKernelGGL(k_chunk_layout<Q8>, grid, dim3(256), 0, st, (const uint32_t*)w->data,
+                           (const uint16_t*)w->deltas, w->rows, nb, (uint32_t*)codes, (uint16_t*)deltas);
+    return launch_status("k_chunk_layout");
+}
+
 // Workgroup shapes, measured on MI355X with Q4 weights (us per launch,
-// exact results in every shape): NG 16-wide column groups per wavefront,
-// NW wavefronts per workgroup sharing one staging of 4 MR rows, PF weight
-// chunks in flight, MF MFMAs first.
+// exact results in every shape).  k_gemm_q: NG 16-wide column groups per
+// wavefront, NW wavefronts per workgroup sharing one staging of 4 MR rows,
+// PF weight chunks in flight, MF MFMAs first.
 //   64 rows:   q|k|v (2560 x 2048) 30.6 -> 22.1 with (1, 1, 4, 3, MF);
 //              o 28.5 -> 21.2, down (2048 x 5632) 67.0 -> 49.8 the same;
 //              gate|up (11264 x 2048) 81.6 -> 56.4 with (1, 2, 8, 4)
 //   512 rows:  (1, 2, 8, 4): q|k|v 138 -> 74, o 93 -> 62, down 196 -> 138;
 //              gate|up 503 -> 265 with (2, 2, 8, 3)
-// Wider shapes re-read the staged rows from LDS fewer times per weight
-// column but leave fewer wavefronts for short prompts; MFMAs first lets a
-// chunk's folds run without waiting on each MFMA result, and needs the
-// chunk's four blocks to exist (nb % 4 == 0).
+// k_gemm_qh over the chunk-major copy (MR, NW, CH, PF), every launch after
+// a 512 MB write that evicts L2 and the memory-side cache, as a prefill
+// meets its weights (the plain layout's launches and k_gemm_q in brackets):
+//   64 rows:   q|k|v 19.3 (2, 2, 8, 3) [24.2, 25.2]; o 16.4 (2, 1, 8, 4)
+//              [21.2, 22.2]; gate|up 41.6 (4, 4, 4, 4) [52.5, 61.6];
+//              down 31.9 (2, 1, 8, 4) [41.6, 48.1]
+//   512 rows:  (4, 4, 4, 4) MiniCPM q|k|v (6912 x 2304) 165 [198, 208], o 66
+//              [78, 83], gate|up (11520 x 2304) 264 [318, 308], down
+//              (2304 x 5760) 150 [176, 190]
+// Where the time goes (the same 64-row shapes with parts of the work left
+// out of a copy of the kernel): the fold is a few percent, the weight loads
+// a quarter and the activation staging another quarter -- a launch is
+// bound by load latency and request count, not by the arithmetic.  The
+// chunk-major copy turns four 4-byte loads from 16 rows into one 16-byte
+// load per thread and chunk.
 constexpr int kGemmWideRows = 256;
 constexpr int kGemmTallCols = 8192;
+constexpr int kGemmShortRows = 80;  // prompts up to this many rows take the short-prompt shapes
 
 int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
-               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop)
+               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop, const nc_tensor* wc)
 {
     if (w->dtype != NC_Q4 && w->dtype != NC_Q8) return fail(NC_ERR_ARG, "gemm: Q4/Q8 weights only");
     if (w->cols % 32 || w->cols <= 0 || w->rows <= 0 || n_rows <= 0)
         return fail(NC_ERR_ARG, "gemm: [%d x %d] weights, %d rows", w->rows, w->cols, n_rows);
     const int N = w->rows, nb = w->cols / 32;
-    auto go = [&](auto kern, int mr, int ng, int nw) {
+    auto go = [&](auto kern, int mr, int ng, int nw, const nc_tensor* wt = nullptr) {
+        if (!wt) wt = w;
         const dim3 grid((N + 16 * ng * nw - 1) / (16 * ng * nw), (n_rows + 4 * mr - 1) / (4 * mr));
         if (ev_start)
             hipExtLaunchKernelGGL(kern, grid, dim3(64 * nw), 0, st, ev_start, ev_stop, 0, x, x_pitch, n_rows,
-                                  (const uint32_t*)w->data, (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+                                  (const uint32_t*)wt->data, (const uint16_t*)wt->deltas, out, out_pitch, N, nb);
         else
-            hipLaunchKernelGGL(kern, grid, dim3(64 * nw), 0, st, x, x_pitch, n_rows, (const uint32_t*)w->data,
-                               (const uint16_t*)w->deltas, out, out_pitch, N, nb);
+            hipLaunchKernelGGL(kern, grid, dim3(64 * nw), 0, st, x, x_pitch, n_rows, (const uint32_t*)wt->data,
+                               (const uint16_t*)wt->deltas, out, out_pitch, N, nb);
     };
     const bool wide = n_rows >= kGemmWideRows, tall = N >= kGemmTallCols;
+    // the chunk-major copy, when the caller has one (shapes measured with
+    // cold caches, as a prefill meets its weights)
+    if (wc) {
+        if (wc->dtype != w->dtype || wc->rows != N || wc->cols != w->cols || !chunk_layout_supported(wc))
+            return fail(NC_ERR_ARG, "gemm: chunk copy [%d x %d] of a [%d x %d] weight", wc->rows, wc->cols, N, w->cols);
+        auto goc = [&](auto kern, int mr, int nw) { go(kern, mr, 1, nw, wc); };
+        auto by_type_c = [&](auto wt) {
+            constexpr int WT = decltype(wt)::value;
+            constexpr int PFT = WT == Q4 ? 4 : 2;  // Q8 chunks hold twice the registers
+            // chunks of 8 blocks need nb % 8 == 0 (the copy itself is in 4-block chunks)
+            if (wide || tall || n_rows > kGemmShortRows || nb % 8) goc(k_gemm_qh<WT, 4, 4, 4, PFT, true>, 4, 4);
+            else if (N <= 2048 || nb >= 128) goc(k_gemm_qh<WT, 2, 1, 8, 4, true>, 2, 1);
+            else goc(k_gemm_qh<WT, 2, 2, 8, 3, true>, 2, 2);
+        };
+        if (w->dtype == NC_Q4) by_type_c(std::integral_constant<int, Q4>{});
+        else by_type_c(std::integral_constant<int, Q8>{});
+        return launch_status("k_gemm_qh (chunk layout)");
+    }
+    // the fp16 matrix-core kernel: chunks of 4 (8) blocks, 8- (16-) byte
+    // delta loads
+    const bool qh4 = nb % 4 == 0 && ((uintptr_t)w->deltas & 7) == 0;
+    const bool qh8 = nb % 8 == 0 && ((uintptr_t)w->deltas & 15) == 0;
+    auto goh = [&](auto kern, int mr, int nw) { go(kern, mr, 1, nw); };
     auto by_type = [&](auto wt) {
         constexpr int WT = decltype(wt)::value;
         if (wide && tall) go(k_gemm_q<WT, 2, 2, 8, 3>, 8, 2, 2);
+        else if (qh4 && (wide || n_rows > kGemmShortRows)) goh(k_gemm_qh<WT, 4, 2, 4, 3, false>, 4, 2);
+        else if (qh4 && tall) goh(k_gemm_qh<WT, 4, 4, 4, 2, false>, 4, 4);
+        else if (qh8 && n_rows <= 16) goh(k_gemm_qh<WT, 2, 2, 8, 3, false>, 2, 2);
+        else if (qh4 && (N <= 2048 || nb >= 128)) goh(k_gemm_qh<WT, 2, 1, 4, 3, false>, 2, 1);
+        else if (qh8) goh(k_gemm_qh<WT, 4, 2, 8, 2, false>, 4, 2);
+        else if (qh4) goh(k_gemm_qh<WT, 4, 1, 4, 3, false>, 4, 1);
         else if (wide || (tall && n_rows >= 32)) go(k_gemm_q<WT, 1, 2, 8, 4>, 8, 1, 2);
-        else if (nb % kGmChunk == 0) go(k_gemm_q<WT, 1, 1, 4, 3, true>, 4, 1, 1);
         else go(k_gemm_q<WT, 1, 1, 4, 3>, 4, 1, 1);
     };
     if (w->dtype == NC_Q4) by_type(std::integral_constant<int, Q4>{});
     else by_type(std::integral_constant<int, Q8>{});
-    return launch_status("k_gemm_q");
+    return launch_status("k_gemm_q / k_gemm_qh");
 }
 
 }  // namespace nc

@@ -16,7 +16,8 @@ int write_rows(const float* in, int in_pitch, uint8_t* out, int out_pitch, int d
 // x rows (pointer at the first row) times weight rows -> fp32 dots.  With
 // events, the launch records them at the kernel's own start and end.
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
-               hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+               hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr,
+               const nc_tensor* wc = nullptr);
 
 // One fp16 row times the fused fp16 gate|up weight [2f, K] with the SwiGLU
 // epilogue: the fp16 row m[f] out.  Built for f a multiple of 4 and the
@@ -39,8 +40,15 @@ int dmv_f16_ln_launch(const uint8_t* a, int a_pitch, const float* braw, uint8_t*
 // x rows times Q4/Q8 weight rows -> fp32 dots on the matrix cores (the
 // reference's block dot product, exact); used by matvec_raw for multi-row
 // (prefill) products.
+// wc (optional): the weight's chunk-major copy (chunk_layout_launch), read
+// instead of w.
 int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
-               hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+               hipStream_t st, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr,
+               const nc_tensor* wc = nullptr);
+// The chunk-major copy of a Q4 / Q8 weight with K % 128 == 0 (codes and
+// deltas the same sizes as the weight's own) that gemm_q_raw reads.
+bool chunk_layout_supported(const nc_tensor* w);
+int chunk_layout_launch(const nc_tensor* w, void* codes, void* deltas, hipStream_t st);
 constexpr int kGemmMinRows = 8;  // matvec_raw takes the matrix-core path from this many rows
 
 // Norm over segments of d_norm values; with `add` the input is

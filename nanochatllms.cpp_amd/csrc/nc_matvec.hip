@@ -646,7 +646,7 @@ bool dmv_f16_dispatch(int G, Launch&& go)
 // out[r, c] = dot(x[r], w[c]) for x rows [0, n_rows) (pointers already at
 // the first row), fp32 out with `out_pitch` floats per row.
 int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_tensor* w, float* out, int out_pitch,
-               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop)
+               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop, const nc_tensor* wc)
 {
     // with events, the dispatch itself records them (the kernel's own start and end)
 #define NC_MV_LAUNCH(KERNEL, GRID, LDS, ...)                                                              \
@@ -660,7 +660,8 @@ int matvec_raw(const uint8_t* x, int x_dtype, int x_pitch, int n_rows, const nc_
     if (w->dtype == NC_Q4 || w->dtype == NC_Q8) {
         if (x_dtype != NC_Q8) return fail(NC_ERR_ARG, "matmul: Q%d weights need Q8 activations", w->dtype == NC_Q4 ? 4 : 8);
         if (K % 32) return fail(NC_ERR_ARG, "matmul: K=%d is not a multiple of 32", K);
-        if (n_rows >= kGemmMinRows) return gemm_q_raw(x, x_pitch, n_rows, w, out, out_pitch, st, ev_start, ev_stop);
+        if (n_rows >= kGemmMinRows)
+            return gemm_q_raw(x, x_pitch, n_rows, w, out, out_pitch, st, ev_start, ev_stop, wc);
         const int nb = K / 32;
         constexpr int R = 4;
         if (R * nb > kMvThreads * kMvMaxItems) return fail(NC_ERR_ARG, "matmul: K=%d too large", K);

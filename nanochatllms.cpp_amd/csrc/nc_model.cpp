@@ -37,6 +37,8 @@ namespace {
 struct Layer {
     int hq, hkv, qd, kvd, f;
     nc_tensor qkv{}, o{}, gu{}, down{};
+    // chunk-major copies read by the prefill matmul (data == nullptr: none)
+    nc_tensor cqkv{}, co{}, cgu{}, cdown{};
     uint16_t *attn_norm = nullptr, *attn_norm_b = nullptr, *mlp_norm = nullptr, *mlp_norm_b = nullptr;
     uint16_t *bq = nullptr, *bk = nullptr, *bv = nullptr, *qn = nullptr, *kn = nullptr;
     uint8_t *kc = nullptr, *vc = nullptr, *res1 = nullptr, *res2 = nullptr;
@@ -117,6 +119,8 @@ public:
     // fused step's lm-head kernel; rebuilt from the weight whenever it
     // changes (refresh_head).  data == nullptr: no copy.
     nc_tensor hl{};
+    // The layers' chunk-major copies need rebuilding (a weight changed since).
+    bool chunks_dirty = true;
 
     // Matvec launch timing: a start/end event pair recorded on the model's
     // stream around every matvec launch while profiling is on.
@@ -217,12 +221,14 @@ public:
         return NC_OK;
     }
 
-    int mv(const uint8_t* x, int x_pitch, int rows, const nc_tensor* w, float* out, int out_pitch, int role)
+    int mv(const uint8_t* x, int x_pitch, int rows, const nc_tensor* w, float* out, int out_pitch, int role,
+           const nc_tensor* wc = nullptr)
     {
         const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
+        if (wc && !wc->data) wc = nullptr;
         int s = timed ? matvec_raw(x, adt, x_pitch, rows, w, out, out_pitch, st, prof.ev[prof.used],
-                                   prof.ev[prof.used + 1])
-                      : matvec_raw(x, adt, x_pitch, rows, w, out, out_pitch, st);
+                                   prof.ev[prof.used + 1], wc)
+                      : matvec_raw(x, adt, x_pitch, rows, w, out, out_pitch, st, nullptr, nullptr, wc);
         if (s) return s;
         if (timed) {
             prof.used += 2;
@@ -369,6 +375,12 @@ public:
             if ((s = alloc_weight(&y.o, c->wdtype, d, y.qd))) return s;
             if ((s = alloc_weight(&y.gu, c->wdtype, 2 * y.f, d))) return s;
             if ((s = alloc_weight(&y.down, c->wdtype, d, y.f))) return s;
+            // the prefill matmul's chunk-major copies
+            for (auto wc : {std::make_pair(&y.qkv, &y.cqkv), std::make_pair(&y.o, &y.co), std::make_pair(&y.gu, &y.cgu),
+                            std::make_pair(&y.down, &y.cdown)})
+                if (chunk_layout_supported(wc.first) &&
+                    (s = alloc_weight(wc.second, c->wdtype, wc.first->rows, wc.first->cols)))
+                    return s;
             if ((s = alloc_t(&y.attn_norm, (size_t)d * 2)) || (s = alloc_t(&y.mlp_norm, (size_t)d * 2))) return s;
             if (c->arch == NC_ARCH_ZEPHYR) {
                 if ((s = alloc_t(&y.attn_norm_b, (size_t)d * 2)) || (s = alloc_t(&y.mlp_norm_b, (size_t)d * 2))) return s;
@@ -512,6 +524,7 @@ public:
             }
             return launch_status("weight fill");
         };
+        chunks_dirty = true;
         const unsigned globals[4] = {NC_TID_EMB, NC_TID_NORM, NC_TID_NORM_B, NC_TID_LM};
         for (unsigned g : globals)
             if ((s = one(-1, (int)g))) return s;
@@ -521,6 +534,22 @@ public:
         if ((s = refresh_head())) return s;
         hipError_t e = hipStreamSynchronize(st);
         return e == hipSuccess ? NC_OK : hip_fail(e, "init_synthetic");
+    }
+
+    // The chunk-major copies of the layer weights, rebuilt from the weights
+    // when one changed (before a prefill reads them).
+    int refresh_chunks()
+    {
+        if (!chunks_dirty) return NC_OK;
+        for (Layer& y : L)
+            for (auto wc : {std::make_pair(&y.qkv, &y.cqkv), std::make_pair(&y.o, &y.co),
+                            std::make_pair(&y.gu, &y.cgu), std::make_pair(&y.down, &y.cdown)})
+                if (wc.second->data) {
+                    int s = chunk_layout_launch(wc.first, wc.second->data, wc.second->deltas, st);
+                    if (s) return s;
+                }
+        chunks_dirty = false;
+        return NC_OK;
     }
 
     // The head-layout copy of the lm head, rebuilt from the weight.
@@ -542,6 +571,7 @@ public:
 
     int set_weight_only(int layer, int slot, const void* ref, size_t n_bytes)
     {
+        chunks_dirty = true;
         Loc o;
         int s = locate(layer, slot, &o);
         if (s) return s;
@@ -752,11 +782,12 @@ public:
     {
         const int R = dpos ? 1 : n - sp;
         if (R == 1 && fused) return forward_fused(sp, dpos);
+        int s;
+        if (R >= kGemmMinRows && (s = refresh_chunks())) return s;
         const int pd = pitch(d);
         const size_t off = dpos ? 0 : (size_t)sp * pd;  // host-side offset of position-indexed rows
         const bool minicpm = cfg.arch == NC_ARCH_MINICPM;
         const float bs = branch_scale();
-        int s;
         // embedding (+ MiniCPM's x12, minicpm.cpp:96)
         if ((s = embed_launch(&emb, dpos ? tokens : tokens + sp, x0 + off, pd, adt, R, minicpm ? 12.0f : 1.0f, st,
                               dpos)))
@@ -779,7 +810,7 @@ public:
                                first ? nullptr : L[l - 1].res2 + off, y.attn_norm, y.attn_norm_b, &y.qkv, qkv_raw,
                                nullptr, false, NC_PROF_QKV, dpos)))
                     return s;
-            } else if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv, NC_PROF_QKV))) {
+            } else if ((s = mv(xn, pd, R, &y.qkv, qkv_raw, nqkv, NC_PROF_QKV, &y.cqkv))) {
                 return s;
             }
             if (R == 1 && adt == NC_F16 && attn_decode_supported(y.hq, y.hkv, cfg.max_ctx)) {
@@ -795,7 +826,7 @@ public:
                                      cfg.max_ctx)))
                     return s;
             }
-            if ((s = mv(attn, pq, R, &y.o, o_raw, d, NC_PROF_O))) return s;
+            if ((s = mv(attn, pq, R, &y.o, o_raw, d, NC_PROF_O, &y.co))) return s;
             // h = x + attn (MiniCPM: attn scaled first), then the MLP norm and gate|up
             if (lnf) {
                 if ((s = mv_ln(xin + off, o_raw, y.res1 + off, y.mlp_norm, y.mlp_norm_b, &y.gu, nullptr, m_act, true,
@@ -808,11 +839,11 @@ public:
                 if (R == 1 && adt == NC_F16 && matvec_f16_glu_supported(&y.gu)) {
                     if ((s = mv_glu(xn, &y.gu, m_act))) return s;
                 } else {
-                    if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f, NC_PROF_GATE_UP))) return s;
+                    if ((s = mv(xn, pd, R, &y.gu, gu_raw, 2 * y.f, NC_PROF_GATE_UP, &y.cgu))) return s;
                     if ((s = silu_mul_launch(adt, gu_raw, 2 * y.f, y.f, m_act, pf, R, st))) return s;
                 }
             }
-            if ((s = mv(m_act, pf, R, &y.down, down_raw, d, NC_PROF_DOWN))) return s;
+            if ((s = mv(m_act, pf, R, &y.down, down_raw, d, NC_PROF_DOWN, &y.cdown))) return s;
             // out = h + mlp, then the next layer's attention norm (or the final norm)
             const bool last = l + 1 == cfg.n_layers;
             const uint16_t* nw = last ? norm_w : L[l + 1].attn_norm;
