@@ -395,7 +395,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_rows(const uint8_t* __res
     extern __shared__ __align__(16) float sm[];
     __shared__ float outs[R][64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int h = blockIdx.x, qr0 = blockIdx.y * R;
+    // the last row groups (the longest causal rows) are dispatched first, so
+    // the short ones fill the tail of the launch
+    const int h = blockIdx.x, qr0 = (gridDim.y - 1 - blockIdx.y) * R;
     const int nr = min(R, rows - qr0);
     const int m = start + qr0 + nr;  // positions attended by any of the rows
     const int mpad = (m + 3) & ~3;

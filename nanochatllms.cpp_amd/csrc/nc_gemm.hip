@@ -530,6 +530,8 @@ int chunk_layout_launch(const nc_tensor* w, void* codes, void* deltas, hipStream
 //   512 rows:  (4, 4, 4, 4) MiniCPM q|k|v (6912 x 2304) 165 [198, 208], o 66
 //              [78, 83], gate|up (11520 x 2304) 264 [318, 308], down
 //              (2304 x 5760) 150 [176, 190]
+//   Q8, 64 rows: q|k|v 22.8 (4, 4, 4, 4) [24.4, 24.9]; gate|up 48.2
+//              (4, 4, 4, 2) [61.0, 64.1]; down 32.6 (2, 2, 8, 3) [39.1, 47.2]
 // Where the time goes (the same 64-row shapes with parts of the work left
 // out of a copy of the kernel): the fold is a few percent, the weight loads
 // a quarter and the activation staging another quarter -- a launch is
@@ -569,7 +571,9 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
             constexpr int PFT = WT == Q4 ? 4 : 2;  // Q8 chunks hold twice the registers
             // chunks of 8 blocks need nb % 8 == 0 (the copy itself is in 4-block chunks)
             if (wide || tall || n_rows > kGemmShortRows || nb % 8) goc(k_gemm_qh<WT, 4, 4, 4, PFT, true>, 4, 4);
+            else if (WT == Q8 && nb >= 128) goc(k_gemm_qh<WT, 2, 2, 8, 3, true>, 2, 2);
             else if (N <= 2048 || nb >= 128) goc(k_gemm_qh<WT, 2, 1, 8, 4, true>, 2, 1);
+            else if (WT == Q8) goc(k_gemm_qh<WT, 4, 4, 4, 4, true>, 4, 4);
             else goc(k_gemm_qh<WT, 2, 2, 8, 3, true>, 2, 2);
         };
         if (w->dtype == NC_Q4) by_type_c(std::integral_constant<int, Q4>{});
