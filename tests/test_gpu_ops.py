@@ -58,6 +58,20 @@ MATMUL_CASES = [
     (Q8, Q8, 8192, 2048, 1, 0),
     (Q8, Q8, 64, 40, 5, 2),
     (Q8, Q4, 1024, 96, 9, 0),
+    # prompt-row shapes: every launch shape of the prefill matmul's table
+    # (fp16 matrix cores: 8- and 4-block chunks, short / medium / long
+    # prompts, tall weights, columns past a 16-multiple; the integer kernel
+    # for long prompts of tall weights and for rows of K % 128 != 0)
+    (Q8, Q4, 2048, 2560, 64, 0),
+    (Q8, Q4, 2048, 2048, 40, 3),
+    (Q8, Q4, 5632, 2048, 16, 0),
+    (Q8, Q8, 2048, 9000, 24, 0),
+    (Q8, Q8, 2304, 300, 100, 7),
+    (Q8, Q4, 5760, 1000, 50, 0),
+    (Q8, Q4, 1152, 3000, 60, 0),
+    (Q8, Q4, 2048, 8192, 260, 0),
+    (Q8, Q4, 2048, 700, 300, 0),
+    (Q8, Q8, 192, 100, 12, 0),
     (F16, F16, 2048, 2048, 1, 0),
     (F16, F16, 5632, 2048, 1, 0),
     (F16, F16, 128, 44, 4, 1),
