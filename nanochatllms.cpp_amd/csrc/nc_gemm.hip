@@ -305,31 +305,51 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_qh(const uint8_t* __restrict__
     for (int e = tid; e < 2 * CH * MR * 64; e += kThreads)
         if (((e & 15) & 3) != ((e >> 4) & 3)) (&xa[0][0][0][0])[e] = make_uint4(0, 0, 0, 0);
 
-    // staging: thread t < CH kRows stages (row t % kRows, block t / kRows)
-    // of each chunk; rows past the end repeat the last row (their outputs
-    // are not stored); other threads stage nothing
-    constexpr int kStagers = kRows * CH;
-    static_assert(kStagers <= kThreads, "every staged (row, block) needs its own thread");
-    const bool stager = tid < kStagers;
-    const int srow = tid % kRows, sblk = (tid / kRows) % CH;
-    const uint8_t* xrow = x + (size_t)min(r0 + srow, n_rows - 1) * x_pitch;
-    auto stage = [&](const XRaw& q, int buf) {
-        const uint32_t X[8] = {q.a.x, q.a.y, q.a.z, q.a.w, q.b.x, q.b.y, q.b.z, q.b.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t a = pick_pair(X[k >> 1], X[2 + (k >> 1)], k & 1);
-            const uint32_t b = pick_pair(X[4 + (k >> 1)], X[6 + (k >> 1)], k & 1);
-            uint4 h;
-            s8x4_to_h(a, h.x, h.y);
-            s8x4_to_h(b, h.z, h.w);
-            xa[buf][sblk][srow >> 2][(srow & 3) * 4 + k + 16 * k] = h;
-        }
-        xd[buf][sblk][srow] = h2f(q.d16);
+    // staging, spread over every thread: a task is one AVX lane k of one
+    // (row, block) of the chunk -- its eight codes as fp16 (16 bytes) -- and
+    // lane 0's task also stages the block's delta.  Rows past the end repeat
+    // the last row (their outputs are not stored).
+    constexpr int kTasks = 4 * kRows * CH;
+    constexpr int TPT = (kTasks + kThreads - 1) / kThreads;  // tasks per thread
+    struct XLane {
+        uint32_t d[4];  // dwords k/2, 2 + k/2, 4 + k/2, 6 + k/2 of the block
+        uint16_t d16;
     };
-    auto x_load = [&](int ch) {
-        XRaw q{};
-        if (stager) q = load_x_block(xrow, nb, min(ch, nch - 1) * CH + sblk);
-        return q;
+    int t_row[TPT], t_blk[TPT], t_k[TPT];
+    const uint8_t* t_src[TPT];
+#pragma unroll
+    for (int i = 0; i < TPT; i++) {
+        const int t = min(tid + i * kThreads, kTasks - 1);  // surplus slots repeat the last task
+        t_k[i] = t & 3;
+        t_row[i] = (t >> 2) % kRows;
+        t_blk[i] = (t >> 2) / kRows;
+        t_src[i] = x + (size_t)min(r0 + t_row[i], n_rows - 1) * x_pitch;
+    }
+    auto x_load = [&](int ch, XLane (&q)[TPT]) {
+        const int b0 = min(ch, nch - 1) * CH;
+#pragma unroll
+        for (int i = 0; i < TPT; i++) {
+            const int b = b0 + t_blk[i];
+            const uint32_t* blk = reinterpret_cast<const uint32_t*>(t_src[i] + (size_t)b * 32);
+            const int h = t_k[i] >> 1;
+#pragma unroll
+            for (int v = 0; v < 4; v++) q[i].d[v] = blk[2 * v + h];
+            q[i].d16 = reinterpret_cast<const uint16_t*>(t_src[i] + (size_t)nb * 32)[b];
+        }
+    };
+    auto stage = [&](const XLane (&q)[TPT], int buf) {
+#pragma unroll
+        for (int i = 0; i < TPT; i++) {
+            if (tid + i * kThreads >= kTasks) break;  // uniform per wave: kTasks is a multiple of 64
+            const int k = t_k[i], r = t_row[i], j = t_blk[i];
+            const uint32_t a = pick_pair(q[i].d[0], q[i].d[1], k & 1);
+            const uint32_t bq = pick_pair(q[i].d[2], q[i].d[3], k & 1);
+            uint4 hv;
+            s8x4_to_h(a, hv.x, hv.y);
+            s8x4_to_h(bq, hv.z, hv.w);
+            xa[buf][j][r >> 2][(r & 3) * 4 + k + 16 * k] = hv;
+            if (k == 0) xd[buf][j][r] = h2f(q[i].d16);
+        }
     };
 
     const uint32_t* wcol = wq + (size_t)col * nb * WD + WV * lg;
@@ -402,13 +422,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_qh(const uint8_t* __restrict__
     // weights and activation blocks in a ring of PF chunks (requested PF
     // chunks ahead, every request issued so the waits are exact counts)
     WChunk wr[PF];
-    XRaw xq[PF];
+    XLane xq[PF][TPT];
 #pragma unroll
     for (int p = 0; p < PF; p++) {
         w_load(p, wr[p]);
-        xq[p] = x_load(p);
+        x_load(p, xq[p]);
     }
-    if (stager) stage(xq[0], 0);
+    stage(xq[0], 0);
     lds_barrier();
     for (int cb = 0; cb < nch; cb += PF) {
 #pragma unroll
@@ -457,8 +477,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_qh(const uint8_t* __restrict__
                 }
             }
             w_load(ch + PF, wr[p]);
-            xq[p] = x_load(ch + PF);
-            if (ch + 1 < nch && stager) stage(xq[(p + 1) % PF], buf ^ 1);
+            x_load(ch + PF, xq[p]);
+            if (ch + 1 < nch) stage(xq[(p + 1) % PF], buf ^ 1);
             lds_barrier();
         }
     }
@@ -523,21 +543,22 @@ int chunk_layout_launch(const nc_tensor* w, void* codes, void* deltas, hipStream
 //              gate|up 503 -> 265 with (2, 2, 8, 3)
 // k_gemm_qh over the chunk-major copy (MR, NW, CH, PF), every launch after
 // a 512 MB write that evicts L2 and the memory-side cache, as a prefill
-// meets its weights (the plain layout's launches and k_gemm_q in brackets):
-//   64 rows:   q|k|v 19.3 (2, 2, 8, 3) [24.2, 25.2]; o 16.4 (2, 1, 8, 4)
-//              [21.2, 22.2]; gate|up 41.6 (4, 4, 4, 4) [52.5, 61.6];
-//              down 31.9 (2, 1, 8, 4) [41.6, 48.1]
-//   512 rows:  (4, 4, 4, 4) MiniCPM q|k|v (6912 x 2304) 165 [198, 208], o 66
-//              [78, 83], gate|up (11520 x 2304) 264 [318, 308], down
-//              (2304 x 5760) 150 [176, 190]
-//   Q8, 64 rows: q|k|v 22.8 (4, 4, 4, 4) [24.4, 24.9]; gate|up 48.2
-//              (4, 4, 4, 2) [61.0, 64.1]; down 32.6 (2, 2, 8, 3) [39.1, 47.2]
-// Where the time goes (the same 64-row shapes with parts of the work left
-// out of a copy of the kernel): the fold is a few percent, the weight loads
-// a quarter and the activation staging another quarter -- a launch is
-// bound by load latency and request count, not by the arithmetic.  The
+// meets its weights (k_gemm_q in brackets):
+//   64 rows, (2, 4, 8, 2):  q|k|v (2560 x 2048) 18.2 [24.5]; o 14.2 [22.2];
+//              down (2048 x 5632) 29.5 [47.3]; Q8 q|k|v 20.5 [24.7], down
+//              32.6 [48.8]
+//   gate|up (11264 x 2048, 64 rows) and every 512-row shape, (4, 4, 4, 2):
+//              gate|up 40.0 [61.5], Q8 48.6 [64.5]; MiniCPM q|k|v (6912 x
+//              2304) 162 [210], o 63 [81], gate|up (11520 x 2304) 266
+//              [318], down (2304 x 5760) 145 [186]
+// Where the time goes (the same shapes with parts of the work left out of a
+// copy of the kernel): at 64 rows the fold was a few percent, the weight
+// loads a quarter and the activation staging another quarter -- a launch
+// is bound by load latency and request count, not by the arithmetic.  The
 // chunk-major copy turns four 4-byte loads from 16 rows into one 16-byte
-// load per thread and chunk.
+// load per thread and chunk; at 512 rows the staging was the largest part
+// (28%) while one wavefront of four did it, so every thread now stages one
+// AVX lane of one (row, block).
 constexpr int kGemmWideRows = 256;
 constexpr int kGemmTallCols = 8192;
 constexpr int kGemmShortRows = 80;  // prompts up to this many rows take the short-prompt shapes
@@ -568,13 +589,9 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
         auto goc = [&](auto kern, int mr, int nw) { go(kern, mr, 1, nw, wc); };
         auto by_type_c = [&](auto wt) {
             constexpr int WT = decltype(wt)::value;
-            constexpr int PFT = WT == Q4 ? 4 : 2;  // Q8 chunks hold twice the registers
             // chunks of 8 blocks need nb % 8 == 0 (the copy itself is in 4-block chunks)
-            if (wide || tall || n_rows > kGemmShortRows || nb % 8) goc(k_gemm_qh<WT, 4, 4, 4, PFT, true>, 4, 4);
-            else if (WT == Q8 && nb >= 128) goc(k_gemm_qh<WT, 2, 2, 8, 3, true>, 2, 2);
-            else if (N <= 2048 || nb >= 128) goc(k_gemm_qh<WT, 2, 1, 8, 4, true>, 2, 1);
-            else if (WT == Q8) goc(k_gemm_qh<WT, 4, 4, 4, 4, true>, 4, 4);
-            else goc(k_gemm_qh<WT, 2, 2, 8, 3, true>, 2, 2);
+            if (wide || tall || n_rows > kGemmShortRows || nb % 8) goc(k_gemm_qh<WT, 4, 4, 4, 2, true>, 4, 4);
+            else goc(k_gemm_qh<WT, 2, 4, 8, 2, true>, 2, 4);
         };
         if (w->dtype == NC_Q4) by_type_c(std::integral_constant<int, Q4>{});
         else by_type_c(std::integral_constant<int, Q8>{});
