@@ -42,8 +42,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // NG 16-wide column groups per wavefront, NW wavefronts per workgroup (all
 // on the same rows, side by side in columns), MR groups of 4 rows (one MFMA
 // row operand each) per workgroup; the first 4 MR x kGmChunk threads stage
-// the activation blocks.
-template <int WT, int NG, int NW, int MR, int PF, bool MF = false>
+// the activation blocks.  Kept for rows whose blocks do not come in fours and
+// for long prompts of tall weights without the chunk-major copy.
+template <int WT, int NG, int NW, int MR, int PF>
 __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
                                                       const uint32_t* __restrict__ wq,
                                                       const uint16_t* __restrict__ wd, float* __restrict__ out,
@@ -123,52 +124,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q(const uint8_t* __restrict__ 
             const int ch = cb + p;
             if (ch >= nch) break;  // uniform
             const int buf = ch & 1;
-            if constexpr (MF) {
-                // the chunk's MFMAs first (nb % kGmChunk == 0), then its folds
-                // in block order: no fold waits on the MFMA just issued
-                v4i L[kGmChunk][MR][kGmNg];
-                float dd[kGmChunk][MR][kGmNg];
-#pragma unroll
-                for (int j = 0; j < kGmChunk; j++) {
-                    long B[kGmNg];
-                    float dw[kGmNg];
-#pragma unroll
-                    for (int n = 0; n < kGmNg; n++) {
-                        if (WT == Q4) {
-                            const uint32_t P = wr[p][j][n][0];
-                            B[n] = (long)(uint64_t)(((P >> 4) & 0x0F0F0F0Fu) | ((uint64_t)(P & 0x0F0F0F0Fu) << 32));
-                        } else {
-                            B[n] = (long)(uint64_t)(wr[p][j][n][0] | ((uint64_t)wr[p][j][n][1] << 32));
-                        }
-                        dw[n] = h2f(dr[p][j][n]);
-                    }
-#pragma unroll
-                    for (int m = 0; m < MR; m++) {
-                        const uint32_t* sa = xs[buf][j][4 * m + (lc >> 2)];
-                        const uint2 v = *reinterpret_cast<const uint2*>(sa + 2 * lg);
-                        const bool own = lg == (lc & 3);
-                        const long A = (long)(uint64_t)((own ? v.x : 0u) | ((uint64_t)(own ? v.y : 0u) << 32));
-                        const uint32_t* sr = xs[buf][j][4 * m + lg];
-                        const uint4 cs = *reinterpret_cast<const uint4*>(sr + 8);
-                        const v4i cinit = WT == Q4 ? v4i{(int)cs.x, (int)cs.y, (int)cs.z, (int)cs.w} : v4i{0, 0, 0, 0};
-                        const float dx = __uint_as_float(sr[12]);
-#pragma unroll
-                        for (int n = 0; n < kGmNg; n++) {
-                            L[j][m][n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B[n], cinit, 0, 0, 0);
-                            dd[j][m][n] = dx * dw[n];
-                        }
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < kGmChunk; j++)
-#pragma unroll
-                    for (int m = 0; m < MR; m++)
-#pragma unroll
-                        for (int n = 0; n < kGmNg; n++)
-#pragma unroll
-                            for (int k = 0; k < 4; k++)
-                                acc[m][n][k] = acc[m][n][k] + (float)L[j][m][n][k] * dd[j][m][n];
-            } else {
+            {
 #pragma unroll
             for (int j = 0; j < kGmChunk; j++) {
                 if (ch * kGmChunk + j >= nb) break;  // uniform
@@ -535,7 +491,8 @@ int chunk_layout_launch(const nc_tensor* w, void* codes, void* deltas, hipStream
 // Workgroup shapes, measured on MI355X with Q4 weights (us per launch,
 // exact results in every shape).  k_gemm_q: NG 16-wide column groups per
 // wavefront, NW wavefronts per workgroup sharing one staging of 4 MR rows,
-// PF weight chunks in flight, MF MFMAs first.
+// PF weight chunks in flight (MF: a variant that issued a chunk's MFMAs
+// before its folds, since replaced by k_gemm_qh).
 //   64 rows:   q|k|v (2560 x 2048) 30.6 -> 22.1 with (1, 1, 4, 3, MF);
 //              o 28.5 -> 21.2, down (2048 x 5632) 67.0 -> 49.8 the same;
 //              gate|up (11264 x 2048) 81.6 -> 56.4 with (1, 2, 8, 4)
@@ -605,12 +562,10 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
     auto by_type = [&](auto wt) {
         constexpr int WT = decltype(wt)::value;
         if (wide && tall) go(k_gemm_q<WT, 2, 2, 8, 3>, 8, 2, 2);
-        else if (qh4 && (wide || n_rows > kGemmShortRows)) goh(k_gemm_qh<WT, 4, 2, 4, 3, false>, 4, 2);
-        else if (qh4 && tall) goh(k_gemm_qh<WT, 4, 4, 4, 2, false>, 4, 4);
+        else if (qh4 && (wide || tall || n_rows > kGemmShortRows || !qh8)) goh(k_gemm_qh<WT, 4, 4, 4, 2, false>, 4, 4);
         else if (qh8 && n_rows <= 16) goh(k_gemm_qh<WT, 2, 2, 8, 3, false>, 2, 2);
-        else if (qh4 && (N <= 2048 || nb >= 128)) goh(k_gemm_qh<WT, 2, 1, 4, 3, false>, 2, 1);
-        else if (qh8) goh(k_gemm_qh<WT, 4, 2, 8, 2, false>, 4, 2);
-        else if (qh4) goh(k_gemm_qh<WT, 4, 1, 4, 3, false>, 4, 1);
+        else if (qh8 && (N <= 2048 || nb >= 128)) goh(k_gemm_qh<WT, 2, 4, 8, 2, false>, 2, 4);
+        else if (qh8) goh(k_gemm_qh<WT, 4, 4, 4, 2, false>, 4, 4);
         else if (wide || (tall && n_rows >= 32)) go(k_gemm_q<WT, 1, 2, 8, 4>, 8, 1, 2);
         else go(k_gemm_q<WT, 1, 1, 4, 3>, 4, 1, 1);
     };
