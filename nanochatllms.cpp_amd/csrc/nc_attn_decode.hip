@@ -13,11 +13,14 @@
 //     positions) and P.V as qkv_attn (gten/ops.cpp:1017-1220): the Q8 dot's
 //     four lane sums per block, P.V as eight fp32 lanes (position mod 8)
 //     summed left to right, then the n mod 8 tail.
-// Any context up to kAdMaxCtx positions: the scores sit in shared memory,
-// the K rows are read straight into registers (the next row requested before
-// the current one is used), and the V slice streams through shared memory in
-// double-buffered chunks of kAdVc positions while the P.V lane chains run
-// over them in position order.  The softmax denominator of a long row is the
+// Any context up to kAttnMaxCtx positions: the scores sit in shared memory
+// and the K rows are read straight into registers (the next row requested
+// before the current one is used).  For caches of up to kAdResMax positions
+// the whole V slice is staged into shared memory while the scores run, in a
+// layout where one dword read gives a lane chain four positions' codes and
+// one 16-byte read four positions' deltas or probabilities, so the P.V lane
+// chains then run without a barrier.  Longer caches stream the V slice
+// through shared memory in double-buffered chunks of kAdVc positions.  The softmax denominator of a long row is the
 // exact workgroup-parallel restatement of the sequential sum (nc_seqsum.h);
 // short rows take the plain loop on one wavefront.
 #include <type_traits>
@@ -44,6 +47,10 @@ constexpr int kAdMaxK = 2;      // K rows per thread requested at kernel start, 
 constexpr int kAdVB = 80;       // LDS bytes per staged V position: 64 codes, 2 fp16 deltas, pad
 constexpr int kAdVc = 128;      // positions per staged V chunk (2 16-byte parts per thread)
 constexpr int kAdSeqMax = 1024; // softmax rows up to this long are summed by one wavefront's loop
+constexpr int kAdResMax = 1024; // caches up to this long hold the whole V slice in shared memory
+// s_waitcnt immediate that waits for every vector memory load (vmcnt 0) and
+// leaves the export and LDS/scalar counters alone (expcnt 7, lgkmcnt 15).
+constexpr int kVmcnt0 = 0x0F70;
 
 __device__ __forceinline__ uint32_t ad_pick(uint32_t lo, uint32_t hi, int odd)
 {
@@ -168,8 +175,16 @@ __device__ __forceinline__ void store_vchunk(const VChunk& v, uint8_t* buf, int 
 // MK K rows per thread are requested into registers at the start (every
 // slot, so the load counts are static and the waits exact); later rows are
 // read in the score loop, one row ahead.  The launcher sizes MK to the cache:
-// issuing the loads is itself a cost.
-template <bool QKNORM, int MK>
+// issuing the loads is itself a cost.  VP > 0: the V slice of the positions
+// < n is resident in shared memory (the cache holds at most VP rows); VP == 0
+// streams it in chunks.
+//
+// Resident layout (VP > 0): positions c = 32 k4 + 8 j + l (lane l = c mod 8
+// of the P.V chains, k4 = c / 32, j = (c / 8) mod 4):
+//   codes   [l][k4][column 64] dwords, byte j = the code at position c;
+//   deltas  [block 2][l][VP / 8] fp32, entry c / 8;
+//   P       [l][sT] fp32 (the probabilities, entry c / 8).
+template <bool QKNORM, int MK, int VP>
 __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict__ raw, int hq, int hkv,
                                                          const uint16_t* __restrict__ qn_w,
                                                          const uint16_t* __restrict__ kn_w,
@@ -206,18 +221,26 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     const uint8_t* kslice = kc + g * 64;
     const uint8_t* vslice = vc + g * 64;
     // the first V chunk does not depend on the position either
+    constexpr bool kRes = VP > 0;
+    static_assert(VP % 32 == 0 && VP <= kAdResMax, "resident V: whole 32-position groups");
     VChunk vch;
-    load_vchunk(vch, vslice, vc + kvd, 0, kv_pitch, g, kv_rows);
+    if constexpr (!kRes) load_vchunk(vch, vslice, vc + kvd, 0, kv_pitch, g, kv_rows);
     const int pos = dpos ? load_pos(dpos) : pos_host;
     if (!rope_cur && rope_lane_in) rp = table[(size_t)pos * d_half + pair];
     __builtin_amdgcn_sched_barrier(0);
     const int n = pos + 1;
     // shared memory: scores [spad] (whole 256-position chunks, zero-padded
-    // for the block sum), P.V lane sums [8][64], two V chunk buffers
+    // for the block sum); resident V: P [8][sT], P.V lane sums [8][64], codes,
+    // deltas; streamed V: P.V lane sums, two V chunk buffers
     const int spad = (kv_rows + kSsThreads - 1) & ~(kSsThreads - 1);
+    const int sT = spad / 8 + 4;  // padded: the transposed P stores hit distinct banks
     float* S = sm;
-    float* acc = S + spad;
+    float* PT = S + spad;
+    float* acc = kRes ? PT + 8 * sT : S + spad;
     uint8_t* Vb = reinterpret_cast<uint8_t*>(acc + 512);
+    uint32_t* CT = reinterpret_cast<uint32_t*>(acc + 512);
+    float* DT = reinterpret_cast<float*>(CT + VP * 16);
+    constexpr int K4 = VP / 32, TPT = (VP + kAdThreads - 1) / kAdThreads;
 
     // ---- K rows (positions < pos) into registers
     KRow kr[MK];
@@ -254,12 +277,37 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
             if ((lane & 31) == 0) reinterpret_cast<uint16_t*>(row + kvd)[g * 2 + (lane >> 5)] = d16;
         }
     }
+    // resident V: the rows of positions < n requested (after this wave's
+    // q/k/v work, so that work is not queued behind them).  Item t =
+    // (k4, l, part q) covers rows 32 k4 + l + {0, 8, 16, 24}, bytes 16 q..
+    uint32_t vw[kRes ? TPT : 1][4][4];
+    uint32_t vd[kRes ? TPT : 1];
+    if constexpr (kRes) {
+        static_for<0, TPT>([&](auto T) {
+            const int t = tid + T * kAdThreads;
+            const int q = t & 3, l = (t >> 2) & 7, k4 = t >> 5;
+            if (t < VP && 32 * k4 + l < n) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int c = min(32 * k4 + 8 * j + l, kv_rows - 1);
+                    const uint4 x = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[q];
+                    vw[T][j][0] = x.x;
+                    vw[T][j][1] = x.y;
+                    vw[T][j][2] = x.z;
+                    vw[T][j][3] = x.w;
+                }
+            }
+            if (t < n) vd[T] = reinterpret_cast<const uint32_t*>(vc + kvd + (size_t)t * kv_pitch)[g];
+        });
+    }
     lds_barrier();
 
-    // the first V chunk into buffer 0; the second one requested
+    // streamed V: the first chunk into buffer 0; the second one requested
     const int nch = (n + kAdVc - 1) / kAdVc;
-    store_vchunk(vch, Vb, 0, pos, s_v);
-    if (nch > 1) load_vchunk(vch, vslice, vc + kvd, 1, kv_pitch, g, kv_rows);
+    if constexpr (!kRes) {
+        store_vchunk(vch, Vb, 0, pos, s_v);
+        if (nch > 1) load_vchunk(vch, vslice, vc + kvd, 1, kv_pitch, g, kv_rows);
+    }
 
     // ---- scores of positions c <= pos (thread = position)
     {
@@ -294,6 +342,46 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
             S[pos] = score_of(qv, dq, kk) * scale;
         }
     }
+    if constexpr (kRes) {
+        // ---- resident V into shared memory: four rows' dwords transposed so
+        // each output dword holds one column at four positions of a chain;
+        // the new position's row comes from s_v.  Every vector load is waited
+        // for here: the compiler cannot tell which are still in flight past
+        // the divergent score branches, and would otherwise wait inside the
+        // P.V loop.
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        static_for<0, TPT>([&](auto T) {
+            const int t = tid + T * kAdThreads;
+            const int q = t & 3, l = (t >> 2) & 7, k4 = t >> 5;
+            if (t < VP && 32 * k4 + l < n) {
+                uint32_t r[4][4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bool cur = 32 * k4 + 8 * j + l == pos;
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        r[j][i] = cur ? reinterpret_cast<const uint32_t*>(s_v)[4 * q + i] : vw[T][j][i];
+                }
+                uint4* dst = reinterpret_cast<uint4*>(CT + (l * K4 + k4) * 64 + 16 * q);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t lo01 = __builtin_amdgcn_perm(r[1][i], r[0][i], 0x05010400u);
+                    const uint32_t hi01 = __builtin_amdgcn_perm(r[1][i], r[0][i], 0x07030602u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(r[3][i], r[2][i], 0x05010400u);
+                    const uint32_t hi23 = __builtin_amdgcn_perm(r[3][i], r[2][i], 0x07030602u);
+                    dst[i] = make_uint4(__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
+                                        __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                        __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
+                                        __builtin_amdgcn_perm(hi23, hi01, 0x07060302u));
+                }
+            }
+            if (t < n) {
+                const uint32_t d = t == pos ? reinterpret_cast<const uint32_t*>(s_v + 64)[0] : vd[T];
+                DT[(t & 7) * (VP / 8) + (t >> 3)] = h2f((uint16_t)(d & 0xFFFFu));
+                DT[(8 + (t & 7)) * (VP / 8) + (t >> 3)] = h2f((uint16_t)(d >> 16));
+            }
+        });
+    }
     lds_barrier();
 
     // ---- softmax: max (order-free), expf, sequential sum, divide, requantize
@@ -327,7 +415,10 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         const bool valid = c < n;
         const float p = valid ? S[c] / sum : 0.0f;
         const float pr = q8_roundtrip_lane(p, valid);  // P stored as Act: 32-position blocks
-        if (valid) S[c] = pr;
+        if (valid) {
+            if constexpr (kRes) PT[(c & 7) * sT + (c >> 3)] = pr;
+            else S[c] = pr;
+        }
     }
     lds_barrier();
 
@@ -339,33 +430,65 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     const int l = tid >> 6, m = tid & 63;
     const int n8 = n & ~7;
     float a0 = 0.0f;
-    for (int ch = 0; ch < nch; ch++) {
-        const uint8_t* B = Vb + (ch & 1) * (kAdVc * kAdVB);
-        const int c0 = ch * kAdVc;
-        const int cend = min(c0 + kAdVc, n8);
-        auto vone = [&](int c) {
-            const uint8_t* vrow = B + (c - c0) * kAdVB;
-            const float d = h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[m >> 5]);  // block of column m
-            return (float)reinterpret_cast<const int8_t*>(vrow)[m] * d;
-        };
-        int c = c0;
-        for (; c + 64 <= cend; c += 64) {
-            // eight positions of the chain: loads first, then the adds in order
-            float p[8], v[8];
+    if constexpr (kRes) {
+        // the chain's positions l + 8 k, k < n8 / 8, four at a time: one
+        // dword of codes, one 16-byte read each of deltas and P
+        const int kn = n8 >> 3, ng = kn >> 2;
+        const float* Pl = PT + l * sT;
+        const uint32_t* Cl = CT + l * K4 * 64 + m;
+        const float* Dl = DT + ((m >> 5) * 8 + l) * (VP / 8);
+        auto four = [&](uint32_t cw, float4 d4, float4 p4) {
+            const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+            const float pp[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                p[u] = S[c + 8 * u + l];
-                v[u] = vone(c + 8 * u + l);
+            for (int j = 0; j < 4; j++) a0 = pp[j] * ((float)(int)(int8_t)(cw >> (8 * j)) * dd[j]) + a0;
+        };
+        int k4 = 0;
+        for (; k4 + 4 <= ng; k4 += 4) {
+            uint32_t cw[4];
+            float4 d4[4], p4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                cw[u] = Cl[(k4 + u) * 64];
+                d4[u] = reinterpret_cast<const float4*>(Dl)[k4 + u];
+                p4[u] = reinterpret_cast<const float4*>(Pl)[k4 + u];
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) a0 = p[u] * v[u] + a0;
+            for (int u = 0; u < 4; u++) four(cw[u], d4[u], p4[u]);
         }
-        for (; c < cend; c += 8) a0 = S[c + l] * vone(c + l) + a0;
-        if (ch + 1 < nch) {
-            store_vchunk(vch, Vb + ((ch + 1) & 1) * (kAdVc * kAdVB), ch + 1, pos, s_v);
-            if (ch + 2 < nch) load_vchunk(vch, vslice, vc + kvd, ch + 2, kv_pitch, g, kv_rows);
+        for (; k4 < ng; k4++)
+            four(Cl[k4 * 64], reinterpret_cast<const float4*>(Dl)[k4], reinterpret_cast<const float4*>(Pl)[k4]);
+        for (int k = ng * 4; k < kn; k++)
+            a0 = Pl[k] * ((float)(int)(int8_t)(Cl[(k >> 2) * 64] >> (8 * (k & 3))) * Dl[k]) + a0;
+    } else {
+        for (int ch = 0; ch < nch; ch++) {
+            const uint8_t* B = Vb + (ch & 1) * (kAdVc * kAdVB);
+            const int c0 = ch * kAdVc;
+            const int cend = min(c0 + kAdVc, n8);
+            auto vone = [&](int c) {
+                const uint8_t* vrow = B + (c - c0) * kAdVB;
+                const float d = h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[m >> 5]);  // block of column m
+                return (float)reinterpret_cast<const int8_t*>(vrow)[m] * d;
+            };
+            int c = c0;
+            for (; c + 64 <= cend; c += 64) {
+                // eight positions of the chain: loads first, then the adds in order
+                float p[8], v[8];
+    #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    p[u] = S[c + 8 * u + l];
+                    v[u] = vone(c + 8 * u + l);
+                }
+    #pragma unroll
+                for (int u = 0; u < 8; u++) a0 = p[u] * v[u] + a0;
+            }
+            for (; c < cend; c += 8) a0 = S[c + l] * vone(c + l) + a0;
+            if (ch + 1 < nch) {
+                store_vchunk(vch, Vb + ((ch + 1) & 1) * (kAdVc * kAdVB), ch + 1, pos, s_v);
+                if (ch + 2 < nch) load_vchunk(vch, vslice, vc + kvd, ch + 2, kv_pitch, g, kv_rows);
+            }
+            lds_barrier();
         }
-        lds_barrier();
     }
     acc[l * 64 + m] = a0;
     lds_barrier();
@@ -376,12 +499,21 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
         float s = acc[j];
 #pragma unroll
         for (int q = 1; q < 8; q++) s = s + acc[q * 64 + j];
-        const uint8_t* B = Vb + ((nch - 1) & 1) * (kAdVc * kAdVB);
-        const int c0 = (nch - 1) * kAdVc;
-        for (int c = n8; c < n; c++) {
-            const uint8_t* vrow = B + (c - c0) * kAdVB;
-            s = s + S[c] * ((float)reinterpret_cast<const int8_t*>(vrow)[j] *
-                            h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[j >> 5]));
+        if constexpr (kRes) {
+            for (int c = n8; c < n; c++) {
+                const int lc = c & 7, kc8 = c >> 3;
+                const uint32_t cw = CT[(lc * K4 + (kc8 >> 2)) * 64 + j];
+                s = s + PT[lc * sT + kc8] *
+                            ((float)(int)(int8_t)(cw >> (8 * (kc8 & 3))) * DT[((j >> 5) * 8 + lc) * (VP / 8) + kc8]);
+            }
+        } else {
+            const uint8_t* B = Vb + ((nch - 1) & 1) * (kAdVc * kAdVB);
+            const int c0 = (nch - 1) * kAdVc;
+            for (int c = n8; c < n; c++) {
+                const uint8_t* vrow = B + (c - c0) * kAdVB;
+                s = s + S[c] * ((float)reinterpret_cast<const int8_t*>(vrow)[j] *
+                                h2f(reinterpret_cast<const uint16_t*>(vrow + 64)[j >> 5]));
+            }
         }
         act_store<Q8>(out, h * 64 + j, act_delta_offset(hq * 64), s, true);
     }
@@ -668,10 +800,18 @@ int attn_decode_f16_launch(const float* raw, int hq, int hkv, const uint16_t* bq
     return launch_status("k_attn_dec_f16");
 }
 
+// Resident V positions of k_attn_dec for a cache of max_ctx rows (0: streamed).
+static int attn_decode_vp(int max_ctx)
+{
+    return max_ctx <= 256 ? 256 : max_ctx <= 512 ? 512 : max_ctx <= kAdResMax ? kAdResMax : 0;
+}
+
 // Shared memory of k_attn_dec for a cache of max_ctx rows.
 static size_t attn_decode_lds(int max_ctx)
 {
     const size_t spad = ((size_t)max_ctx + kSsThreads - 1) & ~(size_t)(kSsThreads - 1);
+    const size_t vp = (size_t)attn_decode_vp(max_ctx);
+    if (vp) return (spad + 8 * (spad / 8 + 4) + 512) * 4 + vp * 64 + vp * 8;
     return (spad + 512) * 4 + 2 * (size_t)kAdVc * kAdVB;
 }
 
@@ -695,11 +835,15 @@ int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, 
                            d_half, pos, dpos, kc, vc, kv_pitch, out, scale, (const float2*)rope_cur, max_ctx);
     };
     // K rows requested at the start: one per thread for caches of up to
-    // kAdThreads positions, two beyond
+    // kAdThreads positions, two beyond; the V slice resident up to kAdResMax
     auto by_ctx = [&](auto qk) {
         constexpr bool QK = decltype(qk)::value;
-        if (max_ctx <= kAdThreads) go(k_attn_dec<QK, 1>);
-        else go(k_attn_dec<QK, kAdMaxK>);
+        switch (attn_decode_vp(max_ctx)) {
+        case 256: go(k_attn_dec<QK, 1, 256>); break;
+        case 512: go(k_attn_dec<QK, 1, 512>); break;
+        case kAdResMax: go(k_attn_dec<QK, kAdMaxK, kAdResMax>); break;
+        default: go(k_attn_dec<QK, kAdMaxK, 0>); break;
+        }
     };
     if (qn_w) by_ctx(std::true_type{});
     else by_ctx(std::false_type{});
