@@ -596,7 +596,10 @@ __device__ __forceinline__ void store_vchunk16(const VChunk16& v, uint8_t* buf, 
     }
 }
 
-template <bool BIAS, bool QKNORM, int MK>
+// VP > 0: the V slice resident in shared memory as k_attn_dec's, with fp16
+// pairs: dword (l, k2, column) holds the column's values at positions
+// 16 k2 + l (low half) and 16 k2 + l + 8 (high half).
+template <bool BIAS, bool QKNORM, int MK, int VP>
 __global__ __launch_bounds__(kAdThreads) void k_attn_dec_f16(
     const float* __restrict__ raw, int hq, int hkv, const uint16_t* __restrict__ bq, const uint16_t* __restrict__ bk,
     const uint16_t* __restrict__ bv, const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w,
@@ -621,17 +624,23 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec_f16(
     const bool rope_lane_in = w < 2 && lane < 2 * d_half;
     const uint8_t* kslice = kc + g * 128;
     const uint8_t* vslice = vc + g * 128;
+    constexpr bool kRes = VP > 0;
+    static_assert(VP % 16 == 0, "resident V: whole 16-position groups");
     VChunk16 vch;
-    load_vchunk16(vch, vslice, 0, kv_pitch, kv_rows);
+    if constexpr (!kRes) load_vchunk16(vch, vslice, 0, kv_pitch, kv_rows);
     const int pos = dpos ? load_pos(dpos) : pos_host;
     float2 rp = make_float2(0.0f, 0.0f);
     if (rope_lane_in) rp = table[(size_t)pos * d_half + pair];
     __builtin_amdgcn_sched_barrier(0);
     const int n = pos + 1;
     const int spad = (kv_rows + kSsThreads - 1) & ~(kSsThreads - 1);
+    const int sT = spad / 8 + 4;
     float* S = sm;
-    float* acc = S + spad;
+    float* PT = S + spad;
+    float* acc = kRes ? PT + 8 * sT : S + spad;
     uint8_t* Vb = reinterpret_cast<uint8_t*>(acc + 512);
+    uint32_t* CT = reinterpret_cast<uint32_t*>(acc + 512);
+    constexpr int K2 = VP / 16, TPT = (4 * VP + kAdThreads - 1) / kAdThreads;
 
     // ---- K rows (positions < pos) into registers
     KRow16 kr[MK];
@@ -662,11 +671,33 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec_f16(
         if (w > 0 && h % gs == 0)
             reinterpret_cast<uint16_t*>((w == 1 ? kc : vc) + (size_t)pos * kv_pitch)[g * 64 + lane] = hx;
     }
+    // resident V: item t = (k2, l, part q) covers rows 16 k2 + l and + 8,
+    // bytes 16 q.. (columns 8 q..8 q + 7)
+    uint32_t vw[kRes ? TPT : 1][2][4];
+    if constexpr (kRes) {
+        static_for<0, TPT>([&](auto T) {
+            const int t = tid + T * kAdThreads;
+            const int q = t & 7, l = (t >> 3) & 7, k2 = t >> 6;
+            if (t < 4 * VP && 16 * k2 + l < n) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int c = min(16 * k2 + 8 * j + l, kv_rows - 1);
+                    const uint4 x = reinterpret_cast<const uint4*>(vslice + (size_t)c * kv_pitch)[q];
+                    vw[T][j][0] = x.x;
+                    vw[T][j][1] = x.y;
+                    vw[T][j][2] = x.z;
+                    vw[T][j][3] = x.w;
+                }
+            }
+        });
+    }
     lds_barrier();
 
     const int nch = (n + kAdVc - 1) / kAdVc;
-    store_vchunk16(vch, Vb, 0, pos, s_v);
-    if (nch > 1) load_vchunk16(vch, vslice, 1, kv_pitch, kv_rows);
+    if constexpr (!kRes) {
+        store_vchunk16(vch, Vb, 0, pos, s_v);
+        if (nch > 1) load_vchunk16(vch, vslice, 1, kv_pitch, kv_rows);
+    }
 
     // ---- scores of positions c <= pos (thread = position)
     {
@@ -697,6 +728,35 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec_f16(
             S[pos] = score16(qv, kk, scale);
         }
     }
+    if constexpr (kRes) {
+        // ---- resident V into shared memory: two rows' dwords interleaved by
+        // halves; the new position's row comes from s_v (all vector loads
+        // waited for here, as in k_attn_dec)
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        static_for<0, TPT>([&](auto T) {
+            const int t = tid + T * kAdThreads;
+            const int q = t & 7, l = (t >> 3) & 7, k2 = t >> 6;
+            if (t < 4 * VP && 16 * k2 + l < n) {
+                uint32_t r[2][4];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const bool cur = 16 * k2 + 8 * j + l == pos;
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        r[j][i] = cur ? reinterpret_cast<const uint32_t*>(s_v)[4 * q + i] : vw[T][j][i];
+                }
+                uint4* dst = reinterpret_cast<uint4*>(CT + (l * K2 + k2) * 64 + 8 * q);
+                dst[0] = make_uint4(__builtin_amdgcn_perm(r[1][0], r[0][0], 0x05040100u),
+                                    __builtin_amdgcn_perm(r[1][0], r[0][0], 0x07060302u),
+                                    __builtin_amdgcn_perm(r[1][1], r[0][1], 0x05040100u),
+                                    __builtin_amdgcn_perm(r[1][1], r[0][1], 0x07060302u));
+                dst[1] = make_uint4(__builtin_amdgcn_perm(r[1][2], r[0][2], 0x05040100u),
+                                    __builtin_amdgcn_perm(r[1][2], r[0][2], 0x07060302u),
+                                    __builtin_amdgcn_perm(r[1][3], r[0][3], 0x05040100u),
+                                    __builtin_amdgcn_perm(r[1][3], r[0][3], 0x07060302u));
+            }
+        });
+    }
     lds_barrier();
 
     // ---- softmax: max (order-free), expf, sequential sum, divide, fp16
@@ -723,35 +783,57 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec_f16(
         lds_barrier();
         sum = s_sum;
     }
-    for (int c = tid; c < n; c += kAdThreads) S[c] = f16_roundtrip(S[c] / sum);  // P stored as an fp16 row
+    for (int c = tid; c < n; c += kAdThreads) {
+        const float p = f16_roundtrip(S[c] / sum);  // P stored as an fp16 row
+        if constexpr (kRes) PT[(c & 7) * sT + (c >> 3)] = p;
+        else S[c] = p;
+    }
     lds_barrier();
 
     // ---- P.V: as k_attn_dec, the chain (l, m) over positions l, l + 8, ...
     const int l = tid >> 6, m = tid & 63;
     const int n8 = n & ~7;
     float a0 = 0.0f;
-    for (int ch = 0; ch < nch; ch++) {
-        const uint8_t* B = Vb + (ch & 1) * (kAdVc * kAdVB16);
-        const int c0 = ch * kAdVc;
-        const int cend = min(c0 + kAdVc, n8);
-        auto vone = [&](int c) { return h2f(reinterpret_cast<const uint16_t*>(B + (c - c0) * kAdVB16)[m]); };
-        int c = c0;
-        for (; c + 64 <= cend; c += 64) {
-            float p[8], v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                p[u] = S[c + 8 * u + l];
-                v[u] = vone(c + 8 * u + l);
+    if constexpr (kRes) {
+        const int kn = n8 >> 3, ng = kn >> 2;
+        const float* Pl = PT + l * sT;
+        const uint32_t* Cl = CT + l * K2 * 64 + m;
+        for (int k4 = 0; k4 < ng; k4++) {
+            const uint32_t w0 = Cl[(2 * k4) * 64], w1 = Cl[(2 * k4 + 1) * 64];
+            const float4 p4 = reinterpret_cast<const float4*>(Pl)[k4];
+            a0 = p4.x * h2f((uint16_t)(w0 & 0xFFFFu)) + a0;
+            a0 = p4.y * h2f((uint16_t)(w0 >> 16)) + a0;
+            a0 = p4.z * h2f((uint16_t)(w1 & 0xFFFFu)) + a0;
+            a0 = p4.w * h2f((uint16_t)(w1 >> 16)) + a0;
+        }
+        for (int k = ng * 4; k < kn; k++) {
+            const uint32_t wk = Cl[(k >> 1) * 64];
+            a0 = Pl[k] * h2f((uint16_t)((k & 1) ? wk >> 16 : wk & 0xFFFFu)) + a0;
+        }
+    } else {
+        for (int ch = 0; ch < nch; ch++) {
+            const uint8_t* B = Vb + (ch & 1) * (kAdVc * kAdVB16);
+            const int c0 = ch * kAdVc;
+            const int cend = min(c0 + kAdVc, n8);
+            auto vone = [&](int c) { return h2f(reinterpret_cast<const uint16_t*>(B + (c - c0) * kAdVB16)[m]); };
+            int c = c0;
+            for (; c + 64 <= cend; c += 64) {
+                float p[8], v[8];
+    #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    p[u] = S[c + 8 * u + l];
+                    v[u] = vone(c + 8 * u + l);
+                }
+    #pragma unroll
+                for (int u = 0; u < 8; u++) a0 = p[u] * v[u] + a0;
             }
-#pragma unroll
-            for (int u = 0; u < 8; u++) a0 = p[u] * v[u] + a0;
+            for (; c < cend; c += 8) a0 = S[c + l] * vone(c + l) + a0;
+            if (ch + 1 < nch) {
+                store_vchunk16(vch, Vb + ((ch + 1) & 1) * (kAdVc * kAdVB16), ch + 1, pos, s_v);
+                if (ch + 2 < nch) load_vchunk16(vch, vslice, ch + 2, kv_pitch, kv_rows);
+            }
+            lds_barrier();
         }
-        for (; c < cend; c += 8) a0 = S[c + l] * vone(c + l) + a0;
-        if (ch + 1 < nch) {
-            store_vchunk16(vch, Vb + ((ch + 1) & 1) * (kAdVc * kAdVB16), ch + 1, pos, s_v);
-            if (ch + 2 < nch) load_vchunk16(vch, vslice, ch + 2, kv_pitch, kv_rows);
-        }
-        lds_barrier();
     }
     acc[l * 64 + m] = a0;
     lds_barrier();
@@ -760,9 +842,18 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec_f16(
         float s = acc[j];
 #pragma unroll
         for (int q = 1; q < 8; q++) s = s + acc[q * 64 + j];
-        const uint8_t* B = Vb + ((nch - 1) & 1) * (kAdVc * kAdVB16);
-        const int c0 = (nch - 1) * kAdVc;
-        for (int c = n8; c < n; c++) s = s + S[c] * h2f(reinterpret_cast<const uint16_t*>(B + (c - c0) * kAdVB16)[j]);
+        if constexpr (kRes) {
+            for (int c = n8; c < n; c++) {
+                const int lc = c & 7, kc8 = c >> 3;
+                const uint32_t wk = CT[(lc * K2 + (kc8 >> 1)) * 64 + j];
+                s = s + PT[lc * sT + kc8] * h2f((uint16_t)((kc8 & 1) ? wk >> 16 : wk & 0xFFFFu));
+            }
+        } else {
+            const uint8_t* B = Vb + ((nch - 1) & 1) * (kAdVc * kAdVB16);
+            const int c0 = (nch - 1) * kAdVc;
+            for (int c = n8; c < n; c++)
+                s = s + S[c] * h2f(reinterpret_cast<const uint16_t*>(B + (c - c0) * kAdVB16)[j]);
+        }
         reinterpret_cast<uint16_t*>(out)[h * 64 + j] = f2h(s);
     }
 }
@@ -779,7 +870,10 @@ int attn_decode_f16_launch(const float* raw, int hq, int hkv, const uint16_t* bq
     if ((bq != nullptr) != (bk != nullptr) || (bq != nullptr) != (bv != nullptr))
         return fail(NC_ERR_ARG, "attention: q, k and v biases come together");
     const size_t spad = ((size_t)max_ctx + kSsThreads - 1) & ~(size_t)(kSsThreads - 1);
-    const size_t lds = (spad + 512) * 4 + 2 * (size_t)kAdVc * kAdVB16;
+    // the V slice resident for caches of up to 256 rows (128 bytes a row)
+    const bool res = max_ctx <= 256;
+    const size_t lds = res ? (spad + 8 * (spad / 8 + 4) + 512) * 4 + 256 * 128
+                           : (spad + 512) * 4 + 2 * (size_t)kAdVc * kAdVB16;
     const float scale = 1.0f / sqrtf(64.0f);
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, bq, bk, bv, qn_w, kn_w,
@@ -787,8 +881,9 @@ int attn_decode_f16_launch(const float* raw, int hq, int hkv, const uint16_t* bq
     };
     auto by_ctx = [&](auto bias, auto qk) {
         constexpr bool B = decltype(bias)::value, QK = decltype(qk)::value;
-        if (max_ctx <= kAdThreads) go(k_attn_dec_f16<B, QK, 1>);
-        else go(k_attn_dec_f16<B, QK, kAdMaxK>);
+        if (res) go(k_attn_dec_f16<B, QK, 1, 256>);
+        else if (max_ctx <= kAdThreads) go(k_attn_dec_f16<B, QK, 1, 0>);
+        else go(k_attn_dec_f16<B, QK, kAdMaxK, 0>);
     };
     if (bq) {
         if (qn_w) by_ctx(std::true_type{}, std::true_type{});
