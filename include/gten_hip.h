@@ -146,6 +146,14 @@ int nc_block_seq_sum(const float* t, int n, int count, float* out, int* fast, vo
 /* Host run of the same decomposition (no GPU): binades predicted from a
  * double prefix scaled by (1 + skew); *fast = 1 when its checks passed. */
 float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int* fast);
+/* Test hook (no counterpart in the reference): the fused decode matvecs with
+ * an rms_norm prologue compute their weight terms from a row normalized with
+ * a predicted sum of squares, beside the exact sum, and recompute every
+ * block whose exact row differs.  Launches made after this call scale the
+ * prediction by skew (1: none), so that tests can force the recomputation;
+ * when fixups (device int) is not null, each workgroup that recomputed adds
+ * one to it.  Results are the same for every skew > 0. */
+int nc_debug_spec(float skew, void* fixups);
 /* Greedy pick of greedy_sample (src/gten/sampler.cpp:33-41): first index of
  * the maximum. */
 int nc_argmax(const float* x, int n, int32_t* out, void* stream);

@@ -132,7 +132,7 @@ def lib():
         "nc_add": (I, [TP, TP, TP, I, I, VP]), "nc_scale": (I, [TP, F, I, I, VP]),
         "nc_bias_add": (I, [TP, VP, I, I, VP]), "nc_qkv_attn": (I, [TP, TP, TP, TP, I, I, I, I, I, VP]),
         "nc_argmax": (I, [VP, I, VP, VP]), "nc_expf": (I, [VP, VP, C.c_int64, VP]),
-        "nc_expf_host": (F, [F]),
+        "nc_expf_host": (F, [F]), "nc_debug_spec": (I, [F, VP]),
         "nc_model_create": (I, [C.POINTER(ModelConfig), C.POINTER(VP)]), "nc_model_free": (I, [VP]),
         "nc_model_init_synthetic": (I, [VP, U64]), "nc_model_set_weight": (I, [VP, I, I, VP, SZ]),
         "nc_model_get_weight": (I, [VP, I, I, VP, SZ]), "nc_model_logits": (I, [VP, VP, I, I, VP]),

@@ -65,6 +65,11 @@ struct DmvArgs {
     // Nonzero: wq / wd are an lm head in the head layout (head_layout_launch);
     // only with PRO_RES_RMS and EPI_RAW / EPI_ARGMAX.
     int head = 0;
+    // Speculative norm launches (set by decode_matvec from nc_debug_spec):
+    // the factor on the predicted sum of squares (1: none) and a device
+    // counter of the workgroups that recomputed blocks (null: none).
+    float spec_skew = 1.0f;
+    int* spec_fixups = nullptr;
 };
 
 // The lm-head copy of a Q4 / Q8 weight [N, K] read by the head kernel: rows

@@ -36,36 +36,43 @@ __device__ __forceinline__ XRaw load_x_block(const uint8_t* xrow, int nb, int i)
     return XRaw{q[0], q[1], reinterpret_cast<const uint16_t*>(xrow + (size_t)nb * 32)[i]};
 }
 
-__device__ __forceinline__ void stage_x_block(const XRaw& x, uint32_t* dst)
-{
-    const uint4 a = x.a, b = x.b;
-    const uint32_t X[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    const uint16_t d16 = x.d16;
-    uint32_t o[16];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint32_t xa = pick_pair(X[k >> 1], X[2 + (k >> 1)], k & 1);
-        const uint32_t xb = pick_pair(X[4 + (k >> 1)], X[6 + (k >> 1)], k & 1);
-        o[2 * k] = xa;
-        o[2 * k + 1] = xb;
-        const int s = __builtin_amdgcn_sdot4((int)xa, 0x01010101, __builtin_amdgcn_sdot4((int)xb, 0x01010101, 0, false),
-                                             false);
-        o[8 + k] = (uint32_t)(-7 * s);
-    }
-    o[12] = __float_as_uint(h2f(d16));
-    o[13] = o[14] = o[15] = 0;
-    uint4* d = reinterpret_cast<uint4*>(dst);
-#pragma unroll
-    for (int v = 0; v < 4; v++) d[v] = make_uint4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
-}
-
-// A staged activation block read back from LDS: the lane codes, the lane
-// offsets c_k and the delta.
+// A staged activation block: the lane codes, the lane offsets c_k and the
+// delta.
 struct StagedX {
     uint32_t xa[4], xb[4];
     int c[4];
     float dx;
 };
+
+// The staged form of a raw block, in registers.
+__device__ __forceinline__ StagedX make_staged(const XRaw& x)
+{
+    const uint4 a = x.a, b = x.b;
+    const uint32_t X[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    StagedX r;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t xa = pick_pair(X[k >> 1], X[2 + (k >> 1)], k & 1);
+        const uint32_t xb = pick_pair(X[4 + (k >> 1)], X[6 + (k >> 1)], k & 1);
+        r.xa[k] = xa;
+        r.xb[k] = xb;
+        const int s = __builtin_amdgcn_sdot4((int)xa, 0x01010101, __builtin_amdgcn_sdot4((int)xb, 0x01010101, 0, false),
+                                             false);
+        r.c[k] = -7 * s;
+    }
+    r.dx = h2f(x.d16);
+    return r;
+}
+
+__device__ __forceinline__ void stage_x_block(const XRaw& x, uint32_t* dst)
+{
+    const StagedX t = make_staged(x);
+    uint4* d = reinterpret_cast<uint4*>(dst);
+    d[0] = make_uint4(t.xa[0], t.xb[0], t.xa[1], t.xb[1]);
+    d[1] = make_uint4(t.xa[2], t.xb[2], t.xa[3], t.xb[3]);
+    d[2] = make_uint4((uint32_t)t.c[0], (uint32_t)t.c[1], (uint32_t)t.c[2], (uint32_t)t.c[3]);
+    d[3] = make_uint4(__float_as_uint(t.dx), 0u, 0u, 0u);
+}
 
 __device__ __forceinline__ StagedX load_staged(const uint32_t* staged)
 {

@@ -160,22 +160,37 @@ __device__ __forceinline__ SsSeg wave_scan_seg(SsSeg x)
 // chunk once: binade predicted from an approximate prefix, step maps
 // composed, and up to four crossings recorded (more fall back).  A segmented
 // scan joins the chunks, and wave 0 replays the few records in order.
-template <int C>
-__device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* fast)
-{
-    if (threadIdx.x >= kSsThreads) {
-        // waves past the first four (larger workgroups) only keep the
-        // barrier count of the path below: its four phase barriers, the
-        // fallback's barrier when it is taken, and the final one
-        lds_barrier();
-        lds_barrier();
-        lds_barrier();
-        lds_barrier();
-        if (!sh.ok) lds_barrier();
-        const float res = sh.result;
-        lds_barrier();
-        return res;
+//
+// The barrier among the 256 threads is a functor: the workgroup's LDS
+// barrier, or SsWaveBarrier when the first four wavefronts compute the sum
+// while the others do work of their own.
+struct SsLdsBarrier {
+    __device__ void operator()() { lds_barrier(); }
+};
+
+// Barrier among the first NW wavefronts through an LDS counter (zeroed by
+// a workgroup barrier before each sum that uses it): each wavefront adds one
+// and waits until the count reaches NW times the number of barriers passed.
+// LDS traffic only (global loads stay in flight across it).
+template <int NW>
+struct SsWaveBarrier {
+    int* cnt;
+    int gen;
+    __device__ void operator()()
+    {
+        gen += NW;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if ((threadIdx.x & (kWave - 1)) == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < gen) {
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
+};
+
+// Threads 0..255 only.
+template <int C, class Bar>
+__device__ __forceinline__ float block_seq_sum_core(const float* t, int n, SsShared& sh, bool* fast, Bar& bar)
+{
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
     const int c = C ? C : n / kSsThreads;
     const int i0 = tid * c;
@@ -210,7 +225,7 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
     // last lane's wf_{w-1} + WP_{w-1} equals the next wave's WP_w.
     float I = wave_scan_add(cs);
     if (lane == kWave - 1) sh.wf[w] = I;
-    lds_barrier();
+    bar();
     float WP = 0.0f;
     {
         const float4 F = *reinterpret_cast<const float4*>(sh.wf);  // every wave's total at once
@@ -297,7 +312,7 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
         sh.wfl[w] = x.f;
         sh.wcnt[w] = x.n | (over << 30);
     }
-    lds_barrier();
+    bar();
     SsSeg pre{0, 0, 0, 0};
     int any_over;
     {
@@ -332,7 +347,7 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
         sh.m = any_over ? kSsMaxCross + 1 : cnt;
         if (cnt < kSsMaxCross) sh.rec[cnt] = make_int4(x.c0, x.c1, (x.f & 1) ? ss_binade(I) : 0, 0);
     }
-    lds_barrier();
+    bar();
     // ---- replay on wave 0 from thread 0's exact chunk sum: record r in lane
     // r; per record s = s + u C(parity) (when the segment holds a nonzero
     // term), then the crossing add; the binade checks ride beside the chain
@@ -377,21 +392,42 @@ __device__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* f
             sh.ok = ok;
         }
     }
-    lds_barrier();
+    bar();
     if (!sh.ok) {
         // fallback: the plain loop on one wavefront
         if (tid < kWave) {
             const float s = seq_sum(t, n);
             if (tid == 0) sh.result = s;
         }
-        lds_barrier();
+        bar();
     }
     if (fast && tid == 0) *fast = sh.ok != 0;
     const float res = sh.result;
-    lds_barrier();  // sh reusable after return
+    bar();  // sh reusable after return
     return res;
 }
 
+
+// Every thread of a workgroup of 256 or more threads calls it; threads past
+// the first 256 only keep the barrier count of the computing ones.
+template <int C>
+__device__ __forceinline__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* fast)
+{
+    if (threadIdx.x >= kSsThreads) {
+        // the four phase barriers, the fallback's barrier when it is
+        // taken, and the final one
+        lds_barrier();
+        lds_barrier();
+        lds_barrier();
+        lds_barrier();
+        if (!sh.ok) lds_barrier();
+        const float res = sh.result;
+        lds_barrier();
+        return res;
+    }
+    SsLdsBarrier bar;
+    return block_seq_sum_core<C>(t, n, sh, fast, bar);
+}
 
 // Dispatch on the terms per thread (compile-time chunk lengths for the
 // model widths: 2048 -> 8, 2304 -> 9).
@@ -400,6 +436,18 @@ __device__ __forceinline__ float block_seq_sum_nonneg(const float* t, int n, SsS
     if (n == 8 * kSsThreads) return block_seq_sum_impl<8>(t, n, sh, fast);
     if (n == 9 * kSsThreads) return block_seq_sum_impl<9>(t, n, sh, fast);
     return block_seq_sum_impl<0>(t, n, sh, fast);
+}
+
+// The same computed by threads 0..255 alone (only they call it), which
+// synchronize through the LDS counter *cnt (zeroed before each call, then a
+// workgroup barrier): the workgroup's other wavefronts run work of their
+// own meanwhile.  Returns the sum on threads 0..255.
+__device__ __forceinline__ float block_seq_sum_nonneg_waves(const float* t, int n, SsShared& sh, int* cnt)
+{
+    SsWaveBarrier<kSsThreads / kWave> bar{cnt, 0};
+    if (n == 8 * kSsThreads) return block_seq_sum_core<8>(t, n, sh, nullptr, bar);
+    if (n == 9 * kSsThreads) return block_seq_sum_core<9>(t, n, sh, nullptr, bar);
+    return block_seq_sum_core<0>(t, n, sh, nullptr, bar);
 }
 
 #endif  // __HIPCC__

@@ -124,6 +124,9 @@ def test_argument_errors_are_reported(nc):
     k = nc.Tensor(1, None, nc.F16, 4, 64, 128)
     assert L.nc_qkv_attn(C.byref(q), C.byref(k), C.byref(k), C.byref(q), 2, 1, 64, 0, 4, None) == -1
     assert b"dtypes" in L.nc_last_error()
+    assert L.nc_debug_spec(-1.0, None) == -1
+    assert b"skew" in L.nc_last_error()
+    assert L.nc_debug_spec(1.0, None) == 0
 
 
 def test_kernel_expf_equals_host_libm_exhaustive(nc, oracle):

@@ -137,6 +137,14 @@ def test_decode_steps_match_reference(gpu, name):
     layer's row at the step's position equal the reference's bit for bit,
     and each step's greedy token is the reference's.  Then the same stream
     through the captured step graph."""
+    reference_loop(gpu, name)
+
+
+def reference_loop(gpu, name):
+    """Model::logits stepped as the reference's greedy loop (start_pos = n -
+    1 after the prompt): the prefill digests, the recorded decode steps'
+    logits and layer rows and every token must be the reference's; then the
+    stream through the captured step graph."""
     w = ALL[name]
     g = golden(name)
     prompt = prompt_of(w)
@@ -163,7 +171,7 @@ def test_decode_steps_match_reference(gpu, name):
                 assert sha(m.layer_out(l, len(toks) - 1)) == digest, f"step {i}: layer {l}"
             seen.add(i)
         t = greedy_pick(logits)
-        if i == len(ref):  # the reference stopped at eos here
+        if i == len(ref):
             assert t == cfg.eos
             break
         assert t == ref[i], f"step {i}: token {t}, reference {ref[i]}"
@@ -174,6 +182,29 @@ def test_decode_steps_match_reference(gpu, name):
     m.init_synthetic(w["seed"])
     assert m.generate(prompt, w["gen"]).tolist() == ref
     m.close()
+
+
+@pytest.mark.parametrize("skew", [2.0, 1.001, 1.0 + 2.0 ** -22])
+@pytest.mark.parametrize("name", ["wide-llama-q4", "wide-llama-q8", "wide-minicpm-q4", "tinyllama-q4"])
+def test_speculative_norm_rows_recomputed(gpu, name, skew):
+    """The fused norm launches compute their weight terms from a row
+    normalized with a predicted sum of squares, beside the exact sum, and
+    recompute the blocks where the exact row differs.  A prediction skewed
+    from the host makes rows differ (all blocks at 2x, some at 1.001x, the
+    odd tie at 1 + 2^-22): the fix-ups must run and every digest and token
+    must still be the reference's."""
+    L = gpu.lib()
+    cnt = gpu.DeviceBuffer(4)
+    cnt.upload(np.zeros(1, np.int32))
+    gpu.check(L.nc_debug_spec(skew, cnt.ptr))
+    try:
+        reference_loop(gpu, name)
+    finally:
+        gpu.check(L.nc_debug_spec(1.0, None))
+    fixups = int(cnt.download(np.zeros(1, np.int32))[0])
+    cnt.close()
+    if skew > 1.0005:
+        assert fixups > 0, "the recomputation path did not run"
 
 
 @pytest.mark.parametrize("max_ctx", [200, 1024, 4096])
