@@ -67,8 +67,8 @@ FUSED_KERNEL = {"qkv": "k_dmv (qkv, residual add + rms_norm prologue)",
                 "lm_head": "k_dmv_head (lm head in the head layout, residual add + final norm prologue, "
                            "greedy-token epilogue; k_dmv for widths other than 2048 / 2304)"}
 
-FUSED_F16_KERNEL = {"qkv": "k_dmv_f16_ln (q|k|v, residual add + layer_norm prologue)",
-                    "gate_up": "k_dmv_f16_ln<GLU> (gate|up, residual add + layer_norm prologue, SwiGLU epilogue)"}
+FUSED_F16_KERNEL = {"qkv": "k_dmv_f16_nrm (q|k|v, residual add + norm prologue)",
+                    "gate_up": "k_dmv_f16_nrm<GLU> (gate|up, residual add + norm prologue, SwiGLU epilogue)"}
 
 
 def prompt_tokens(w):

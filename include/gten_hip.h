@@ -146,6 +146,16 @@ int nc_block_seq_sum(const float* t, int n, int count, float* out, int* fast, vo
 /* Host run of the same decomposition (no GPU): binades predicted from a
  * double prefix scaled by (1 + skew); *fast = 1 when its checks passed. */
 float nc_seq_sum_nonneg_host(const float* t, int n, double skew, int* fast);
+/* The left-to-right fp32 sum of signed values of layer_norm's mean (src/gten/
+ * ops.cpp:673-676) as the fused layer-norm prologues compute it on the
+ * device, for values on the fp16 grid (multiples of 2^-24 below 2^17: fp16
+ * activations, Q8 codes times fp16 deltas): out[b] = sum of x[b*n ..
+ * b*n+n) for n = 1024, 2048 or 2304; passes[b] = the parallel passes made
+ * (0 when its sequential fallback ran). */
+int nc_block_seq_sum_grid(const float* x, int n, int count, float* out, int* passes, void* stream);
+/* Host run of the same decomposition (no GPU); plant = 1 drops the rounding
+ * error after each rounding step (a planted mistake for tests). */
+float nc_seq_sum_grid_host(const float* x, int n, int plant, int* passes);
 /* Test hook (no counterpart in the reference): the fused decode matvecs with
  * an rms_norm prologue compute their weight terms from a row normalized with
  * a predicted sum of squares, beside the exact sum, and recompute every

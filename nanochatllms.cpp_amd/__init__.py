@@ -133,6 +133,8 @@ def lib():
         "nc_bias_add": (I, [TP, VP, I, I, VP]), "nc_qkv_attn": (I, [TP, TP, TP, TP, I, I, I, I, I, VP]),
         "nc_argmax": (I, [VP, I, VP, VP]), "nc_expf": (I, [VP, VP, C.c_int64, VP]),
         "nc_expf_host": (F, [F]), "nc_debug_spec": (I, [F, VP]),
+        "nc_block_seq_sum_grid": (I, [VP, I, I, VP, VP, VP]),
+        "nc_seq_sum_grid_host": (F, [VP, I, I, C.POINTER(I)]),
         "nc_model_create": (I, [C.POINTER(ModelConfig), C.POINTER(VP)]), "nc_model_free": (I, [VP]),
         "nc_model_init_synthetic": (I, [VP, U64]), "nc_model_set_weight": (I, [VP, I, I, VP, SZ]),
         "nc_model_get_weight": (I, [VP, I, I, VP, SZ]), "nc_model_logits": (I, [VP, VP, I, I, VP]),

@@ -312,8 +312,10 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
     // stores (through the XCD's L2) and read with agent-scope atomic loads,
     // so they are coherent across the XCDs' L2s without a cache flush.  A
     // writer waits for its store to complete (wait_stores_done) before it
-    // bumps the counter, so a reader that sees the count sees every key
-    // counted; the reader's loads depend on the count it got back.
+    // bumps the counter (the release of that one location, without the L2
+    // write-back of a release fence), so a reader that sees the count sees
+    // every key counted; the last arriver takes an agent-scope acquire fence
+    // before it reads them.
     // Scratch layout (64-bit words): [0] top counter, [64, 192) level-1
     // results, [192, 320) level-1 counters, [320, 320 + grid) workgroup keys.
     unsigned long long* top = A.amax;
@@ -344,6 +346,7 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
         const int members = min(32, G - grp * 32);
         done = __shfl(done, 0);
         if (done == (unsigned long long)members - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             unsigned long long k = tid < members
                     ? __hip_atomic_load(slot + grp * 32 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                     : 0ull;
@@ -361,6 +364,7 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
             }
             done2 = __shfl(done2, 0);
             if (done2 == (unsigned long long)ngrp - 1) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
                 unsigned long long b2 = 0;
                 for (int q = tid; q < ngrp; q += kWave) {
                     const unsigned long long o = __hip_atomic_load(sub + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -968,6 +972,34 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
             if (j * NT >= nch) break;  // uniform
             qx[j] = spec_norm_chunk(h[j], gain[j], denom, A.post_scale);
         }
+        // once the speculative row is complete (every weight wavefront has
+        // passed its first barrier), compare it block by block with the
+        // exact one (a lane quad holds a block) while the weight threads
+        // finish
+        while (__hip_atomic_load(&sy.spec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NS / kWave) {
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        int any = 0;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            if (j * NT >= nch) break;  // uniform
+            const bool valid = ch < nch;
+            const int cc = valid ? ch : 0;
+            const Q8Chunk& q = qx[j];
+            const uint2 sc = *reinterpret_cast<const uint2*>(L.row + (size_t)cc * 8);
+            const uint16_t sd = reinterpret_cast<const uint16_t*>(L.row + K)[cc >> 2];
+            uint32_t w[2] = {0, 0};
+#pragma unroll
+            for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q.q[i] << (8 * (i & 3));
+            int diff = valid && (sc.x != w[0] || sc.y != w[1] || sd != q.d16) ? 1 : 0;
+            diff |= dpp_i<kDppQuadXor1>(diff);
+            diff |= dpp_i<kDppQuadXor2>(diff);
+            any |= diff;
+            if (valid && (ch & 3) == 0) L.bad[ch >> 2] = (uint8_t)diff;
+        }
+        if (__builtin_amdgcn_ballot_w64(any != 0) && lane == 0) sy.anybad = 1;
+        __builtin_amdgcn_s_setprio(0);
     } else {
         // the speculative row (weight threads 0-255, a quad per block), a
         // barrier among the weight threads, every block's terms, then the
@@ -994,40 +1026,22 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
         spec_tail(sbar);
     }
     lds_barrier();
-    if (ex) {
-        // compare block by block (a lane quad holds a block), store the
-        // exact row over the speculative one
-        int any = 0;
-#pragma unroll
-        for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * NT;
-            if (j * NT >= nch) break;  // uniform
-            const bool valid = ch < nch;
-            const int cc = valid ? ch : 0;
-            const Q8Chunk& q = qx[j];
-            const uint2 sc = *reinterpret_cast<const uint2*>(L.row + (size_t)cc * 8);
-            const uint16_t sd = reinterpret_cast<const uint16_t*>(L.row + K)[cc >> 2];
-            uint32_t w[2] = {0, 0};
-#pragma unroll
-            for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q.q[i] << (8 * (i & 3));
-            int diff = valid && (sc.x != w[0] || sc.y != w[1] || sd != q.d16) ? 1 : 0;
-            diff |= dpp_i<kDppQuadXor1>(diff);
-            diff |= dpp_i<kDppQuadXor2>(diff);
-            any |= diff;
-            if (valid) {
-                store_act_chunk(L.row, K, ch, q);
-                if ((ch & 3) == 0) L.bad[ch >> 2] = (uint8_t)diff;
-            }
-        }
-        if (__builtin_amdgcn_ballot_w64(any != 0) && lane == 0) sy.anybad = 1;
-        __builtin_amdgcn_s_setprio(0);
-    }
-    lds_barrier();
     if (!sy.anybad) {
         commit();
         return;
     }
+    // some block differs: the exact row over the speculative one, the
+    // differing blocks' terms recomputed, and the fold and epilogue again
     if (A.spec_fixups && tid == 0) atomicAdd(A.spec_fixups, 1);
+    if (ex) {
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            if (j * NT >= nch) break;  // uniform
+            if (ch < nch) store_act_chunk(L.row, K, ch, qx[j]);
+        }
+    }
+    lds_barrier();
     terms(-1);
     lds_barrier();
     exact_tail();
@@ -1174,7 +1188,7 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
     // thread 4r + k folds lane k of row r in block order (rows 0..31 gate,
     // 32..63 up) into s_out
     auto fold = [&](int t) {
-        const float acc = seq_sum<16>(T + t * TP, NB);
+        const float acc = seq_sum<32>(T + t * TP, NB);
         const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
         if ((t & 3) == 0) s_out[t >> 2] = res;
     };

@@ -62,6 +62,7 @@ __global__ __launch_bounds__(1024) void k_norm(const uint8_t* __restrict__ a, in
     __shared__ __align__(16) float buf[kNormMaxCols];
     __shared__ float stat[2];
     __shared__ SsShared ssh;
+    __shared__ SgShared sgh;
     const int tid = threadIdx.x;
     const int bs = blockDim.x;
     // a workgroup of 256 threads or more over a multiple of 256 values: the
@@ -95,7 +96,12 @@ __global__ __launch_bounds__(1024) void k_norm(const uint8_t* __restrict__ a, in
         buf[tid + m * bs] = KIND == kRms ? x * x : x;
     }
     __syncthreads();
-    if (KIND == kRms && block_sum) {
+    if (KIND == kLayerNorm && bs == 1024 && n == 2 * 1024) {
+        // the mean of a decode row (Zephyr's final norm): the exact
+        // workgroup sum of the fp16-grid values
+        const float s1 = block_seq_sum_grid<2, 1024>(buf, sgh);
+        if (tid == 0) stat[0] = s1 / (float)n;
+    } else if (KIND == kRms && block_sum) {
         const float s1 = block_seq_sum_nonneg(buf, n, ssh);
         if (tid == 0) {
             stat[0] = 0.0f;
@@ -650,6 +656,26 @@ __global__ __launch_bounds__(kSsThreads) void k_block_seq_sum(const float* __res
     }
 }
 
+// One row of n values per workgroup through the fp16-grid sum (4 values per
+// thread).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_block_seq_sum_grid(const float* __restrict__ x, float* __restrict__ out,
+                                                           int* __restrict__ passes)
+{
+    constexpr int n = 4 * NT;
+    __shared__ __align__(16) float buf[n];
+    __shared__ SgShared sh;
+    const float* xv = x + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += NT) buf[i] = xv[i];
+    __syncthreads();
+    int np = 0;
+    const float s = block_seq_sum_grid<4, NT>(buf, sh, &np);
+    if (threadIdx.x == 0) {
+        out[blockIdx.x] = s;
+        passes[blockIdx.x] = np;
+    }
+}
+
 __global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, int64_t n)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -672,6 +698,67 @@ extern "C" int nc_block_seq_sum(const float* t, int n, int count, float* out, in
     hipLaunchKernelGGL(nc::k_block_seq_sum, dim3(count), dim3(nc::kSsThreads), (size_t)n * 4, stream_of(stream), t, n,
                        out, fast);
     return launch_status("k_block_seq_sum");
+}
+
+// The sequential sum of signed values on the fp16 grid (gten/ops.cpp:673-676)
+// as the fused layer-norm prologues compute it, over `count` rows of n =
+// 1024, 2048 or 2304 values; passes[b] = the parallel passes made (0: the
+// plain loop ran).
+extern "C" int nc_block_seq_sum_grid(const float* x, int n, int count, float* out, int* passes, void* stream)
+{
+    NC_CHECK_ARG(x && out && passes && count >= 0, "block_seq_sum_grid: bad arguments");
+    NC_CHECK_ARG(n == 1024 || n == 2048 || n == 2304, "block_seq_sum_grid: n=%d (1024, 2048 or 2304)", n);
+    if (!count) return NC_OK;
+    hipStream_t st = stream_of(stream);
+    if (n == 1024)
+        hipLaunchKernelGGL(nc::k_block_seq_sum_grid<256>, dim3(count), dim3(256), 0, st, x, out, passes);
+    else if (n == 2048)
+        hipLaunchKernelGGL(nc::k_block_seq_sum_grid<512>, dim3(count), dim3(512), 0, st, x, out, passes);
+    else
+        hipLaunchKernelGGL(nc::k_block_seq_sum_grid<576>, dim3(count), dim3(576), 0, st, x, out, passes);
+    return launch_status("k_block_seq_sum_grid");
+}
+
+// The fp16-grid decomposition on the host: exact double prefixes, then from
+// each rounding step the next one found by a pass over the later steps.
+// plant = 1 plants a mistake (the error after a rounding step is dropped),
+// for tests that must catch it.
+extern "C" float nc_seq_sum_grid_host(const float* x, int n, int plant, int* passes)
+{
+    std::vector<double> P(n + 1, 0.0);
+    bool ok = true;
+    for (int i = 0; i < n; i++) {
+        ok = ok && nc::sg_on_grid(x[i]);
+        P[i + 1] = P[i] + (double)x[i];
+    }
+    int np = 0;
+    if (ok) {
+        double e = 0.0;
+        int r = 0;
+        while (np < nc::kSgMaxPass) {
+            np++;
+            int f = n;
+            for (int i = r; i < n; i++) {
+                const double v = P[i + 1] + e;
+                if ((double)(float)v != v) {
+                    f = i;
+                    break;
+                }
+            }
+            if (f == n) {
+                *passes = np;
+                return (float)(P[n] + e);
+            }
+            const float si = (float)(P[f] + e);
+            const float sn = si + x[f];
+            e = plant ? 0.0 : (double)sn - P[f + 1];
+            r = f + 1;
+        }
+    }
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s = s + x[i];
+    *passes = 0;
+    return s;
 }
 
 // The same segment / crossing decomposition run on the host with the

@@ -26,16 +26,17 @@ bool matvec_f16_glu_supported(const nc_tensor* w);
 int matvec_f16_glu(const uint8_t* x, const nc_tensor* w, uint8_t* m_out, hipStream_t st,
                    hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 
-// Layer norm of one fp16 row fused into the fp16 decode matvec that
-// consumes it (Zephyr, d = 2048): braw != nullptr adds the residual first
-// (a + Act(braw), stored to h_out); the normalized row times w -> fp32 out,
-// or with glu (w the fused gate|up weight) the SwiGLU row -> m_out.  dpos:
-// the a / h_out rows sit at the device-held position.
-bool dmv_f16_ln_supported(const nc_tensor* w, int d, bool glu);
-int dmv_f16_ln_launch(const uint8_t* a, int a_pitch, const float* braw, uint8_t* h_out, int h_pitch,
-                      const uint16_t* nw, const uint16_t* nb, const nc_tensor* w, float* out, uint8_t* m_out,
-                      bool glu, hipStream_t st, const int* dpos = nullptr, hipEvent_t ev_start = nullptr,
-                      hipEvent_t ev_stop = nullptr);
+// The norm of one fp16 row fused into the fp16 decode matvec that consumes
+// it (d = 2048 or 2304): kind 0 layer_norm (nb the bias), 1 rms_norm;
+// braw != nullptr adds the residual first (a + Act(Act(braw) [* bscale]),
+// stored to h_out); the normalized row times w -> fp32 out, or with glu (w
+// the fused gate|up weight) the SwiGLU row -> m_out.  dpos: the a / h_out
+// rows sit at the device-held position.
+bool dmv_f16_nrm_supported(const nc_tensor* w, int d, bool glu);
+int dmv_f16_nrm_launch(int kind, const uint8_t* a, int a_pitch, const float* braw, float bscale, uint8_t* h_out,
+                       int h_pitch, const uint16_t* nw, const uint16_t* nb, const nc_tensor* w, float* out,
+                       uint8_t* m_out, bool glu, hipStream_t st, const int* dpos = nullptr,
+                       hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 
 // x rows times Q4/Q8 weight rows -> fp32 dots on the matrix cores (the
 // reference's block dot product, exact); used by matvec_raw for multi-row

@@ -28,6 +28,8 @@
 // order; the eight lanes of a row meet through wavefront shuffles.
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "nc_kernels.h"
 #include "nc_qdot.h"
 #include "nc_seqsum.h"
@@ -546,85 +548,114 @@ __global__ __launch_bounds__(64) void k_dmv_f16(const uint8_t* __restrict__ x, c
     dmv_f16_finish<GLU>(acc, lane, q, row, N, out, m_out);
 }
 
-// Zephyr's layer norm fused into the fp16 decode matvec that consumes it:
-// every workgroup (8 wavefronts, 64 rows) computes the norm of the row
-// itself while its weight loads are in flight, as
-// k_norm<F16, layer norm> does (gten/ops.cpp:669-698): ADD, the residual sum
-// h = a + Act(braw) (stored to h_out by workgroup 0, the Act row the next
-// residual reads); the mean as the sequential sum on wavefront 0, the
-// variance as the exact workgroup sum of the squared deviations, then
-// y = ((x - mean) / (sqrt(var) + 1e-5)) * w + b rounded to fp16 into the
-// fold's LDS order.  Under graph replay (dpos) the a and h_out rows sit at
-// the device-held position.
-constexpr int kLnThreads = 512;
-template <int G, int D, int P, bool ADD, bool GLU>
-__global__ __launch_bounds__(kLnThreads) void k_dmv_f16_ln(
-    const uint8_t* __restrict__ a, int a_pitch, const float* __restrict__ braw, uint8_t* __restrict__ h_out,
+// The norm of the row fused into the fp16 decode matvec that consumes it
+// (Zephyr's layer_norm, gten/ops.cpp:669-698; the fp16 Llama, MiniCPM and
+// OpenELM models' rms_norm, gten/ops.cpp:830-903).  Threads 0-255 build the
+// row -- ADD: the residual sum h = a + Act(Act(braw) [* bscale], Act) stored
+// to h_out by workgroup 0 -- and compute the norm, synchronizing among
+// themselves through an LDS counter: layer_norm's mean as the exact
+// workgroup sum of the fp16 values (nc_seqsum.h), the variance (or rms_norm's
+// sum of squares) as the exact workgroup sum of non-negative terms, then
+// y = ((x - mean) / (sqrt(var) + 1e-5)) * w + b, or y = x / (sqrt(ss / n) +
+// 1e-6) * w, rounded to fp16 into the fold's LDS order.  The other 512
+// threads (8 wavefronts, 64 rows) issue their whole weight ring at once and
+// fold once the row is there: a wavefront issuing a large transfer waits at
+// the issue until the memory system takes it, so the norm's wavefronts hold
+// no weights.  They issue the ring only once the norm's row loads have
+// returned (a CU serves its loads in order, and rows queued behind the
+// ring's hundreds of KB arrive microseconds late).  Under graph replay
+// (dpos) the a and h_out rows sit at the device-held position.
+constexpr int kNrmNorm = kSsThreads;  // norm threads
+constexpr int kNrmFold = 512;         // fold threads
+enum { kNrmLayer = 0, kNrmRms = 1 };
+
+template <int G, int D, int P, int KIND, bool ADD, bool GLU>
+__global__ __launch_bounds__(kNrmNorm + kNrmFold) void k_dmv_f16_nrm(
+    const uint8_t* __restrict__ a, int a_pitch, const float* __restrict__ braw, float bscale, uint8_t* __restrict__ h_out,
     int h_pitch, const uint16_t* __restrict__ nw, const uint16_t* __restrict__ nb, const uint16_t* __restrict__ w,
     float* __restrict__ out, uint16_t* __restrict__ m_out, int N, const int* __restrict__ dpos)
 {
-    constexpr int K = G * 64, PER = K / kLnThreads;
-    static_assert(K % kLnThreads == 0 && K % kSsThreads == 0, "row width");
+    constexpr int K = G * 64, C = K / kNrmNorm;  // values per norm thread
+    static_assert(K % kNrmNorm == 0 && C <= kSsMaxPer, "row width");
     __shared__ __align__(16) float buf[K];
     __shared__ __align__(16) uint16_t xs[K];
-    __shared__ float s_mean;
+    __shared__ SgShared sgh;
     __shared__ SsShared ssh;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int j = lane & 7, q = (int)blockIdx.x * (kLnThreads / kWave) + tid / kWave;
+    __shared__ int cnt, rows_in;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        cnt = 0;
+        rows_in = 0;
+    }
+    lds_barrier();
+    if (tid < kNrmNorm) {
+        const size_t prow = dpos ? (size_t)load_pos(dpos) : 0;
+        const uint16_t* arow = reinterpret_cast<const uint16_t*>(a + prow * a_pitch);
+        float x[C], g[C], bb[C];
+#pragma unroll
+        for (int k = 0; k < C; k++) {
+            const int e = tid * C + k;
+            x[k] = h2f(arow[e]);
+            g[k] = h2f(nw[e]);
+            bb[k] = KIND == kNrmLayer ? h2f(nb[e]) : 0.0f;
+        }
+        float bw[C];
+        if (ADD) {
+#pragma unroll
+            for (int k = 0; k < C; k++) bw[k] = braw[tid * C + k];
+        }
+        // every row load of this wavefront has returned: the fold's
+        // wavefronts may queue their weights
+        wait_loads_done();
+        if ((tid & (kWave - 1)) == 0) __hip_atomic_fetch_add(&rows_in, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (ADD) {
+#pragma unroll
+            for (int k = 0; k < C; k++) {
+                const int e = tid * C + k;
+                float bv = f16_roundtrip(bw[k]);  // the Linear output as an fp16 Act
+                if (bscale != 1.0f) bv = f16_roundtrip(bv * bscale);
+                const float sm = x[k] + bv;
+                x[k] = f16_roundtrip(sm);
+                if (blockIdx.x == 0) reinterpret_cast<uint16_t*>(h_out + prow * h_pitch)[e] = f2h(sm);
+            }
+        }
+        SsWaveBarrier<kNrmNorm / kWave> bar{&cnt, 0};
+        float mean = 0.0f;
+        if (KIND == kNrmLayer) {
+#pragma unroll
+            for (int k = 0; k < C; k++) buf[tid * C + k] = x[k];
+            bar();
+            mean = block_seq_sum_grid<C, kNrmNorm>(buf, sgh, nullptr, bar) / (float)K;
+#pragma unroll
+            for (int k = 0; k < C; k++) buf[tid * C + k] = (x[k] - mean) * (x[k] - mean);
+        } else {
+#pragma unroll
+            for (int k = 0; k < C; k++) buf[tid * C + k] = x[k] * x[k];
+        }
+        bar();
+        const float ss = block_seq_sum_core<C>(buf, K, ssh, nullptr, bar);
+        const float denom = KIND == kNrmLayer ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
+#pragma unroll
+        for (int k = 0; k < C; k++) {
+            const int e = tid * C + k;
+            const float y = KIND == kNrmLayer ? ((x[k] - mean) / denom) * g[k] + bb[k] : x[k] / denom * g[k];
+            xs[((e >> 6) * 8 + (e & 7)) * 8 + ((e >> 3) & 7)] = f2h(y);
+        }
+        lds_barrier();
+        return;
+    }
+    const int ft = tid - kNrmNorm, lane = tid & (kWave - 1);
+    const int j = lane & 7, q = (int)blockIdx.x * (kNrmFold / kWave) + ft / kWave;
     const int row = dmv_f16_row<GLU>(q, lane >> 3, N);
     const int rowc = row < N ? row : N - 1;  // rows past N read a valid row and store nothing
     const size_t gstride = (size_t)((N + 7) & ~7) * 8;
     const uint4* wrow = reinterpret_cast<const uint4*>(w) + (size_t)rowc * 8 + j;
-    const size_t prow = dpos ? (size_t)dpos[0] : 0;
-    const uint16_t* arow = reinterpret_cast<const uint16_t*>(a + prow * a_pitch);
-    // the row's inputs and the norm's weights first
-    float av[PER], bv[PER], nwv[PER], nbv[PER];
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-        const int e = tid + m * kLnThreads;
-        av[m] = h2f(arow[e]);
-        bv[m] = ADD ? braw[e] : 0.0f;
-        nwv[m] = h2f(nw[e]);
-        nbv[m] = h2f(nb[e]);
-    }
-    float xv[PER];
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-        const int e = tid + m * kLnThreads;
-        float x = av[m];
-        if (ADD) {
-            const float s = x + f16_roundtrip(bv[m]);  // the Linear output as an fp16 Act, then the add
-            x = f16_roundtrip(s);
-            if (blockIdx.x == 0) reinterpret_cast<uint16_t*>(h_out + prow * h_pitch)[e] = f2h(s);
-        }
-        xv[m] = x;
-        buf[e] = x;
-    }
-    __syncthreads();
-    if (tid < kWave) {
-        const float s1 = seq_sum(buf, K);
-        if (tid == 0) s_mean = s1 / (float)K;
-    }
-    // the weight ring: wavefronts 1.. issue theirs while wavefront 0 runs
-    // the mean's chain (a wavefront issuing a large transfer waits at the
-    // issue until the memory system takes it), wavefront 0 after the chain
     uint4 wv[D];
+    while (__hip_atomic_load(&rows_in, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kNrmNorm / kWave)
+        __builtin_amdgcn_s_sleep(2);
 #pragma unroll
     for (int i = 0; i < D; i++) wv[i] = load_stream(wrow + (size_t)i * gstride);
-    __syncthreads();
-    const float mean = s_mean;
-#pragma unroll
-    for (int m = 0; m < PER; m++) buf[tid + m * kLnThreads] = (xv[m] - mean) * (xv[m] - mean);
-    __syncthreads();
-    const float ssq = block_seq_sum_nonneg(buf, K, ssh);
-    const float denom = sqrtf(ssq / (float)K) + 1e-05f;
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-        const int e = tid + m * kLnThreads;
-        const float y = ((xv[m] - mean) / denom) * nwv[m] + nbv[m];
-        xs[((e >> 6) * 8 + (e & 7)) * 8 + ((e >> 3) & 7)] = f2h(y);
-    }
-    __syncthreads();
+    lds_barrier();  // the normalized row is in xs
     const float acc = dmv_f16_fold<G, D, P>(xs, wv, wrow, gstride, j);
     dmv_f16_finish<GLU>(acc, lane, q, row, N, out, m_out);
 }
@@ -751,34 +782,51 @@ int matvec_f16_glu(const uint8_t* x, const nc_tensor* w, uint8_t* m_out, hipStre
     return launch_status("k_dmv_f16<GLU>");
 }
 
-bool dmv_f16_ln_supported(const nc_tensor* w, int d, bool glu)
+bool dmv_f16_nrm_supported(const nc_tensor* w, int d, bool glu)
 {
-    return w->dtype == NC_F16 && w->cols == d && d == 2048 && (!glu || w->rows % 8 == 0);
+    return w->dtype == NC_F16 && w->cols == d && (d == 2048 || d == 2304) && (!glu || w->rows % 8 == 0);
 }
 
-int dmv_f16_ln_launch(const uint8_t* a, int a_pitch, const float* braw, uint8_t* h_out, int h_pitch,
-                      const uint16_t* nw, const uint16_t* nb, const nc_tensor* w, float* out, uint8_t* m_out,
-                      bool glu, hipStream_t st, const int* dpos, hipEvent_t ev_start, hipEvent_t ev_stop)
+int dmv_f16_nrm_launch(int kind, const uint8_t* a, int a_pitch, const float* braw, float bscale, uint8_t* h_out,
+                       int h_pitch, const uint16_t* nw, const uint16_t* nb, const nc_tensor* w, float* out,
+                       uint8_t* m_out, bool glu, hipStream_t st, const int* dpos, hipEvent_t ev_start,
+                       hipEvent_t ev_stop)
 {
     const int N = w->rows, K = w->cols;
-    if (!dmv_f16_ln_supported(w, K, glu))
-        return fail(NC_ERR_ARG, "layer norm + fp16 matvec: [%d x %d] dtype %d", N, K, w->dtype);
-    const int quads = glu ? N / 8 : (N + 7) / 8;  // wavefronts: 8 rows each
-    const dim3 grid((quads + kLnThreads / kWave - 1) / (kLnThreads / kWave));
+    if (!dmv_f16_nrm_supported(w, K, glu) || (kind == kNrmLayer && !nb))
+        return fail(NC_ERR_ARG, "norm + fp16 matvec: [%d x %d] dtype %d", N, K, w->dtype);
+    const int quads = glu ? N / 8 : (N + 7) / 8;  // fold wavefronts: 8 rows each
+    const dim3 grid((quads + kNrmFold / kWave - 1) / (kNrmFold / kWave));
     auto go = [&](auto kern) {
         if (ev_start)
-            hipExtLaunchKernelGGL(kern, grid, dim3(kLnThreads), 0, st, ev_start, ev_stop, 0, a, a_pitch, braw, h_out,
-                                  h_pitch, nw, nb, (const uint16_t*)w->data, out, (uint16_t*)m_out, N, dpos);
+            hipExtLaunchKernelGGL(kern, grid, dim3(kNrmNorm + kNrmFold), 0, st, ev_start, ev_stop, 0, a, a_pitch, braw,
+                                  bscale, h_out, h_pitch, nw, nb, (const uint16_t*)w->data, out, (uint16_t*)m_out, N,
+                                  dpos);
         else
-            hipLaunchKernelGGL(kern, grid, dim3(kLnThreads), 0, st, a, a_pitch, braw, h_out, h_pitch, nw, nb,
-                               (const uint16_t*)w->data, out, (uint16_t*)m_out, N, dpos);
+            hipLaunchKernelGGL(kern, grid, dim3(kNrmNorm + kNrmFold), 0, st, a, a_pitch, braw, bscale, h_out, h_pitch,
+                               nw, nb, (const uint16_t*)w->data, out, (uint16_t*)m_out, N, dpos);
     };
     const bool add = braw != nullptr;
-    if (add && glu) go(k_dmv_f16_ln<32, 32, 8, true, true>);
-    else if (add) go(k_dmv_f16_ln<32, 32, 8, true, false>);
-    else if (glu) go(k_dmv_f16_ln<32, 32, 8, false, true>);
-    else go(k_dmv_f16_ln<32, 32, 8, false, false>);
-    return launch_status("k_dmv_f16_ln");
+    // ADD x GLU for each norm kind and row width (32 or 36 groups of 64;
+    // rows of 36 groups keep 24 in the register ring, the rest refilled
+    // during the fold: a full ring would spill at 768 threads)
+    auto pick = [&](auto kd) {
+        constexpr int KD = decltype(kd)::value;
+        if (K == 2048) {
+            if (add && glu) go(k_dmv_f16_nrm<32, 32, 8, KD, true, true>);
+            else if (add) go(k_dmv_f16_nrm<32, 32, 8, KD, true, false>);
+            else if (glu) go(k_dmv_f16_nrm<32, 32, 8, KD, false, true>);
+            else go(k_dmv_f16_nrm<32, 32, 8, KD, false, false>);
+        } else {
+            if (add && glu) go(k_dmv_f16_nrm<36, 24, 8, KD, true, true>);
+            else if (add) go(k_dmv_f16_nrm<36, 24, 8, KD, true, false>);
+            else if (glu) go(k_dmv_f16_nrm<36, 24, 8, KD, false, true>);
+            else go(k_dmv_f16_nrm<36, 24, 8, KD, false, false>);
+        }
+    };
+    if (kind == kNrmLayer) pick(std::integral_constant<int, kNrmLayer>{});
+    else pick(std::integral_constant<int, kNrmRms>{});
+    return launch_status("k_dmv_f16_nrm");
 }
 
 }  // namespace nc

@@ -175,17 +175,20 @@ public:
         return wb + rows * (xb + 4.0 * N);
     }
 
-    // Zephyr decode row: layer norm (after the residual add when braw) fused
-    // into the fp16 matvec that consumes it; glu: the gate|up product with
-    // the SwiGLU epilogue, m row out.
+    // fp16 decode row: the norm (after the residual add when braw, the
+    // branch scaled as the model scales it) fused into the fp16 matvec that
+    // consumes it; glu: the gate|up product with the SwiGLU epilogue, m row
+    // out.
     int mv_ln(const uint8_t* a, const float* braw, uint8_t* h_out, const uint16_t* nw, const uint16_t* nb,
               const nc_tensor* w, float* out, uint8_t* m_out, bool glu, int role, const int* dpos)
     {
         const int pd = pitch(d);
+        const int kind = norm_kind() == kNormLayer ? 0 : 1;
+        const float bs = branch_scale();
         const bool timed = prof.on && prof.used + 2 <= prof.ev.size();
-        int s = timed ? dmv_f16_ln_launch(a, pd, braw, h_out, pd, nw, nb, w, out, m_out, glu, st, dpos,
-                                          prof.ev[prof.used], prof.ev[prof.used + 1])
-                      : dmv_f16_ln_launch(a, pd, braw, h_out, pd, nw, nb, w, out, m_out, glu, st, dpos);
+        int s = timed ? dmv_f16_nrm_launch(kind, a, pd, braw, bs, h_out, pd, nw, nb, w, out, m_out, glu, st, dpos,
+                                           prof.ev[prof.used], prof.ev[prof.used + 1])
+                      : dmv_f16_nrm_launch(kind, a, pd, braw, bs, h_out, pd, nw, nb, w, out, m_out, glu, st, dpos);
         if (s) return s;
         if (timed) {
             prof.used += 2;
@@ -195,13 +198,13 @@ public:
         return NC_OK;
     }
 
-    // The layer norms of Zephyr's single-row steps run inside the q|k|v and
+    // The norms of an fp16 model's single-row steps run inside the q|k|v and
     // gate|up matvecs (all but the final norm).
     bool ln_fused(int R) const
     {
-        if (R != 1 || adt != NC_F16 || norm_kind() != kNormLayer) return false;
+        if (R != 1 || adt != NC_F16) return false;
         for (int l = 0; l < cfg.n_layers; l++)
-            if (!dmv_f16_ln_supported(&L[l].qkv, d, false) || !dmv_f16_ln_supported(&L[l].gu, d, true)) return false;
+            if (!dmv_f16_nrm_supported(&L[l].qkv, d, false) || !dmv_f16_nrm_supported(&L[l].gu, d, true)) return false;
         return true;
     }
 

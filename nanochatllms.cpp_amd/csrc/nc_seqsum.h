@@ -450,6 +450,191 @@ __device__ __forceinline__ float block_seq_sum_nonneg_waves(const float* t, int 
     return block_seq_sum_core<0>(t, n, sh, nullptr, bar);
 }
 
+// ---------------------------------------------------------------------------
+// The left-to-right fp32 sum of signed values on the fp16 grid (layer_norm's
+// mean, gten/ops.cpp:673-676, over an fp16 or Q8 activation row), computed
+// by a whole workgroup with the sequential loop's result, bit for bit.
+//
+// Why it can be parallel: every value is a multiple of 2^-24 below 2^17 in
+// magnitude (an fp16 value, or a Q8 code times an fp16 delta), so every
+// prefix sum P_i = x_0 + ... + x_{i-1} is exact in fp64 (at most 51
+// significant bits), in any order.  The sequential fp32 sum is s_i = P_i +
+// e_i, where e_i is the rounding error so far; it changes only at the steps
+// whose exact result s_i + x_i is not an fp32 value.  From a step r with
+// known e, every step up to the first i >= r at which P_{i+1} + e is not an
+// fp32 value is exact, and that step is one fp32 add:
+// s_{i+1} = fl(s_i + x_i), e = s_{i+1} - P_{i+1} (exact in fp64).  Sums of
+// 2048 fp16 activations round at 3-10 steps (measured on normal and
+// heavy-tailed rows), so a few parallel passes over the row replace the
+// 2048-step chain.  Values off the grid, or more passes than kSgMaxPass,
+// fall back to the plain loop; the result is exact either way.
+constexpr int kSgMaxPass = 48;
+constexpr int kSgMaxWaves = 16;
+
+struct SgShared {
+    double tot[kSgMaxWaves];            // wavefront totals
+    double err[2][kSgMaxWaves];         // per pass and wavefront: the error after its first rounding step
+    int idx[2][kSgMaxWaves];            // ... and that step (n: none)
+    int bad;
+    float result;
+};
+
+// Lane moves of a double (its halves moved alike).
+template <int CTRL, int ROW_MASK = 0xf, bool BZ = true>
+__device__ __forceinline__ double dpp_d(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)dpp_i<CTRL, ROW_MASK, BZ>((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)dpp_i<CTRL, ROW_MASK, BZ>((int)(uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// Inclusive wave scan of exact doubles (any order is exact here).
+__device__ __forceinline__ double wave_scan_add_d(double v)
+{
+    v = v + dpp_d<0x111>(v);
+    v = v + dpp_d<0x112>(v);
+    v = v + dpp_d<0x114>(v);
+    v = v + dpp_d<0x118>(v);
+    v = v + dpp_d<kDppBcast15, 0xa, false>(v);
+    v = v + dpp_d<kDppBcast31, 0xc, false>(v);
+    return v;
+}
+
+// A value the parallel path takes: finite, |x| < 2^17, a multiple of 2^-24.
+NC_HD bool sg_on_grid(float x)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, x) & 0x7FFFFFFFu;
+    if (u == 0) return true;
+    const int e = (int)(u >> 23);
+    if (e == 0 || e >= 127 + 17) return false;  // subnormal (below 2^-126), too large, inf, NaN
+    // the lowest set bit of the significand, as a power of two
+    const uint32_t m = (u & 0x7FFFFFu) | 0x800000u;
+    return e - 150 + __builtin_ctz(m) >= -24;
+}
+
+// Sum of x[0..n) in index order, n = C * NT, called by threads 0 .. NT-1
+// (NT a multiple of 64, at most 1024), which synchronize through bar; thread
+// t owns x[t C .. t C + C).  Every calling thread returns the sum; *passes
+// (thread 0's view) gets the passes made (0: the plain loop ran).
+template <int C, int NT, class Bar>
+__device__ __forceinline__ float block_seq_sum_grid(const float* x, SgShared& sh, int* passes, Bar& bar)
+{
+    static_assert(NT % kWave == 0 && NT / kWave <= kSgMaxWaves, "workgroup");
+    constexpr int NW = NT / kWave;
+    const int n = C * NT;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+    float v[C];
+    double p[C];  // P at the end of each of this thread's steps
+    bool ok = true;
+    double acc = 0.0;
+#pragma unroll
+    for (int k = 0; k < C; k++) {
+        v[k] = x[tid * C + k];
+        ok = ok && sg_on_grid(v[k]);
+        acc = acc + (double)v[k];
+        p[k] = acc;
+    }
+    const double incl = wave_scan_add_d(acc);
+    if (lane == kWave - 1) sh.tot[w] = incl;
+    if (tid == 0) sh.bad = 0;
+    bar();
+    if (__builtin_amdgcn_ballot_w64(!ok) && lane == 0) sh.bad = 1;
+    double base = incl - acc;  // this thread's first P: the earlier waves' totals, then the lanes'
+#pragma unroll
+    for (int q = 0; q < NW - 1; q++)
+        if (q < w) base = base + sh.tot[q];
+    const double pn = [&] {
+        double t = 0.0;
+#pragma unroll
+        for (int q = 0; q < NW; q++) t = t + sh.tot[q];
+        return t;
+    }();
+#pragma unroll
+    for (int k = 0; k < C; k++) p[k] = p[k] + base;
+    bar();
+    int np = 0;
+    float res = 0.0f;
+    bool done = false;
+    double e = 0.0;
+    int r = 0;
+    // values off the grid go straight to the plain loop
+    while (!done && sh.bad == 0 && np < kSgMaxPass) {
+        // this thread's first step i >= r whose exact result is not an fp32 value
+        int f = n;
+        double en = 0.0;
+#pragma unroll
+        for (int k = C - 1; k >= 0; k--) {
+            const int i = tid * C + k;
+            const double val = p[k] + e;
+            if (i >= r && (double)(float)val != val) {
+                f = i;
+                const float si = (float)((k ? p[k - 1] : base) + e);  // s_i, an fp32 value
+                const float sn = si + v[k];
+                en = (double)sn - p[k];
+            }
+        }
+        // the wavefront's first such step: its lowest lane's (chunks are in
+        // lane order)
+        const uint64_t m = __builtin_amdgcn_ballot_w64(f < n);
+        const int slot = np & 1;
+        int wf = n;
+        double we = 0.0;
+        if (m) {
+            const int fl = __builtin_ctzll(m);
+            wf = __builtin_amdgcn_readlane(f, fl);
+            const uint64_t eb = __builtin_bit_cast(uint64_t, en);
+            const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)eb, fl);
+            const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(eb >> 32), fl);
+            we = __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+        }
+        if (lane == 0) {
+            sh.idx[slot][w] = wf;
+            sh.err[slot][w] = we;
+        }
+        bar();
+        np++;
+        int fi = n;
+        double ei = 0.0;
+#pragma unroll
+        for (int q = NW - 1; q >= 0; q--)
+            if (sh.idx[slot][q] < n) {
+                fi = sh.idx[slot][q];
+                ei = sh.err[slot][q];
+            }
+        if (fi == n) {
+            res = (float)(pn + e);
+            done = true;
+        } else {
+            e = ei;
+            r = fi + 1;
+        }
+    }
+    if (!done) {
+        // off the grid or too many rounding steps: the plain loop
+        if (tid < kWave) {
+            float s = 0.0f;
+            for (int i = 0; i < n; i++) s = s + x[i];
+            if (tid == 0) sh.result = s;
+        }
+        bar();
+        res = sh.result;
+        np = 0;
+    }
+    if (passes && tid == 0) *passes = np;
+    bar();  // sh reusable after return
+    return res;
+}
+
+// The same with the workgroup's LDS barrier (all NT threads of the
+// workgroup call it).
+template <int C, int NT>
+__device__ __forceinline__ float block_seq_sum_grid(const float* x, SgShared& sh, int* passes = nullptr)
+{
+    SsLdsBarrier bar;
+    return block_seq_sum_grid<C, NT>(x, sh, passes, bar);
+}
+
 #endif  // __HIPCC__
 
 }  // namespace nc

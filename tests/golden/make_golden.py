@@ -19,6 +19,7 @@ import hashlib
 import json
 import os
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -26,6 +27,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
+import gten_file as G  # noqa: E402
 import oracle_lib as OL  # noqa: E402
 from workloads import LONG, SMALL, WIDE, config_of, prompt_of  # noqa: E402
 from nc_pkg import nc  # noqa: E402
@@ -50,6 +52,13 @@ def record(name, w, full_logits=False):
     cfg = config_of(w)
     t0 = time.time()
     m = ref.model_create(cfg, w["seed"])
+    if w.get("emb_scale"):
+        # the synthetic weights with the embedding's deltas scaled, read
+        # by the reference's own .gten reader
+        path = os.path.join(tempfile.mkdtemp(), "w.gten")
+        G.write(path, cfg, w["seed"], OL.Oracle(), payload_fn=G.scaled_embedding(w["emb_scale"], cfg.wdtype == OL.Q8))
+        assert ref.model_load_gten(m, os.fsencode(path)) == 0
+        os.remove(path)
     prompt = prompt_of(w)
     adt = OL.F16 if w["wdtype"] == OL.F16 else OL.Q8
     rb = OL.row_bytes(adt, cfg.n_embd)

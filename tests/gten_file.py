@@ -79,6 +79,33 @@ def distinct_vectors(layer, slot, data):
     return v.astype(np.float16).tobytes()
 
 
+def scaled_embedding(factor, q8):
+    """payload_fn scaling the embedding's Q8 (q8) or Q4 block deltas (fp16,
+    rounded to nearest) by factor; other tensors unchanged."""
+    def fn(layer, slot, data):
+        if slot != TID_EMB:
+            return data
+        return scale_block_deltas(np.frombuffer(data, np.uint8), q8, factor).tobytes()
+    return fn
+
+
+def scale_block_deltas(buf, q8, factor):
+    """Q8 (34-byte) or Q4 (18-byte) blocks with every fp16 delta times factor."""
+    blk = np.array(buf, np.uint8).reshape(-1, 34 if q8 else 18)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float32) * np.float32(factor)
+    blk[:, :2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return blk.reshape(-1)
+
+
+def workload_weight(oracle, cfg, w, layer, slot):
+    """Weight (layer, slot) of a workload dict: the synthetic one, with the
+    embedding deltas scaled when the workload has emb_scale."""
+    data = weight_bytes(oracle, cfg, w["seed"], layer, slot)
+    if slot == TID_EMB and w.get("emb_scale"):
+        data = scale_block_deltas(data, cfg.wdtype == OL.Q8, w["emb_scale"])
+    return data
+
+
 def payloads(cfg, seed, oracle, payload_fn=None):
     """{(layer, slot): payload bytes} of every tensor of the model."""
     out = {}

@@ -130,17 +130,28 @@ def greedy_pick(logits):
 
 
 @pytest.mark.parametrize("name", list(SMALL) + list(WIDE) + list(LONG) + FULL)
-def test_decode_steps_match_reference(gpu, name):
+def test_decode_steps_match_reference(gpu, oracle, name):
     """The reference's greedy loop replayed through Model::logits (start_pos
     = n - 1 after the prompt), every step a fused (or op-by-op) decode step
     with direct launches: at the recorded steps the fp32 logits and every
     layer's row at the step's position equal the reference's bit for bit,
     and each step's greedy token is the reference's.  Then the same stream
     through the captured step graph."""
-    reference_loop(gpu, name)
+    reference_loop(gpu, name, oracle)
 
 
-def reference_loop(gpu, name):
+def workload_model(gpu, w, oracle=None):
+    """The device model of a workload dict: synthetic weights, the embedding's
+    deltas scaled when the workload has emb_scale."""
+    m = gpu.Model(config_of(w, cls=gpu.ModelConfig))
+    m.init_synthetic(w["seed"])
+    if w.get("emb_scale"):
+        import gten_file as G
+        m.set_weight(-1, OL.TID_EMB, G.workload_weight(oracle, config_of(w), w, -1, OL.TID_EMB))
+    return m
+
+
+def reference_loop(gpu, name, oracle=None):
     """Model::logits stepped as the reference's greedy loop (start_pos = n -
     1 after the prompt): the prefill digests, the recorded decode steps'
     logits and layer rows and every token must be the reference's; then the
@@ -150,8 +161,7 @@ def reference_loop(gpu, name):
     prompt = prompt_of(w)
     assert prompt.tolist() == g["prompt"]
     cfg = config_of(w)
-    m = gpu.Model(config_of(w, cls=gpu.ModelConfig))
-    m.init_synthetic(w["seed"])
+    m = workload_model(gpu, w, oracle)
     logits = m.logits(prompt, 0)
     assert sha(logits) == g["prefill_logits_sha256"], "prefill logits"
     for l, digest in enumerate(g["layer_out_sha256"]):
@@ -178,8 +188,7 @@ def reference_loop(gpu, name):
         toks.append(t)
     assert seen == set(steps)
     m.close()
-    m = gpu.Model(config_of(w, cls=gpu.ModelConfig))
-    m.init_synthetic(w["seed"])
+    m = workload_model(gpu, w, oracle)
     assert m.generate(prompt, w["gen"]).tolist() == ref
     m.close()
 
@@ -238,3 +247,84 @@ def test_context_limit(gpu):
     w = SMALL["small-llama-q4"]
     with pytest.raises(gpu.HipError, match="max_ctx"):
         gpu.Model(config_of(w, cls=gpu.ModelConfig, max_ctx=gpu.MAX_CTX + 1))
+
+
+def crafted_head(oracle, cfg, seed, layer, slot):
+    """The synthetic lm head (or tied embedding) rewritten so that its logits
+    hold NaN, +0 and exact ties for any input: rows 0-3 and 100-199 all-zero
+    codes (logit +0), rows 4 and 17 NaN deltas (NaN logits), every other row
+    a copy of row 6 (one shared logit, tied at every index)."""
+    import gten_file as G
+    rows, cols, dt = oracle.weight_shape(cfg, layer, slot)
+    rb = OL.row_bytes(dt, cols)
+    W = G.weight_bytes(oracle, cfg, seed, layer, slot).reshape(rows, rb).copy()
+    W[:] = W[6]
+    bsz = 18 if dt == OL.Q4 else 34
+    blk = W.reshape(rows, cols // 32, bsz)
+    zero = 0x77 if dt == OL.Q4 else 0x00  # Q4 code 7 is the value 0
+    for r in list(range(0, 4)) + list(range(100, 200)):
+        blk[r, :, 2:] = zero
+    for r in (4, 17):
+        blk[r, :, 0] = 0x00
+        blk[r, :, 1] = 0x7E  # fp16 NaN delta
+    return np.ascontiguousarray(W.reshape(-1))
+
+
+@pytest.mark.parametrize("name", ["wide-llama-q4", "wide-llama-q8", "small-llama-q4", "wide-minicpm-q4"])
+def test_greedy_pick_with_nan_and_tied_logits(gpu, oracle, name):
+    """The greedy token of each decode step (the fused lm head's argmax
+    epilogue for the wide models, k_argmax_advance after the op-by-op step of
+    the small one) is greedy_sample's scan (src/gten/sampler.cpp:30-41) over
+    logits holding NaN, +0 and exact ties: the first index of the largest
+    non-NaN value.  The oracle runs the same model and scan."""
+    w = ALL[name]
+    cfg = config_of(w)
+    slot = OL.TID_EMB if cfg.arch == OL.MINICPM else OL.TID_LM
+    W = crafted_head(oracle, cfg, w["seed"], -1, slot)
+    m = gpu.Model(config_of(w, cls=gpu.ModelConfig))
+    m.init_synthetic(w["seed"])
+    m.set_weight(-1, slot, W)
+    om = oracle.model_create(cfg, w["seed"])
+    p = oracle.model_weight(om, -1, slot)
+    OL.C.memmove(p, W.ctypes.data, W.nbytes)
+    prompt = prompt_of(w)
+    n_gen = 12
+    logits = m.logits(prompt, 0)
+    assert np.isnan(logits[4]) and np.isnan(logits[17]) and logits[100] == 0.0
+    assert logits[5] == logits[8] == logits[6]
+    want = np.zeros(n_gen, np.int32)
+    n = oracle.generate_greedy(om, OL.ptr(prompt), len(prompt), n_gen, OL.ptr(want))
+    oracle.model_free(om)
+    got = m.generate(prompt, n_gen)
+    m.close()
+    assert got.tolist() == want[:n].tolist()
+    # the first +0 row, or the first shared row (after the NaN row 4)
+    assert set(got.tolist()) <= {0, 5}
+
+
+@pytest.mark.parametrize("case", ["signed_zeros", "nan_first", "nan_between", "all_nan", "neg_inf"])
+def test_argmax_nan_and_signed_zero(gpu, oracle, case):
+    """nc_argmax (the prefill's greedy pick) over NaN, -inf and +-0: the
+    first index of the largest value greedy_sample's `val > max` scan takes."""
+    import ctypes as C
+    from devutil import dev_array
+    n = 5000
+    rng = np.random.default_rng(3)
+    x = -np.abs(rng.standard_normal(n)).astype(np.float32) - 1.0
+    if case == "signed_zeros":
+        x[10], x[20], x[30] = -0.0, 0.0, -0.0  # -0 ties with +0: index 10
+    elif case == "nan_first":
+        x[0], x[1], x[2] = np.nan, np.nan, -0.5
+    elif case == "nan_between":
+        x[100], x[101], x[4000] = 2.0, np.nan, 2.0
+    elif case == "all_nan":
+        x[:] = np.nan
+    elif case == "neg_inf":
+        x[:] = -np.inf
+        x[4321] = np.nan
+    dx = dev_array(x)
+    out = np.zeros(1, np.int32)
+    dout = dev_array(out)
+    gpu.check(gpu.lib().nc_argmax(C.c_void_p(dx.ptr), n, C.c_void_p(dout.ptr), None), "argmax")
+    dout.download(out)
+    assert out[0] == oracle.argmax(OL.ptr(x), n) == greedy_pick(x)

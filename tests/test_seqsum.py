@@ -150,3 +150,131 @@ def test_block_seq_sum_device(gpu, oracle, n):
     real = [fast[i] for i in range(cnt) if names[i] == "q8_rows"]
     floor = 0.99 if n <= 2304 else 0.95
     assert sum(real) >= floor * len(real), f"parallel path taken for {sum(real)} of {len(real)} realistic rows"
+
+
+# ---- layer_norm's mean: the left-to-right fp32 sum of signed fp16-grid values
+# (gten/ops.cpp:673-676), computed from exact double prefixes and the few
+# steps that round.
+
+GRID_SIZES = [1024, 2048, 2304]
+
+
+def grid_rows(n, rng):
+    """Named rows of n signed values on the fp16 grid (fp16 activations and
+    Q8 codes times fp16 deltas), some built to round often or to leave the
+    grid (those must take the plain loop)."""
+    out = {}
+    f16 = lambda a: np.asarray(a, np.float16).astype(np.float32)
+    out["f16_normal"] = f16(rng.standard_normal(n))
+    out["f16_small"] = f16(rng.normal(0, 0.05, n))
+    out["f16_heavy_tail"] = f16(rng.standard_t(3, n) * 0.3)
+    out["f16_outliers"] = f16(np.where(rng.random(n) < 0.01, rng.normal(0, 300, n), rng.normal(0, 1, n)))
+    out["f16_max"] = f16(np.where(rng.random(n) < 0.5, 65504.0, -65504.0) * (rng.random(n) < 0.1))
+    out["f16_subnormal_mix"] = f16(np.where(rng.random(n) < 0.5, rng.normal(0, 1e-6, n), rng.normal(0, 50, n)))
+    up = f16(np.abs(rng.normal(0, 1, n)))
+    out["f16_growing"] = up  # the running sum grows through many binades
+    alt = f16(rng.normal(0, 1, n))
+    alt[::2] = 1000.0
+    alt[1::2] = -1000.0 + alt[1::2] * 1e-3
+    out["f16_cancelling"] = f16(alt)
+    q = rng.integers(-127, 128, n).astype(np.float32)
+    d = f16(rng.uniform(1e-3, 0.05, n // 32))
+    out["q8_row"] = q * np.repeat(d, 32)
+    out["zeros"] = np.zeros(n, np.float32)
+    # a large value, a few small ones that round on its grid (ties to even
+    # keep 1024; the mixed row rounds both ways), then small integers that
+    # add exactly: the error carried from the rounding steps decides the
+    # result
+    ab = rng.integers(-3, 4, n).astype(np.float32)
+    ab[0] = 1024.0
+    ab[1:11] = 2.0 ** -14
+    out["absorbed"] = ab
+    mix = rng.integers(-3, 4, n).astype(np.float32)
+    mix[0] = 1536.0
+    mix[1:13] = f16(2.0 ** rng.integers(-16, -12, 12) * rng.choice([-3.0, -1.0, 1.0, 3.0], 12))
+    out["absorbed_mixed"] = mix
+    off = f16(rng.standard_normal(n))
+    off[n // 2] = np.float32(3.0 * 2.0 ** -30)  # not a multiple of 2^-24: plain loop
+    out["off_grid"] = off
+    big = f16(rng.standard_normal(n))
+    big[n // 3] = np.float32(2.0 ** 18)  # beyond the grid's range: plain loop
+    out["too_large"] = big
+    inf = f16(rng.standard_normal(n))
+    inf[n // 4] = np.inf
+    out["inf"] = inf
+    return out
+
+
+def grid_host(nc):
+    f = nc.lib().nc_seq_sum_grid_host
+    f.restype = C.c_float
+    f.argtypes = [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_int)]
+    return f
+
+
+@pytest.mark.parametrize("n", GRID_SIZES)
+def test_grid_sum_host_equals_sequential_sum(nc, oracle, n):
+    f = grid_host(nc)
+    rng = np.random.default_rng(500 + n)
+    passes = []
+    for rep in range(10):
+        for name, x in grid_rows(n, rng).items():
+            x = np.ascontiguousarray(x, np.float32)
+            want = oracle.seq_sum(x.ctypes.data_as(C.c_void_p), n)
+            p = C.c_int()
+            got = f(x.ctypes.data_as(C.c_void_p), n, 0, C.byref(p))
+            assert same(got, want), (name, n, rep, got, want)
+            if name in ("off_grid", "too_large", "inf"):
+                assert p.value == 0, name  # the plain loop ran
+            elif name.startswith("f16_normal"):
+                passes.append(p.value)
+    # realistic rows round at a few steps: a few passes each
+    assert 1 <= np.mean(passes) <= 16, passes
+
+
+def test_grid_sum_planted_mistake_is_caught(nc, oracle):
+    """Dropping the rounding error after a rounding step (a planted mistake
+    in the host run) must change results on these rows: the test above has
+    teeth."""
+    f = grid_host(nc)
+    rng = np.random.default_rng(9)
+    wrong = 0
+    for rep in range(20):
+        for name in ("absorbed", "absorbed_mixed"):
+            x = np.ascontiguousarray(grid_rows(2048, rng)[name])
+            want = oracle.seq_sum(x.ctypes.data_as(C.c_void_p), 2048)
+            p = C.c_int()
+            wrong += not same(f(x.ctypes.data_as(C.c_void_p), 2048, 1, C.byref(p)), want)
+    assert wrong >= 20, wrong
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", GRID_SIZES)
+def test_grid_sum_device(gpu, oracle, n):
+    L = gpu.lib()
+    rng = np.random.default_rng(700 + n)
+    names, rows = [], []
+    for rep in range(60):
+        for name, x in grid_rows(n, rng).items():
+            names.append(name)
+            rows.append(x)
+    X = np.ascontiguousarray(np.stack(rows).astype(np.float32))
+    cnt = X.shape[0]
+    dx = dev_array(X)
+    dout = NC.DeviceBuffer(cnt * 4)
+    dpass = NC.DeviceBuffer(cnt * 4)
+    NC.check(L.nc_block_seq_sum_grid(C.c_void_p(dx.ptr), n, cnt, C.c_void_p(dout.ptr), C.c_void_p(dpass.ptr), None))
+    sync()
+    out = np.zeros(cnt, np.float32)
+    passes = np.zeros(cnt, np.int32)
+    dout.download(out)
+    dpass.download(passes)
+    host = grid_host(gpu)
+    bad = []
+    for i in range(cnt):
+        want = oracle.seq_sum(X[i].ctypes.data_as(C.c_void_p), n)
+        hp = C.c_int()
+        host(X[i].ctypes.data_as(C.c_void_p), n, 0, C.byref(hp))
+        if not same(out[i], want) or passes[i] != hp.value:
+            bad.append((i, names[i], float(out[i]), float(want), int(passes[i]), hp.value))
+    assert not bad, bad[:5]

@@ -45,6 +45,15 @@ WIDE = {
     # MiniCPM's own vocabulary: its tied lm head runs the row-chain kernel
     "wide-minicpm-q4": dict(arch=nc.MINICPM, wdtype=nc.Q4, n_vocab=122753, n_embd=2304, n_layers=2, n_heads=36,
                             n_kv_heads=36, n_ffn=5760, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0003),
+    # the same with its tied embedding scaled by 1/64 (fp16 block deltas;
+    # emb_scale): the synthetic embedding otherwise dominates the residual
+    # stream, and a tied head then repeats the last prompt token forever; at
+    # this scale the greedy stream varies from the fifth step, so the decode
+    # graph's next-step embedding (x12, written by the lm head) sees changing
+    # tokens
+    "wide-minicpm-q4-varied": dict(arch=nc.MINICPM, wdtype=nc.Q4, n_vocab=122753, n_embd=2304, n_layers=2,
+                                   n_heads=36, n_kv_heads=36, n_ffn=5760, eos=-1, rope_pct=1.0, prompt=16, gen=16,
+                                   seed=0x7EE0003, emb_scale=1.0 / 64),
     # fp16 at MiniCPM's widths: the unrolled fp16 decode matvec for rows of
     # 2304 and 5760 values, its SwiGLU epilogue, and the tied 122753-row head
     "wide-minicpm-f16": dict(arch=nc.MINICPM, wdtype=nc.F16, n_vocab=122753, n_embd=2304, n_layers=2, n_heads=36,
