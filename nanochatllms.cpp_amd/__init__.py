@@ -73,6 +73,11 @@ WORKLOADS = {
     "openelm-q8": dict(arch=OPENELM, wdtype=Q8, n_vocab=32000, n_embd=2048, n_layers=28,
                        n_heads=[16] * 12 + [20] * 16, n_kv_heads=[4] * 12 + [5] * 16, n_ffn=_ELM_F,
                        eos=32002, rope_pct=1.0, prompt=64, gen=256, seed=0x5EED0005),
+    # the reference's other published rows (README.md:36-44) at full size
+    "tinyllama-f16": dict(arch=LLAMA, wdtype=F16, n_vocab=32000, n_embd=2048, n_layers=22, n_heads=32,
+                          n_kv_heads=4, n_ffn=5632, eos=32002, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0001),
+    "zephyr-q4": dict(arch=ZEPHYR, wdtype=Q4, n_vocab=100352, n_embd=2048, n_layers=24, n_heads=32,
+                      n_kv_heads=32, n_ffn=5632, eos=100257, rope_pct=0.25, prompt=128, gen=128, seed=0x5EED0003),
 }
 PROMPT_SEED_OFFSET = 0x1000
 

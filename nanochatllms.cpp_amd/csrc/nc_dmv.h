@@ -1,0 +1,488 @@
+// nc_dmv.h -- device code shared by the fused matvec kernels of the
+// single-row decode step (nc_decode.hip: k_dmv, k_dmv_head; nc_decode_glu.hip:
+// the gate|up kernels): Q8 activation chunks, the norm prologue and the
+// speculative-norm driver, plus the launch entry of the gate|up kernels.
+#pragma once
+
+#include <hip/hip_ext.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "nc_act.h"
+#include "nc_decode.h"
+#include "nc_qdot.h"
+#include "nc_seqsum.h"
+
+namespace nc {
+
+constexpr int kDmvThreads = 256;
+constexpr int kDmvMaxItems = 12;    // weight blocks per thread and row group
+constexpr int kDmvNormChunks = 2;   // norm prologues: 8-value chunks per thread (NCH <= 2: K <= 4096)
+constexpr int kDmvMaxGrid = 4096;
+
+// Q8 round trip of 8 values of one block held by a lane quad:
+// q8_quantize_block (gten/quants.cpp:16-30) -- absmax, delta = absmax/127,
+// fp16 delta stored, scale 1/delta from the fp32 delta, roundf -- and the
+// read back (code * fp16 delta).  Codes and delta returned for storing.
+struct Q8Chunk {
+    int8_t q[8];
+    uint16_t d16;
+};
+
+__device__ __forceinline__ Q8Chunk quad_quantize(const float (&v)[8])
+{
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+    a = quad_max(a);
+    const float delta = a / 127.0f;
+    Q8Chunk r;
+    r.d16 = f2h(delta);
+    const float scale = delta != 0.0f ? 1.0f / delta : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.q[i] = (int8_t)roundf(v[i] * scale);
+    return r;
+}
+
+__device__ __forceinline__ void quad_roundtrip(float (&v)[8])
+{
+    const Q8Chunk c = quad_quantize(v);
+    const float d = h2f(c.d16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)c.q[i] * d;
+}
+
+// Chunk ch (values 8ch .. 8ch+7) of a Q8 Act row of K values.
+__device__ __forceinline__ void load_act_chunk(const uint8_t* row, int K, int ch, float (&v)[8])
+{
+    const uint2 q = *reinterpret_cast<const uint2*>(row + (size_t)ch * 8);
+    const float d = h2f(reinterpret_cast<const uint16_t*>(row + K)[ch >> 2]);
+    const uint32_t w[2] = {q.x, q.y};
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)(int8_t)((w[i >> 2] >> (8 * (i & 3))) & 0xFFu) * d;
+}
+
+__device__ __forceinline__ void store_act_chunk(uint8_t* row, int K, int ch, const Q8Chunk& c)
+{
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)c.q[i] << (8 * (i & 3));
+    *reinterpret_cast<uint2*>(row + (size_t)ch * 8) = make_uint2(w[0], w[1]);
+    if ((ch & 3) == 0) reinterpret_cast<uint16_t*>(row + K)[ch >> 2] = c.d16;
+}
+
+__device__ __forceinline__ void load_f32_chunk(const float* p, int ch, float (&v)[8])
+{
+    const float4 a = reinterpret_cast<const float4*>(p)[2 * ch];
+    const float4 b = reinterpret_cast<const float4*>(p)[2 * ch + 1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// The prologue: builds the activation row the matvec consumes and stages
+// it in LDS by AVX lane (xs).  The inputs are requested first, then
+// load_w() requests the workgroup's first weights, and the row is built
+// while the weights are in flight (LDS barriers do not wait for global
+// loads).  sq: K floats of LDS for the squares and the Act row.  Ends with
+// an LDS barrier.  ROWS_FIRST (norm prologues): the weights are requested
+// only once the rows have arrived -- a launch that requests tens of MB
+// would otherwise queue its rows behind its own weights.
+template <int PRO, int NCH, bool ROWS_FIRST = false, int NT = kDmvThreads, class LoadW>
+__device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, LoadW&& load_w)
+{
+    const int tid = threadIdx.x;
+    const int nb = A.nb, K = nb * 32;
+    const int nch = K / 8;
+    uint8_t* xq = reinterpret_cast<uint8_t*>(sq);
+    if (PRO == PRO_X) {
+        XRaw xr{};
+        if (tid < nb) xr = load_x_block(A.x, nb, tid);
+        // scheduling fences keep the row's loads first and every weight
+        // load issued before anything waits on the row
+        __builtin_amdgcn_sched_barrier(0);
+        load_w();
+        __builtin_amdgcn_sched_barrier(0);
+        if (tid < nb) stage_x_block(xr, xs + tid * kStage);
+        lds_barrier();
+        return A.pos;  // not used after a PRO_X prologue
+    } else {
+        // h: the stored row (PRO_RMS) or the residual sum (PRO_RES_RMS)
+        float h[NCH][8], gain[NCH][8];
+        float av[NCH][8], ov[NCH][8];
+        // A row at a fixed address (x_pitch = 0, res_cur) is requested
+        // before the position: the position is then loaded after the row
+        // and before the weights, so waiting for it does not wait for them.
+        const bool fixed = PRO == PRO_RMS ? A.x_pitch == 0 : A.res_cur != nullptr;
+        int pos = A.pos;
+        const uint8_t* arow;
+        if (fixed) {
+            arow = PRO == PRO_RMS ? A.x : A.res_cur;
+        } else {
+            if (A.dpos) pos = load_pos(A.dpos);
+            arow = PRO == PRO_RMS ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
+        }
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            const int cc = ch < nch ? ch : 0;
+            load_act_chunk(arow, K, cc, av[j]);
+            if (PRO == PRO_RES_RMS) load_f32_chunk(A.raw_in, cc, ov[j]);
+            const uint4 gw = reinterpret_cast<const uint4*>(A.norm_w)[cc];
+            const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        int posv = 0;
+        if (fixed && A.dpos) posv = load_pos(A.dpos);
+        if (ROWS_FIRST) wait_loads_done();
+        __builtin_amdgcn_sched_barrier(0);
+        load_w();
+        __builtin_amdgcn_sched_barrier(0);
+        if (fixed && A.dpos) pos = posv;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            const bool valid = ch < nch;
+            if (j * NT >= nch) break;  // uniform
+            if (PRO == PRO_RES_RMS) {
+                quad_roundtrip(ov[j]);
+                if (A.bscale != 1.0f) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) ov[j][i] = ov[j][i] * A.bscale;
+                    quad_roundtrip(ov[j]);
+                }
+                float s[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) s[i] = av[j][i] + ov[j][i];
+                const Q8Chunk q = quad_quantize(s);
+                if (valid && blockIdx.x == 0) {
+                    store_act_chunk(A.res_out + (size_t)pos * A.res_pitch, K, ch, q);
+                    if (A.res_cur_out) store_act_chunk(A.res_cur_out, K, ch, q);
+                }
+                const float d = h2f(q.d16);
+#pragma unroll
+                for (int i = 0; i < 8; i++) h[j][i] = (float)q.q[i] * d;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) h[j][i] = av[j][i];
+            }
+            if (valid) {
+                const float4 s0 = make_float4(h[j][0] * h[j][0], h[j][1] * h[j][1], h[j][2] * h[j][2], h[j][3] * h[j][3]);
+                const float4 s1 = make_float4(h[j][4] * h[j][4], h[j][5] * h[j][5], h[j][6] * h[j][6], h[j][7] * h[j][7]);
+                reinterpret_cast<float4*>(sq)[2 * ch] = s0;
+                reinterpret_cast<float4*>(sq)[2 * ch + 1] = s1;
+            }
+        }
+        lds_barrier();
+        const float ss = block_seq_sum_nonneg(sq, K, ssh);
+        const float denom = sqrtf(ss / (float)K) + 1e-6f;
+        // the normalized row as stored (codes, then deltas) over sq's bytes
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            if (j * NT >= nch) break;  // uniform
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) y[i] = h[j][i] / denom * gain[j][i];
+            if (A.post_scale != 1.0f) {
+                quad_roundtrip(y);
+#pragma unroll
+                for (int i = 0; i < 8; i++) y[i] = y[i] * A.post_scale;
+            }
+            const Q8Chunk q = quad_quantize(y);
+            if (ch < nch) store_act_chunk(xq, K, ch, q);
+        }
+        lds_barrier();
+        if (tid < nb) stage_x_block(load_x_block(xq, nb, tid), xs + tid * kStage);
+        lds_barrier();
+        return pos;
+    }
+}
+
+constexpr int kGluThreads = 512;  // gate|up workgroup: 64 rows' block terms over 8 wavefronts
+constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / threads, NB <= 72
+
+// ================================================ speculative norm rows ==
+// The norm-prologue launches (q|k|v, gate|up) with the weight-block terms
+// computed beside the exact sum of squares instead of after it.  Threads
+// 0-255 build the row and run the exact rms_norm as dmv_prologue does,
+// synchronizing among themselves through an LDS counter; the other threads
+// (256 or 512 more) hold the weights.  While the exact sum runs they
+// normalize the row with an approximate sum of squares (any order),
+// quantize it and compute every weight block's four terms against that row
+// as the weights arrive.  Once the exact sum is known, threads 0-255
+// quantize the exact row and compare it with the speculative one block by
+// block.  A block's terms are a function of its 32 codes and its fp16 delta
+// alone, so where those match the speculative terms are the exact ones; the
+// weight threads recompute the terms of every block that differs.  The fold
+// then sees the terms of the exact row, and the result is the reference's
+// bit for bit whatever the approximation was.  (With unit norm gains the
+// normalized row is a rescaled Q8 row, and requantizing it meets exact ties
+// that the last bit of the rms decides: a few blocks per row differ there.)
+constexpr int kSpecExact = kSsThreads;  // threads of the exact path
+
+// Dynamic LDS of the speculative prologue (after the kernel's fold terms).
+struct SpecLds {
+    float* sq;     // K squares of the row (the exact sum's terms)
+    float* h;      // K values of the row before the norm
+    float* g;      // K norm gains
+    uint8_t* row;  // the speculative Act row, then the exact one: K codes, nb fp16 deltas
+    uint8_t* bad;  // nb flags: the block differs between the two rows
+};
+
+__host__ __device__ constexpr size_t spec_lds_bytes(int nb)
+{
+    return (size_t)nb * 32 * 4 * 3 + (((size_t)nb * 34 + 15) & ~(size_t)15) + (((size_t)nb + 15) & ~(size_t)15);
+}
+
+__device__ __forceinline__ SpecLds spec_lds(float* base, int nb)
+{
+    const int K = nb * 32;
+    SpecLds L;
+    L.sq = base;
+    L.h = base + K;
+    L.g = base + 2 * K;
+    L.row = reinterpret_cast<uint8_t*>(base + 3 * K);
+    L.bad = L.row + ((nb * 34 + 15) & ~15);
+    return L;
+}
+
+// Sum of the K squares in some order (a prediction only), the same value on
+// every lane of every wavefront that calls it: lane l adds K/64 terms, then
+// a butterfly, then lane 0's value.
+__device__ __forceinline__ float spec_approx_sum(const float* sq, int K)
+{
+    const int lane = threadIdx.x & (kWave - 1), c = K / kWave;
+    float v = 0.0f;
+    for (int k = 0; k < c; k += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(sq + lane * c + k);
+        v = v + ((q.x + q.y) + (q.z + q.w));
+    }
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) v = v + __shfl_xor(v, o);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// y = h / denom * g (then the post scale's round trip), quantized: the
+// rms_norm of dmv_prologue for one 8-value chunk.
+__device__ __forceinline__ Q8Chunk spec_norm_chunk(const float (&h)[8], const float (&g)[8], float denom, float post)
+{
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = h[i] / denom * g[i];
+    if (post != 1.0f) {
+        quad_roundtrip(y);
+#pragma unroll
+        for (int i = 0; i < 8; i++) y[i] = y[i] * post;
+    }
+    return quad_quantize(y);
+}
+
+// LDS state of the two sides.
+struct SpecSync {
+    int exact;    // barrier counter of threads 0-255 (the exact sum)
+    int spec;     // barrier counter of the weight threads
+    int anybad;   // some block differs: the speculative results are void
+    float wsum[kSpecExact / kWave];  // per exact wavefront: its part of the squares (the prediction)
+};
+
+// The whole norm-prologue matvec but its final stores.  load_w(): the weight
+// threads' weight requests (a no-op on threads 0-255).  terms(ph): the
+// weight threads' block terms, ph = 1 (every item, from the speculative
+// row) or -1 (the items of the blocks that differ, from the exact row).
+// spec_tail(bar): the weight threads' fold and epilogue from the
+// speculative terms, held back (bar: their barrier, after every term is
+// stored).  commit(): stores the held results, when every block matched.
+// exact_tail(): otherwise, after the differing terms were recomputed: the
+// fold and epilogue from the exact terms.  NS: weight threads.
+template <int PRO, int NCH, int NS, class LoadW, class Terms, class SpecTail, class Commit, class ExactTail>
+__device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsShared& ssh, SpecSync& sy, LoadW&& load_w,
+                                         Terms&& terms, SpecTail&& spec_tail, Commit&& commit, ExactTail&& exact_tail)
+{
+    constexpr int NT = kSpecExact;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int nb = A.nb, K = nb * 32;
+    const int nch = K / 8;
+    const bool ex = tid < NT;
+    float h[NCH][8], gain[NCH][8], av[NCH][8], ov[NCH][8];
+    const bool fixed = PRO == PRO_RMS ? A.x_pitch == 0 : A.res_cur != nullptr;
+    int pos = A.pos;
+    if (tid == 0) {
+        sy.exact = 0;
+        sy.spec = 0;
+        sy.anybad = 0;
+    }
+    if (ex) {
+        // the exact side is the critical path: its wavefronts issue first
+        __builtin_amdgcn_s_setprio(3);
+        const uint8_t* arow;
+        if (fixed) {
+            arow = PRO == PRO_RMS ? A.x : A.res_cur;
+        } else {
+            if (A.dpos) pos = load_pos(A.dpos);
+            arow = PRO == PRO_RMS ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
+        }
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            const int cc = ch < nch ? ch : 0;
+            load_act_chunk(arow, K, cc, av[j]);
+            if (PRO == PRO_RES_RMS) load_f32_chunk(A.raw_in, cc, ov[j]);
+            const uint4 gw = reinterpret_cast<const uint4*>(A.norm_w)[cc];
+            const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    int posv = 0;
+    if (ex && fixed && A.dpos) posv = load_pos(A.dpos);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w();
+    __builtin_amdgcn_sched_barrier(0);
+    if (ex) {
+        if (fixed && A.dpos) pos = posv;
+        float part = 0.0f;  // this thread's squares, for the prediction
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            const bool valid = ch < nch;
+            if (j * NT >= nch) break;  // uniform
+            if (PRO == PRO_RES_RMS) {
+                quad_roundtrip(ov[j]);
+                if (A.bscale != 1.0f) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) ov[j][i] = ov[j][i] * A.bscale;
+                    quad_roundtrip(ov[j]);
+                }
+                float sm[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) sm[i] = av[j][i] + ov[j][i];
+                const Q8Chunk q = quad_quantize(sm);
+                if (valid && blockIdx.x == 0) {
+                    store_act_chunk(A.res_out + (size_t)pos * A.res_pitch, K, ch, q);
+                    if (A.res_cur_out) store_act_chunk(A.res_cur_out, K, ch, q);
+                }
+                const float d = h2f(q.d16);
+#pragma unroll
+                for (int i = 0; i < 8; i++) h[j][i] = (float)q.q[i] * d;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) h[j][i] = av[j][i];
+            }
+            if (valid) {
+                float sqv[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) sqv[i] = h[j][i] * h[j][i];
+                float4* sq4 = reinterpret_cast<float4*>(L.sq) + 2 * ch;
+                sq4[0] = make_float4(sqv[0], sqv[1], sqv[2], sqv[3]);
+                sq4[1] = make_float4(sqv[4], sqv[5], sqv[6], sqv[7]);
+                part = part + (((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + ((sqv[4] + sqv[5]) + (sqv[6] + sqv[7])));
+                float4* h4 = reinterpret_cast<float4*>(L.h) + 2 * ch;
+                h4[0] = make_float4(h[j][0], h[j][1], h[j][2], h[j][3]);
+                h4[1] = make_float4(h[j][4], h[j][5], h[j][6], h[j][7]);
+                float4* g4 = reinterpret_cast<float4*>(L.g) + 2 * ch;
+                g4[0] = make_float4(gain[j][0], gain[j][1], gain[j][2], gain[j][3]);
+                g4[1] = make_float4(gain[j][4], gain[j][5], gain[j][6], gain[j][7]);
+            }
+        }
+        part = wave_scan_add(part);
+        if (lane == kWave - 1) sy.wsum[tid / kWave] = part;
+    }
+    lds_barrier();
+    Q8Chunk qx[NCH];
+    if (ex) {
+        // the exact sum on threads 0-255, then the exact row (held until the
+        // speculative side is done)
+        const float ss = block_seq_sum_nonneg_waves(L.sq, K, ssh, &sy.exact);
+        const float denom = sqrtf(ss / (float)K) + 1e-6f;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            if (j * NT >= nch) break;  // uniform
+            qx[j] = spec_norm_chunk(h[j], gain[j], denom, A.post_scale);
+        }
+        // once the speculative row is complete (every weight wavefront has
+        // passed its first barrier), compare it block by block with the
+        // exact one (a lane quad holds a block) while the weight threads
+        // finish
+        while (__hip_atomic_load(&sy.spec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NS / kWave) {
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        int any = 0;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            if (j * NT >= nch) break;  // uniform
+            const bool valid = ch < nch;
+            const int cc = valid ? ch : 0;
+            const Q8Chunk& q = qx[j];
+            const uint2 sc = *reinterpret_cast<const uint2*>(L.row + (size_t)cc * 8);
+            const uint16_t sd = reinterpret_cast<const uint16_t*>(L.row + K)[cc >> 2];
+            uint32_t w[2] = {0, 0};
+#pragma unroll
+            for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q.q[i] << (8 * (i & 3));
+            int diff = valid && (sc.x != w[0] || sc.y != w[1] || sd != q.d16) ? 1 : 0;
+            diff |= dpp_i<kDppQuadXor1>(diff);
+            diff |= dpp_i<kDppQuadXor2>(diff);
+            any |= diff;
+            if (valid && (ch & 3) == 0) L.bad[ch >> 2] = (uint8_t)diff;
+        }
+        if (__builtin_amdgcn_ballot_w64(any != 0) && lane == 0) sy.anybad = 1;
+        __builtin_amdgcn_s_setprio(0);
+    } else {
+        // the speculative row (weight threads 0-255, a quad per block), a
+        // barrier among the weight threads, every block's terms, then the
+        // fold and epilogue
+        const int sc = tid - NT;
+        if (sc < NT) {
+            const float approx = (((sy.wsum[0] + sy.wsum[1]) + sy.wsum[2]) + sy.wsum[3]) * A.spec_skew;
+            const float dn = sqrtf(approx / (float)K) + 1e-6f;
+#pragma unroll
+            for (int j = 0; j < NCH; j++) {
+                const int ch = sc + j * NT;
+                if (j * NT >= nch) break;  // uniform
+                const int cc = ch < nch ? ch : 0;
+                float hv[8], gv[8];
+                load_f32_chunk(L.h, cc, hv);
+                load_f32_chunk(L.g, cc, gv);
+                const Q8Chunk q = spec_norm_chunk(hv, gv, dn, A.post_scale);
+                if (ch < nch) store_act_chunk(L.row, K, ch, q);
+            }
+        }
+        SsWaveBarrier<NS / kWave> sbar{&sy.spec, 0};
+        sbar();
+        terms(1);
+        spec_tail(sbar);
+    }
+    lds_barrier();
+    if (!sy.anybad) {
+        commit();
+        return;
+    }
+    // some block differs: the exact row over the speculative one, the
+    // differing blocks' terms recomputed, and the fold and epilogue again
+    if (A.spec_fixups && tid == 0) atomicAdd(A.spec_fixups, 1);
+    if (ex) {
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int ch = tid + j * NT;
+            if (j * NT >= nch) break;  // uniform
+            if (ch < nch) store_act_chunk(L.row, K, ch, qx[j]);
+        }
+    }
+    lds_barrier();
+    terms(-1);
+    lds_barrier();
+    exact_tail();
+}
+
+// Compute units of the current device.
+int device_cus();
+
+// The gate|up launch with the SwiGLU epilogue (nc_decode_glu.hip): K = 32 nb
+// of 2048 or 2304, a norm prologue (PRO_RMS or PRO_RES_RMS).
+int glu_dispatch(const DmvArgs& A, int wdtype, int pro, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+
+}  // namespace nc
