@@ -13,10 +13,17 @@ namespace nc {
 //   PRO_RES_RMS h = Act(res_in[pos] + Act(raw_in [* bscale])) -- the
 //               residual add of the previous Linear's output -- stored to
 //               res_out[pos], then rms_norm(h) as PRO_RMS
-// PRO_RMS with x_pitch = 0 reads the row at x itself, and PRO_RES_RMS with
-// res_cur set reads the residual row there: rows at a fixed address, so the
-// first loads do not wait for the position.
-enum DmvPrologue { PRO_X = 0, PRO_RMS = 1, PRO_RES_RMS = 2 };
+//   PRO_LN, PRO_RES_LN  the same with layer_norm (gain norm_w, bias norm_b)
+//               in place of rms_norm (Zephyr; rows of 2048 values)
+// PRO_RMS / PRO_LN with x_pitch = 0 read the row at x itself, and
+// PRO_RES_RMS / PRO_RES_LN with res_cur set read the residual row there:
+// rows at a fixed address, so the first loads do not wait for the position.
+enum DmvPrologue { PRO_X = 0, PRO_RMS = 1, PRO_RES_RMS = 2, PRO_LN = 3, PRO_RES_LN = 4 };
+
+// Prologue kinds: with the residual add, with layer_norm, with a norm.
+constexpr bool pro_res(int pro) { return pro == PRO_RES_RMS || pro == PRO_RES_LN; }
+constexpr bool pro_ln(int pro) { return pro == PRO_LN || pro == PRO_RES_LN; }
+constexpr bool pro_norm(int pro) { return pro != PRO_X; }
 // Epilogue: EPI_RAW writes the fp32 dot products; EPI_ARGMAX also writes the
 // greedy token to tokens[pos + 1] (and *pos_out = pos + 1 when dpos is set);
 // EPI_SWIGLU takes fused gate|up weights [2f, K] and writes
@@ -40,7 +47,8 @@ struct DmvArgs {
     const uint8_t* res_cur = nullptr;   // PRO_RES_RMS: the residual input row (else res_in at pos)
     uint8_t* res_cur_out = nullptr;     // PRO_RES_RMS: the residual sum also stored here (a fixed row)
     float bscale = 1.0f;                // PRO_RES_RMS: scale of the branch output (1: none)
-    const uint16_t* norm_w = nullptr;   // PRO_RMS / PRO_RES_RMS gain (fp16)
+    const uint16_t* norm_w = nullptr;   // norm gain (fp16)
+    const uint16_t* norm_b = nullptr;   // PRO_LN / PRO_RES_LN bias (fp16)
     float post_scale = 1.0f;            // scale of the normalized row (1: none)
     float* raw = nullptr;               // fp32 dot products [N]
     uint8_t* m_out = nullptr;           // EPI_SWIGLU

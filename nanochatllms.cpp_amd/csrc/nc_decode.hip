@@ -207,6 +207,7 @@ __global__ __launch_bounds__(NT) void k_dmv(DmvArgs A)
     constexpr int WV = WD / 4;
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
+    __shared__ SgShared sgh;
     __shared__ unsigned long long s_key[4];
     __shared__ int s_tok;
     const int nb = A.nb, R = A.rows;
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(NT) void k_dmv(DmvArgs A)
     };
     const int G = gridDim.x;
     int g = blockIdx.x;  // < ngroups: the grid never exceeds the groups
-    const int pos = dmv_prologue<PRO, NCH, false, NT>(A, xs, sq, ssh, [&] { load_group(g, wc, dc); });
+    const int pos = dmv_prologue<PRO, NCH, false, NT>(A, xs, sq, ssh, sgh, [&] { load_group(g, wc, dc); });
 
     // EPI_ARGMAX: each row's lane-0 thread keeps the best key of its rows
     unsigned long long best = 0;
@@ -326,7 +327,7 @@ __host__ __device__ constexpr int head_depth()
 // NCK: 16-byte chunks per row (K / 32 / E).  All chunk and slot indices are
 // compile-time after unrolling; a wavefront's group base is wave-uniform, so
 // a load's address is one scalar base plus a constant offset.
-template <int WT, int EPI, int NCH, int NCK>
+template <int WT, int PRO, int EPI, int NCH, int NCK>
 __global__ __launch_bounds__(kDmvThreads) void k_dmv_head(DmvArgs A)
 {
     constexpr int E = head_chunk_blocks<WT>();
@@ -336,6 +337,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_head(DmvArgs A)
     static_assert(NCK % DEPTH == 0 && NB % 8 == 0, "head layout shape");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
+    __shared__ SgShared sgh;
     __shared__ unsigned long long s_key[4];
     __shared__ int s_tok;
     uint32_t* xs = lds;                                      // staged row: NB * kStage dwords
@@ -380,7 +382,7 @@ __global__ __launch_bounds__(kDmvThreads) void k_dmv_head(DmvArgs A)
             wd[b][0] = __builtin_amdgcn_raw_buffer_load_b32(rd, doff, dc, 0);
         }
     };
-    const int pos = dmv_prologue<PRO_RES_RMS, NCH, true>(A, xs, sq, ssh, [&] {
+    const int pos = dmv_prologue<PRO, NCH, true>(A, xs, sq, ssh, sgh, [&] {
         const auto rq = code_rsrc(gw, true);
         const auto rd = delta_rsrc(gw, true);
 #pragma unroll
@@ -555,10 +557,10 @@ int dmv_go(DmvArgs A, size_t lds, bool spread, hipStream_t st, hipEvent_t ev0, h
 }
 
 // LM heads in the head layout, rows of NCK chunks.
-template <int WT, int EPI, int NCH, int NCK>
+template <int WT, int PRO, int EPI, int NCH, int NCK>
 int head_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
-    auto kern = k_dmv_head<WT, EPI, NCH, NCK>;
+    auto kern = k_dmv_head<WT, PRO, EPI, NCH, NCK>;
     const size_t lds = (size_t)A.nb * kStage * 4 + (size_t)A.nb * 32 * 4;
     static int max_grid = 0;  // workgroups resident at once
     if (!max_grid) {
@@ -617,11 +619,29 @@ int dmv_r_wide(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t e
     return dmv_go<WT, 6, PRO, EPI_RAW, 1, NT>(A, lds, sh.spread, st, ev0, ev1);
 }
 
+// The launch for a prologue kind known at run time; layer_norm (PRO_LN,
+// PRO_RES_LN) at one 8-value chunk per thread only.
+template <int NCH, class Go>
+int with_pro(int pro, Go&& go)
+{
+    switch (pro) {
+    case PRO_RMS: return go(std::integral_constant<int, PRO_RMS>{});
+    case PRO_RES_RMS: return go(std::integral_constant<int, PRO_RES_RMS>{});
+    default:
+        if constexpr (NCH == 1) {
+            if (pro == PRO_LN) return go(std::integral_constant<int, PRO_LN>{});
+            return go(std::integral_constant<int, PRO_RES_LN>{});
+        } else {
+            return fail(NC_ERR_ARG, "decode matvec: layer_norm prologue over more than 2048 values");
+        }
+    }
+}
+
 template <int WT>
 int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     const size_t K = (size_t)A.nb * 32;
-    const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
+    const bool norm = pro_norm(pro);
     const DmvShape R = dmv_shape(A.nb, A.N, norm);
     const bool two = K > (size_t)kDmvThreads * 8;  // norm prologue: two 8-value chunks per thread
     // staged row (kStage dwords per block), the fold terms, then the norm
@@ -631,38 +651,47 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
     if (A.head) {
         // an lm head in the head layout: one fold chain per thread, the
         // weights streamed straight into registers
-        if (pro != PRO_RES_RMS || epi == EPI_SWIGLU)
+        if (!pro_res(pro) || epi == EPI_SWIGLU)
             return fail(NC_ERR_ARG, "decode matvec: head layout with prologue %d epilogue %d", pro, epi);
         // rows of 2048 (one 8-value chunk per thread in the prologue) or
         // 2304 values (two)
         constexpr int E = head_chunk_blocks<WT>();
-        if (A.nb == 64) {
-            if (epi == EPI_ARGMAX) return head_go<WT, EPI_ARGMAX, 1, 64 / E>(A, st, ev0, ev1);
-            return head_go<WT, EPI_RAW, 1, 64 / E>(A, st, ev0, ev1);
+        if (A.nb == 64)
+            return with_pro<1>(pro, [&](auto p) {
+                constexpr int P = decltype(p)::value;
+                if (epi == EPI_ARGMAX) return head_go<WT, P, EPI_ARGMAX, 1, 64 / E>(A, st, ev0, ev1);
+                return head_go<WT, P, EPI_RAW, 1, 64 / E>(A, st, ev0, ev1);
+            });
+        if (A.nb == 72 && pro == PRO_RES_RMS) {
+            if (epi == EPI_ARGMAX) return head_go<WT, PRO_RES_RMS, EPI_ARGMAX, 2, 72 / E>(A, st, ev0, ev1);
+            return head_go<WT, PRO_RES_RMS, EPI_RAW, 2, 72 / E>(A, st, ev0, ev1);
         }
-        if (A.nb == 72) {
-            if (epi == EPI_ARGMAX) return head_go<WT, EPI_ARGMAX, 2, 72 / E>(A, st, ev0, ev1);
-            return head_go<WT, EPI_RAW, 2, 72 / E>(A, st, ev0, ev1);
-        }
-        return fail(NC_ERR_ARG, "decode matvec: head layout rows of %d blocks", A.nb);
+        return fail(NC_ERR_ARG, "decode matvec: head layout rows of %d blocks, prologue %d", A.nb, pro);
     }
     if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
     if (epi == EPI_ARGMAX) {
-        if (pro == PRO_RMS)
-            return two ? dmv_r<WT, PRO_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
-                       : dmv_r<WT, PRO_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
-        return two ? dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1)
-                   : dmv_r<WT, PRO_RES_RMS, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1);
+        if (two)
+            return with_pro<2>(pro, [&](auto p) {
+                return dmv_r<WT, decltype(p)::value, EPI_ARGMAX, 2>(A, lds0, R, st, ev0, ev1);
+            });
+        return with_pro<1>(
+            pro, [&](auto p) { return dmv_r<WT, decltype(p)::value, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1); });
     }
     if (R.spread && R.rows * A.nb > kDmvThreads * 4 && R.rows * A.nb <= kDmvWideThreads * 6) {
-        if (pro == PRO_RMS) return dmv_r_wide<WT, PRO_RMS>(A, lds0, R, st, ev0, ev1);
-        return dmv_r_wide<WT, PRO_RES_RMS>(A, lds0, R, st, ev0, ev1);
+        if (K > (size_t)kDmvWideThreads * 8) {
+            // more than one 8-value chunk per thread: rms_norm only
+            if (pro == PRO_RMS) return dmv_r_wide<WT, PRO_RMS>(A, lds0, R, st, ev0, ev1);
+            if (pro == PRO_RES_RMS) return dmv_r_wide<WT, PRO_RES_RMS>(A, lds0, R, st, ev0, ev1);
+            return fail(NC_ERR_ARG, "decode matvec: layer_norm prologue over %zu values", K);
+        }
+        return with_pro<1>(
+            pro, [&](auto p) { return dmv_r_wide<WT, decltype(p)::value>(A, lds0, R, st, ev0, ev1); });
     }
-    if (pro == PRO_RMS)
-        return two ? dmv_r<WT, PRO_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
-                   : dmv_r<WT, PRO_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
-    return two ? dmv_r<WT, PRO_RES_RMS, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1)
-               : dmv_r<WT, PRO_RES_RMS, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
+    if (two)
+        return with_pro<2>(
+            pro, [&](auto p) { return dmv_r<WT, decltype(p)::value, EPI_RAW, 2>(A, lds0, R, st, ev0, ev1); });
+    return with_pro<1>(
+        pro, [&](auto p) { return dmv_r<WT, decltype(p)::value, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1); });
 }
 
 }  // namespace
@@ -670,8 +699,11 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
 bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi)
 {
     if (wdtype != NC_Q4 && wdtype != NC_Q8) return false;
-    if (pro < PRO_X || pro > PRO_RES_RMS || epi < EPI_RAW || epi > EPI_SWIGLU) return false;
-    const bool norm = pro == PRO_RMS || pro == PRO_RES_RMS;
+    if (pro < PRO_X || pro > PRO_RES_LN || epi < EPI_RAW || epi > EPI_SWIGLU) return false;
+    const bool norm = pro_norm(pro);
+    // layer_norm: rows of 2048 values (its mean is the workgroup's exact
+    // sum over one 8-value chunk per thread)
+    if (pro_ln(pro) && K != 2048) return false;
     if (K <= 0 || K % 32 || N <= 0 || !dmv_shape(K / 32, N, norm).rows) return false;
     if (norm && (K % kSsThreads || K > kDmvThreads * 8 * kDmvNormChunks)) return false;
     if (epi == EPI_ARGMAX && !norm) return false;

@@ -1,7 +1,7 @@
 // nc_decode_glu.hip -- the gate|up matvec of the single-row decode step with
 // the SwiGLU epilogue (Q8 activations, Q4/Q8 weights): k_dmv_glu, and
 // k_dmv_glu_spec, which computes the weight terms, fold and SwiGLU beside the
-// exact rms_norm sum from a predicted row (nc_dmv.h: spec_run).  The
+// exact norm sums from a predicted row (nc_dmv.h: spec_run).  The
 // arithmetic is the reference's block dot product, fold order and
 // requantization points (tinyllama/tinyllama.cpp:88-97).
 #include "nc_dmv.h"
@@ -24,6 +24,7 @@ __global__ __launch_bounds__(kGluThreads) void k_dmv_glu(DmvArgs A)
     static_assert(NB % 8 == 0 && IT <= kGluMaxItems, "gate|up block shape");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
+    __shared__ SgShared sgh;
     __shared__ float s_out[64];
     uint32_t* xs = lds;
     float* T = reinterpret_cast<float*>(xs + NB * kStage);  // 64 rows (gate, then up) x 4 lanes x TP
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(kGluThreads) void k_dmv_glu(DmvArgs A)
     int b = blockIdx.x;  // < nblk: the grid never exceeds the blocks
     DmvArgs P = A;
     P.nb = NB;
-    dmv_prologue<PRO, NCH, false, kGluThreads>(P, xs, sq, ssh, [&] { load_block(b); });
+    dmv_prologue<PRO, NCH, false, kGluThreads>(P, xs, sq, ssh, sgh, [&] { load_block(b); });
 
     // the terms of all 64 rows, then the gate rows' folds (waves 0-1) and
     // the up rows' folds (waves 2-3) side by side
@@ -113,10 +114,11 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
     static_assert(NB % 8 == 0 && NB * 64 % NS == 0 && IT <= kGluMaxItems, "gate|up block shape");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
+    __shared__ SgShared sgh;
     __shared__ SpecSync sy;
     __shared__ float s_out[64];
     float* T = reinterpret_cast<float*>(lds);  // 64 rows (gate, then up) x 4 lanes x TP
-    const SpecLds L = spec_lds(T + 64 * 4 * TP, NB);
+    const SpecLds L = spec_lds(T + 64 * 4 * TP, NB, pro_ln(PRO));
     const int tid = threadIdx.x, s = tid - kSpecExact;
     const int f = A.N / 2, nblk = f / 32;
 
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
     };
     DmvArgs P = A;
     P.nb = NB;
-    spec_run<PRO, NCH, NS>(P, L, ssh, sy, load_w, terms, spec_tail, commit, exact_tail);
+    spec_run<PRO, NCH, NS>(P, L, ssh, sgh, sy, load_w, terms, spec_tail, commit, exact_tail);
     // further gate|up blocks of this workgroup (when the grid holds fewer
     // workgroups than blocks): the exact row is in place
     for (b += gridDim.x; b < nblk; b += gridDim.x) {
@@ -242,7 +244,7 @@ int glu_spec_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
     constexpr int TP = ((NB + 3) & ~3) + 4;
     constexpr int NT = kSpecExact + kGluThreads;
     auto kern = k_dmv_glu_spec<WT, PRO, NCH, NB>;
-    const size_t lds = (size_t)64 * 4 * TP * 4 + spec_lds_bytes(NB);
+    const size_t lds = (size_t)64 * 4 * TP * 4 + spec_lds_bytes(NB, pro_ln(PRO));
     static int max_grid = 0;
     if (!max_grid) {
         int per_cu = 0;
@@ -268,19 +270,29 @@ int glu_dispatch(const DmvArgs& A, int wdtype, int pro, hipStream_t st, hipEvent
 {
     auto go = [&](auto wt) {
         constexpr int WT = decltype(wt)::value;
-        // gate|up rows of 2048 (64 blocks) or 2304 (72 blocks) values
+        // gate|up rows of 2048 (64 blocks) or 2304 (72 blocks) values;
+        // layer_norm at 2048 only
         if constexpr (kSpecGlu) {
-            if (A.nb == 64)
-                return pro == PRO_RMS ? glu_spec_go<WT, PRO_RMS, 1, 64>(A, st, ev0, ev1)
-                                      : glu_spec_go<WT, PRO_RES_RMS, 1, 64>(A, st, ev0, ev1);
+            if (A.nb == 64) {
+                switch (pro) {
+                case PRO_RMS: return glu_spec_go<WT, PRO_RMS, 1, 64>(A, st, ev0, ev1);
+                case PRO_RES_RMS: return glu_spec_go<WT, PRO_RES_RMS, 1, 64>(A, st, ev0, ev1);
+                case PRO_LN: return glu_spec_go<WT, PRO_LN, 1, 64>(A, st, ev0, ev1);
+                default: return glu_spec_go<WT, PRO_RES_LN, 1, 64>(A, st, ev0, ev1);
+                }
+            }
             return pro == PRO_RMS ? glu_spec_go<WT, PRO_RMS, 2, 72>(A, st, ev0, ev1)
                                   : glu_spec_go<WT, PRO_RES_RMS, 2, 72>(A, st, ev0, ev1);
         } else {
             const int tp = ((A.nb + 3) & ~3) + 4;
             const size_t lds = (size_t)A.nb * kStage * 4 + (size_t)A.nb * 32 * 4 + (size_t)64 * 4 * tp * 4;
             if (A.nb == 64) {
-                if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 64>(A, lds, st, ev0, ev1);
-                return glu_go<WT, PRO_RES_RMS, 1, 64>(A, lds, st, ev0, ev1);
+                switch (pro) {
+                case PRO_RMS: return glu_go<WT, PRO_RMS, 1, 64>(A, lds, st, ev0, ev1);
+                case PRO_RES_RMS: return glu_go<WT, PRO_RES_RMS, 1, 64>(A, lds, st, ev0, ev1);
+                case PRO_LN: return glu_go<WT, PRO_LN, 1, 64>(A, lds, st, ev0, ev1);
+                default: return glu_go<WT, PRO_RES_LN, 1, 64>(A, lds, st, ev0, ev1);
+                }
             }
             if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 72>(A, lds, st, ev0, ev1);
             return glu_go<WT, PRO_RES_RMS, 1, 72>(A, lds, st, ev0, ev1);

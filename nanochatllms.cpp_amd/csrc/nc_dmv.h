@@ -89,8 +89,10 @@ __device__ __forceinline__ void load_f32_chunk(const float* p, int ch, float (&v
 // only once the rows have arrived -- a launch that requests tens of MB
 // would otherwise queue its rows behind its own weights.
 template <int PRO, int NCH, bool ROWS_FIRST = false, int NT = kDmvThreads, class LoadW>
-__device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, LoadW&& load_w)
+__device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, float* sq, SsShared& ssh, SgShared& sgh,
+                                            LoadW&& load_w)
 {
+    constexpr bool RES = pro_res(PRO), LN = pro_ln(PRO);
     const int tid = threadIdx.x;
     const int nb = A.nb, K = nb * 32;
     const int nch = K / 8;
@@ -107,31 +109,37 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
         lds_barrier();
         return A.pos;  // not used after a PRO_X prologue
     } else {
-        // h: the stored row (PRO_RMS) or the residual sum (PRO_RES_RMS)
-        float h[NCH][8], gain[NCH][8];
+        // h: the stored row (PRO_RMS, PRO_LN) or the residual sum (RES)
+        float h[NCH][8], gain[NCH][8], bias[NCH][8];
         float av[NCH][8], ov[NCH][8];
         // A row at a fixed address (x_pitch = 0, res_cur) is requested
         // before the position: the position is then loaded after the row
         // and before the weights, so waiting for it does not wait for them.
-        const bool fixed = PRO == PRO_RMS ? A.x_pitch == 0 : A.res_cur != nullptr;
+        const bool fixed = !RES ? A.x_pitch == 0 : A.res_cur != nullptr;
         int pos = A.pos;
         const uint8_t* arow;
         if (fixed) {
-            arow = PRO == PRO_RMS ? A.x : A.res_cur;
+            arow = !RES ? A.x : A.res_cur;
         } else {
             if (A.dpos) pos = load_pos(A.dpos);
-            arow = PRO == PRO_RMS ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
+            arow = !RES ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
         }
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * NT;
             const int cc = ch < nch ? ch : 0;
             load_act_chunk(arow, K, cc, av[j]);
-            if (PRO == PRO_RES_RMS) load_f32_chunk(A.raw_in, cc, ov[j]);
+            if (RES) load_f32_chunk(A.raw_in, cc, ov[j]);
             const uint4 gw = reinterpret_cast<const uint4*>(A.norm_w)[cc];
             const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
             for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
+            if (LN) {
+                const uint4 bw = reinterpret_cast<const uint4*>(A.norm_b)[cc];
+                const uint32_t bws[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) bias[j][i] = h2f((uint16_t)(bws[i >> 1] >> (16 * (i & 1))));
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         int posv = 0;
@@ -146,7 +154,7 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
             const int ch = tid + j * NT;
             const bool valid = ch < nch;
             if (j * NT >= nch) break;  // uniform
-            if (PRO == PRO_RES_RMS) {
+            if (RES) {
                 quad_roundtrip(ov[j]);
                 if (A.bscale != 1.0f) {
 #pragma unroll
@@ -169,15 +177,37 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
                 for (int i = 0; i < 8; i++) h[j][i] = av[j][i];
             }
             if (valid) {
-                const float4 s0 = make_float4(h[j][0] * h[j][0], h[j][1] * h[j][1], h[j][2] * h[j][2], h[j][3] * h[j][3]);
-                const float4 s1 = make_float4(h[j][4] * h[j][4], h[j][5] * h[j][5], h[j][6] * h[j][6], h[j][7] * h[j][7]);
-                reinterpret_cast<float4*>(sq)[2 * ch] = s0;
-                reinterpret_cast<float4*>(sq)[2 * ch + 1] = s1;
+                // rms_norm: the squares; layer_norm: the values (the mean first)
+                float t[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) t[i] = LN ? h[j][i] : h[j][i] * h[j][i];
+                reinterpret_cast<float4*>(sq)[2 * ch] = make_float4(t[0], t[1], t[2], t[3]);
+                reinterpret_cast<float4*>(sq)[2 * ch + 1] = make_float4(t[4], t[5], t[6], t[7]);
             }
         }
         lds_barrier();
+        float mean = 0.0f;
+        if (LN) {
+            // layer_norm (gten/ops.cpp:669-698): the mean as the exact sum of
+            // the Q8 row's values (on the fp16 grid), then the squared
+            // deviations' exact sum
+            static_assert(!LN || NCH == 1, "layer_norm prologue: rows of up to 8 values per thread");
+            mean = block_seq_sum_grid<(LN ? 2048 / NT : 1), NT>(sq, sgh) / (float)K;
+#pragma unroll
+            for (int j = 0; j < NCH; j++) {
+                const int ch = tid + j * NT;
+                if (ch < nch) {
+                    float t[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) t[i] = (h[j][i] - mean) * (h[j][i] - mean);
+                    reinterpret_cast<float4*>(sq)[2 * ch] = make_float4(t[0], t[1], t[2], t[3]);
+                    reinterpret_cast<float4*>(sq)[2 * ch + 1] = make_float4(t[4], t[5], t[6], t[7]);
+                }
+            }
+            lds_barrier();
+        }
         const float ss = block_seq_sum_nonneg(sq, K, ssh);
-        const float denom = sqrtf(ss / (float)K) + 1e-6f;
+        const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
         // the normalized row as stored (codes, then deltas) over sq's bytes
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
@@ -185,7 +215,8 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
             if (j * NT >= nch) break;  // uniform
             float y[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) y[i] = h[j][i] / denom * gain[j][i];
+            for (int i = 0; i < 8; i++)
+                y[i] = LN ? ((h[j][i] - mean) / denom) * gain[j][i] + bias[j][i] : h[j][i] / denom * gain[j][i];
             if (A.post_scale != 1.0f) {
                 quad_roundtrip(y);
 #pragma unroll
@@ -225,26 +256,30 @@ constexpr int kSpecExact = kSsThreads;  // threads of the exact path
 
 // Dynamic LDS of the speculative prologue (after the kernel's fold terms).
 struct SpecLds {
-    float* sq;     // K squares of the row (the exact sum's terms)
+    float* sq;     // K terms of the exact sums: rms_norm's squares; layer_norm's values, then squared deviations
     float* h;      // K values of the row before the norm
     float* g;      // K norm gains
+    float* b;      // K norm biases (layer_norm)
     uint8_t* row;  // the speculative Act row, then the exact one: K codes, nb fp16 deltas
     uint8_t* bad;  // nb flags: the block differs between the two rows
 };
 
-__host__ __device__ constexpr size_t spec_lds_bytes(int nb)
+__host__ __device__ constexpr size_t spec_lds_bytes(int nb, bool ln)
 {
-    return (size_t)nb * 32 * 4 * 3 + (((size_t)nb * 34 + 15) & ~(size_t)15) + (((size_t)nb + 15) & ~(size_t)15);
+    return (size_t)nb * 32 * 4 * (ln ? 4 : 3) + (((size_t)nb * 34 + 15) & ~(size_t)15) +
+           (((size_t)nb + 15) & ~(size_t)15);
 }
 
-__device__ __forceinline__ SpecLds spec_lds(float* base, int nb)
+__device__ __forceinline__ SpecLds spec_lds(float* base, int nb, bool ln)
 {
     const int K = nb * 32;
+    const int na = ln ? 4 : 3;
     SpecLds L;
     L.sq = base;
     L.h = base + K;
     L.g = base + 2 * K;
-    L.row = reinterpret_cast<uint8_t*>(base + 3 * K);
+    L.b = ln ? base + 3 * K : nullptr;
+    L.row = reinterpret_cast<uint8_t*>(base + na * K);
     L.bad = L.row + ((nb * 34 + 15) & ~15);
     return L;
 }
@@ -265,13 +300,16 @@ __device__ __forceinline__ float spec_approx_sum(const float* sq, int K)
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
-// y = h / denom * g (then the post scale's round trip), quantized: the
-// rms_norm of dmv_prologue for one 8-value chunk.
-__device__ __forceinline__ Q8Chunk spec_norm_chunk(const float (&h)[8], const float (&g)[8], float denom, float post)
+// The normalized chunk, quantized, as dmv_prologue computes it:
+// rms_norm y = h / denom * g, layer_norm y = ((h - mean) / denom) * g + b,
+// then the post scale's round trip.
+template <bool LN>
+__device__ __forceinline__ Q8Chunk spec_norm_chunk(const float (&h)[8], const float (&g)[8], const float (&b)[8],
+                                                   float mean, float denom, float post)
 {
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) y[i] = h[i] / denom * g[i];
+    for (int i = 0; i < 8; i++) y[i] = LN ? ((h[i] - mean) / denom) * g[i] + b[i] : h[i] / denom * g[i];
     if (post != 1.0f) {
         quad_roundtrip(y);
 #pragma unroll
@@ -285,7 +323,8 @@ struct SpecSync {
     int exact;    // barrier counter of threads 0-255 (the exact sum)
     int spec;     // barrier counter of the weight threads
     int anybad;   // some block differs: the speculative results are void
-    float wsum[kSpecExact / kWave];  // per exact wavefront: its part of the squares (the prediction)
+    float wsum[kSpecExact / kWave];   // per exact wavefront: its part of the squares (the prediction)
+    float wsum1[kSpecExact / kWave];  // ... and of the values (layer_norm's predicted mean)
 };
 
 // The whole norm-prologue matvec but its final stores.  load_w(): the weight
@@ -298,16 +337,19 @@ struct SpecSync {
 // exact_tail(): otherwise, after the differing terms were recomputed: the
 // fold and epilogue from the exact terms.  NS: weight threads.
 template <int PRO, int NCH, int NS, class LoadW, class Terms, class SpecTail, class Commit, class ExactTail>
-__device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsShared& ssh, SpecSync& sy, LoadW&& load_w,
-                                         Terms&& terms, SpecTail&& spec_tail, Commit&& commit, ExactTail&& exact_tail)
+__device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsShared& ssh, SgShared& sgh, SpecSync& sy,
+                                         LoadW&& load_w, Terms&& terms, SpecTail&& spec_tail, Commit&& commit,
+                                         ExactTail&& exact_tail)
 {
     constexpr int NT = kSpecExact;
+    constexpr bool RES = pro_res(PRO), LN = pro_ln(PRO);
+    static_assert(!LN || NCH == 1, "layer_norm prologue: rows of 2048 values");
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int nb = A.nb, K = nb * 32;
     const int nch = K / 8;
     const bool ex = tid < NT;
-    float h[NCH][8], gain[NCH][8], av[NCH][8], ov[NCH][8];
-    const bool fixed = PRO == PRO_RMS ? A.x_pitch == 0 : A.res_cur != nullptr;
+    float h[NCH][8], gain[NCH][8], bias[NCH][8], av[NCH][8], ov[NCH][8];
+    const bool fixed = !RES ? A.x_pitch == 0 : A.res_cur != nullptr;
     int pos = A.pos;
     if (tid == 0) {
         sy.exact = 0;
@@ -319,21 +361,27 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
         __builtin_amdgcn_s_setprio(3);
         const uint8_t* arow;
         if (fixed) {
-            arow = PRO == PRO_RMS ? A.x : A.res_cur;
+            arow = !RES ? A.x : A.res_cur;
         } else {
             if (A.dpos) pos = load_pos(A.dpos);
-            arow = PRO == PRO_RMS ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
+            arow = !RES ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
         }
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * NT;
             const int cc = ch < nch ? ch : 0;
             load_act_chunk(arow, K, cc, av[j]);
-            if (PRO == PRO_RES_RMS) load_f32_chunk(A.raw_in, cc, ov[j]);
+            if (RES) load_f32_chunk(A.raw_in, cc, ov[j]);
             const uint4 gw = reinterpret_cast<const uint4*>(A.norm_w)[cc];
             const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
             for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
+            if (LN) {
+                const uint4 bw = reinterpret_cast<const uint4*>(A.norm_b)[cc];
+                const uint32_t bws[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) bias[j][i] = h2f((uint16_t)(bws[i >> 1] >> (16 * (i & 1))));
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -344,13 +392,13 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
     __builtin_amdgcn_sched_barrier(0);
     if (ex) {
         if (fixed && A.dpos) pos = posv;
-        float part = 0.0f;  // this thread's squares, for the prediction
+        float part = 0.0f, part1 = 0.0f;  // this thread's squares and values, for the prediction
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             const int ch = tid + j * NT;
             const bool valid = ch < nch;
             if (j * NT >= nch) break;  // uniform
-            if (PRO == PRO_RES_RMS) {
+            if (RES) {
                 quad_roundtrip(ov[j]);
                 if (A.bscale != 1.0f) {
 #pragma unroll
@@ -376,32 +424,62 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
                 float sqv[8];
 #pragma unroll
                 for (int i = 0; i < 8; i++) sqv[i] = h[j][i] * h[j][i];
+                // the first exact sum's terms: the squares (rms_norm) or the values (layer_norm)
+                const float(&t)[8] = LN ? h[j] : sqv;
                 float4* sq4 = reinterpret_cast<float4*>(L.sq) + 2 * ch;
-                sq4[0] = make_float4(sqv[0], sqv[1], sqv[2], sqv[3]);
-                sq4[1] = make_float4(sqv[4], sqv[5], sqv[6], sqv[7]);
+                sq4[0] = make_float4(t[0], t[1], t[2], t[3]);
+                sq4[1] = make_float4(t[4], t[5], t[6], t[7]);
                 part = part + (((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + ((sqv[4] + sqv[5]) + (sqv[6] + sqv[7])));
+                if (LN)
+                    part1 = part1 + (((h[j][0] + h[j][1]) + (h[j][2] + h[j][3])) +
+                                     ((h[j][4] + h[j][5]) + (h[j][6] + h[j][7])));
                 float4* h4 = reinterpret_cast<float4*>(L.h) + 2 * ch;
                 h4[0] = make_float4(h[j][0], h[j][1], h[j][2], h[j][3]);
                 h4[1] = make_float4(h[j][4], h[j][5], h[j][6], h[j][7]);
                 float4* g4 = reinterpret_cast<float4*>(L.g) + 2 * ch;
                 g4[0] = make_float4(gain[j][0], gain[j][1], gain[j][2], gain[j][3]);
                 g4[1] = make_float4(gain[j][4], gain[j][5], gain[j][6], gain[j][7]);
+                if (LN) {
+                    float4* b4 = reinterpret_cast<float4*>(L.b) + 2 * ch;
+                    b4[0] = make_float4(bias[j][0], bias[j][1], bias[j][2], bias[j][3]);
+                    b4[1] = make_float4(bias[j][4], bias[j][5], bias[j][6], bias[j][7]);
+                }
             }
         }
         part = wave_scan_add(part);
         if (lane == kWave - 1) sy.wsum[tid / kWave] = part;
+        if (LN) {
+            part1 = wave_scan_add(part1);
+            if (lane == kWave - 1) sy.wsum1[tid / kWave] = part1;
+        }
     }
     lds_barrier();
     Q8Chunk qx[NCH];
     if (ex) {
-        // the exact sum on threads 0-255, then the exact row (held until the
-        // speculative side is done)
-        const float ss = block_seq_sum_nonneg_waves(L.sq, K, ssh, &sy.exact);
-        const float denom = sqrtf(ss / (float)K) + 1e-6f;
+        // the exact sums on threads 0-255, then the exact row (held until
+        // the speculative side is done)
+        SsWaveBarrier<NT / kWave> bar{&sy.exact, 0};
+        float mean = 0.0f;
+        if constexpr (LN) {
+            // layer_norm (gten/ops.cpp:669-698): the mean, the exact sum of
+            // the Q8 row's values (on the fp16 grid), then the squared
+            // deviations over the values in sq
+            mean = block_seq_sum_grid<8, NT>(L.sq, sgh, nullptr, bar) / (float)K;
+            const int ch = tid;
+            float t[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) t[i] = (h[0][i] - mean) * (h[0][i] - mean);
+            float4* sq4 = reinterpret_cast<float4*>(L.sq) + 2 * ch;
+            sq4[0] = make_float4(t[0], t[1], t[2], t[3]);
+            sq4[1] = make_float4(t[4], t[5], t[6], t[7]);
+            bar();
+        }
+        const float ss = block_seq_sum_nonneg_bar(L.sq, K, ssh, bar);
+        const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             if (j * NT >= nch) break;  // uniform
-            qx[j] = spec_norm_chunk(h[j], gain[j], denom, A.post_scale);
+            qx[j] = spec_norm_chunk<LN>(h[j], gain[j], bias[j], mean, denom, A.post_scale);
         }
         // once the speculative row is complete (every weight wavefront has
         // passed its first barrier), compare it block by block with the
@@ -437,17 +515,26 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
         // fold and epilogue
         const int sc = tid - NT;
         if (sc < NT) {
-            const float approx = (((sy.wsum[0] + sy.wsum[1]) + sy.wsum[2]) + sy.wsum[3]) * A.spec_skew;
-            const float dn = sqrtf(approx / (float)K) + 1e-6f;
+            const float s2 = ((sy.wsum[0] + sy.wsum[1]) + sy.wsum[2]) + sy.wsum[3];
+            float mn = 0.0f, dn;
+            if (LN) {
+                // mean and variance from the sums of the values and squares
+                mn = (((sy.wsum1[0] + sy.wsum1[1]) + sy.wsum1[2]) + sy.wsum1[3]) / (float)K;
+                const float var = fmaxf(s2 / (float)K - mn * mn, 0.0f) * A.spec_skew;
+                dn = sqrtf(var) + 1e-05f;
+            } else {
+                dn = sqrtf(s2 * A.spec_skew / (float)K) + 1e-6f;
+            }
 #pragma unroll
             for (int j = 0; j < NCH; j++) {
                 const int ch = sc + j * NT;
                 if (j * NT >= nch) break;  // uniform
                 const int cc = ch < nch ? ch : 0;
-                float hv[8], gv[8];
+                float hv[8], gv[8], bv[8];
                 load_f32_chunk(L.h, cc, hv);
                 load_f32_chunk(L.g, cc, gv);
-                const Q8Chunk q = spec_norm_chunk(hv, gv, dn, A.post_scale);
+                if (LN) load_f32_chunk(L.b, cc, bv);
+                const Q8Chunk q = spec_norm_chunk<LN>(hv, gv, bv, mn, dn, A.post_scale);
                 if (ch < nch) store_act_chunk(L.row, K, ch, q);
             }
         }
@@ -482,7 +569,7 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
 int device_cus();
 
 // The gate|up launch with the SwiGLU epilogue (nc_decode_glu.hip): K = 32 nb
-// of 2048 or 2304, a norm prologue (PRO_RMS or PRO_RES_RMS).
+// of 2048 or 2304, a norm prologue (rms_norm; layer_norm at K = 2048).
 int glu_dispatch(const DmvArgs& A, int wdtype, int pro, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
 
 }  // namespace nc

@@ -863,17 +863,23 @@ public:
         return mv(xn + (size_t)(R - 1) * pd, pd, 1, head, logits, cfg.n_vocab, NC_PROF_LM_HEAD);
     }
 
+    // The fused kernels' norm prologues: the first layer's (a stored row) and
+    // the others' (a residual add first).
+    int pro_first() const { return norm_kind() == kNormLayer ? PRO_LN : PRO_RMS; }
+    int pro_res_add() const { return norm_kind() == kNormLayer ? PRO_RES_LN : PRO_RES_RMS; }
+
     bool fused_supported() const
     {
-        if (adt != NC_Q8 || norm_kind() != kNormRms) return false;
-        const int wt = cfg.wdtype;
+        if (adt != NC_Q8) return false;
+        const int wt = cfg.wdtype, pr = pro_res_add();
         for (const Layer& y : L)
-            if (!decode_matvec_supported(wt, d, y.qd + 2 * y.kvd, PRO_RES_RMS, EPI_RAW) ||
+            if (!decode_matvec_supported(wt, d, y.qd + 2 * y.kvd, pr, EPI_RAW) ||
+                !decode_matvec_supported(wt, d, y.qd + 2 * y.kvd, pro_first(), EPI_RAW) ||
                 !decode_matvec_supported(wt, y.qd, d, PRO_X, EPI_RAW) ||
-                !decode_matvec_supported(wt, d, 2 * y.f, PRO_RES_RMS, EPI_SWIGLU) ||
+                !decode_matvec_supported(wt, d, 2 * y.f, pr, EPI_SWIGLU) ||
                 !decode_matvec_supported(wt, y.f, d, PRO_X, EPI_RAW))
                 return false;
-        return decode_matvec_supported(wt, d, cfg.n_vocab, PRO_RES_RMS, EPI_ARGMAX);
+        return decode_matvec_supported(wt, d, cfg.n_vocab, pr, EPI_ARGMAX);
     }
 
     // Algorithmic HBM bytes of one fused launch: weights once, the prologue
@@ -883,9 +889,13 @@ public:
         const double N = w->rows, K = w->cols, row = (K / 32) * 34.0;
         double b = N * (K / 32) * (w->dtype == NC_Q8 ? 34.0 : 18.0);
         b += epi == EPI_SWIGLU ? (N / 64) * 34.0 : 4.0 * N;
+        // the input row (two with the residual add, and its fp32 addend),
+        // the norm gains (and layer_norm's biases)
         if (pro == PRO_X) b += row;
         if (pro == PRO_RMS) b += row + 2.0 * K;
         if (pro == PRO_RES_RMS) b += 2.0 * row + 4.0 * K + 2.0 * K;
+        if (pro == PRO_LN) b += row + 4.0 * K;
+        if (pro == PRO_RES_LN) b += 2.0 * row + 4.0 * K + 4.0 * K;
         return b;
     }
 
@@ -933,24 +943,26 @@ public:
         base.dpos = dpos;
         base.res_pitch = pd;
         base.bscale = bs;
+        const int pr = pro_res_add();
         for (int l = 0; l < cfg.n_layers; l++) {
             Layer& y = L[l];
             const int pq = pitch(y.qd), pkv = pitch(y.kvd);
             const int nqkv = y.qd + 2 * y.kvd;
             DmvArgs a = base;
             a.norm_w = y.attn_norm;
+            a.norm_b = y.attn_norm_b;
             a.raw = qkv_raw;
             if (l == 0) {
                 a.x = cur_x0;
                 a.x_pitch = 0;
-                if ((s = dmv(a, &y.qkv, PRO_RMS, EPI_RAW, NC_PROF_QKV))) return s;
+                if ((s = dmv(a, &y.qkv, pro_first(), EPI_RAW, NC_PROF_QKV))) return s;
             } else {
                 a.res_in = L[l - 1].res1;
                 a.res_cur = cur1;
                 a.raw_in = down_raw;
                 a.res_out = L[l - 1].res2;
                 a.res_cur_out = cur2;
-                if ((s = dmv(a, &y.qkv, PRO_RES_RMS, EPI_RAW, NC_PROF_QKV))) return s;
+                if ((s = dmv(a, &y.qkv, pr, EPI_RAW, NC_PROF_QKV))) return s;
             }
             if (!y.bq) {
                 if ((s = attn_decode_launch(qkv_raw, y.hq, y.hkv, y.qn, y.kn, rope, d_half, pos, dpos, y.kc, y.vc, pkv,
@@ -975,8 +987,9 @@ public:
             a.res_out = y.res1;
             a.res_cur_out = cur1;
             a.norm_w = y.mlp_norm;
+            a.norm_b = y.mlp_norm_b;
             a.m_out = m_act;
-            if ((s = dmv(a, &y.gu, PRO_RES_RMS, EPI_SWIGLU, NC_PROF_GATE_UP))) return s;
+            if ((s = dmv(a, &y.gu, pr, EPI_SWIGLU, NC_PROF_GATE_UP))) return s;
             a = base;
             a.x = m_act;
             a.raw = down_raw;
@@ -988,20 +1001,21 @@ public:
         a.raw_in = down_raw;
         a.res_out = L[cfg.n_layers - 1].res2;
         a.norm_w = norm_w;
+        a.norm_b = norm_b;
         a.post_scale = minicpm ? 1.0f / 9 : 1.0f;  // minicpm.cpp:104-105
         a.raw = logits;
         // the head-layout copy of the lm head when there is one
         const nc_tensor* head = hl.data ? &hl : (tied() ? &emb : &lm);
         a.head = hl.data ? 1 : 0;
         // a sampling step: logits only, the sampler picks the token
-        if (sample_head) return dmv(a, head, PRO_RES_RMS, EPI_RAW, NC_PROF_LM_HEAD);
+        if (sample_head) return dmv(a, head, pr, EPI_RAW, NC_PROF_LM_HEAD);
         a.tokens = tokens;
         a.pos_out = dpos;
         a.amax = am_scratch;
         // the next step's embedding and RoPE rows, from the greedy token (the
         // embedding rows in the embedding's own layout)
         if (dpos) next_input_fields(&a, dpos);
-        return dmv(a, head, PRO_RES_RMS, EPI_ARGMAX, NC_PROF_LM_HEAD);
+        return dmv(a, head, pr, EPI_ARGMAX, NC_PROF_LM_HEAD);
     }
 
     // The fields of the next step's embedding and RoPE rows (the greedy

@@ -438,6 +438,16 @@ __device__ __forceinline__ float block_seq_sum_nonneg(const float* t, int n, SsS
     return block_seq_sum_impl<0>(t, n, sh, fast);
 }
 
+// The same on threads 0..255 with a barrier object of the caller's (an
+// SsWaveBarrier already used for other sums keeps its count).
+template <class Bar>
+__device__ __forceinline__ float block_seq_sum_nonneg_bar(const float* t, int n, SsShared& sh, Bar& bar)
+{
+    if (n == 8 * kSsThreads) return block_seq_sum_core<8>(t, n, sh, nullptr, bar);
+    if (n == 9 * kSsThreads) return block_seq_sum_core<9>(t, n, sh, nullptr, bar);
+    return block_seq_sum_core<0>(t, n, sh, nullptr, bar);
+}
+
 // The same computed by threads 0..255 alone (only they call it), which
 // synchronize through the LDS counter *cnt (zeroed before each call, then a
 // workgroup barrier): the workgroup's other wavefronts run work of their
@@ -445,9 +455,7 @@ __device__ __forceinline__ float block_seq_sum_nonneg(const float* t, int n, SsS
 __device__ __forceinline__ float block_seq_sum_nonneg_waves(const float* t, int n, SsShared& sh, int* cnt)
 {
     SsWaveBarrier<kSsThreads / kWave> bar{cnt, 0};
-    if (n == 8 * kSsThreads) return block_seq_sum_core<8>(t, n, sh, nullptr, bar);
-    if (n == 9 * kSsThreads) return block_seq_sum_core<9>(t, n, sh, nullptr, bar);
-    return block_seq_sum_core<0>(t, n, sh, nullptr, bar);
+    return block_seq_sum_nonneg_bar(t, n, sh, bar);
 }
 
 // ---------------------------------------------------------------------------

@@ -194,14 +194,16 @@ def reference_loop(gpu, name, oracle=None):
 
 
 @pytest.mark.parametrize("skew", [2.0, 1.001, 1.0 + 2.0 ** -22])
-@pytest.mark.parametrize("name", ["wide-llama-q4", "wide-llama-q8", "wide-minicpm-q4", "tinyllama-q4"])
+@pytest.mark.parametrize("name", ["wide-llama-q4", "wide-llama-q8", "wide-minicpm-q4", "wide-zephyr-q4", "wide-zephyr-q8",
+                                  "tinyllama-q4"])
 def test_speculative_norm_rows_recomputed(gpu, name, skew):
     """The fused norm launches compute their weight terms from a row
-    normalized with a predicted sum of squares, beside the exact sum, and
-    recompute the blocks where the exact row differs.  A prediction skewed
-    from the host makes rows differ (all blocks at 2x, some at 1.001x, the
-    odd tie at 1 + 2^-22): the fix-ups must run and every digest and token
-    must still be the reference's."""
+    normalized with a predicted sum of squares (rms_norm) or mean and
+    variance (layer_norm), beside the exact sums, and recompute the blocks
+    where the exact row differs.  A prediction skewed from the host makes
+    rows differ (all blocks at 2x, some at 1.001x, the odd tie at
+    1 + 2^-22): the fix-ups must run and every digest and token must still
+    be the reference's."""
     L = gpu.lib()
     cnt = gpu.DeviceBuffer(4)
     cnt.upload(np.zeros(1, np.int32))

@@ -59,11 +59,14 @@ WIDE = {
     "wide-minicpm-f16": dict(arch=nc.MINICPM, wdtype=nc.F16, n_vocab=122753, n_embd=2304, n_layers=2, n_heads=36,
                              n_kv_heads=36, n_ffn=5760, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0005),
     # TinyLlama's widths in fp16 (the fused rms_norm fp16 decode matvecs at
-    # K = 2048) and Zephyr's in Q4 (layer_norm with bias on a Q8 row)
+    # K = 2048) and Zephyr's in Q4 and Q8 (the fused layer_norm with bias on
+    # a Q8 row)
     "wide-llama-f16": dict(arch=nc.LLAMA, wdtype=nc.F16, n_vocab=32000, n_embd=2048, n_layers=2, n_heads=32,
                            n_kv_heads=4, n_ffn=5632, eos=-1, rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0006),
     "wide-zephyr-q4": dict(arch=nc.ZEPHYR, wdtype=nc.Q4, n_vocab=100352, n_embd=2048, n_layers=2, n_heads=32,
                            n_kv_heads=32, n_ffn=5632, eos=-1, rope_pct=0.25, prompt=16, gen=16, seed=0x7EE0007),
+    "wide-zephyr-q8": dict(arch=nc.ZEPHYR, wdtype=nc.Q8, n_vocab=100352, n_embd=2048, n_layers=2, n_heads=32,
+                           n_kv_heads=32, n_ffn=5632, eos=-1, rope_pct=0.25, prompt=16, gen=16, seed=0x7EE0008),
     "wide-openelm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=32000, n_embd=2048, n_layers=3,
                             n_heads=[16, 16, 20], n_kv_heads=[4, 4, 5], n_ffn=[1024, 4608, 8192], eos=-1,
                             rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0004),
