@@ -24,7 +24,9 @@ during a second pass over the same timed steps with every kernel launched
 directly; `per_kernel` gives the same figures for each matvec role.
 `traffic` is the measured HBM bytes per launch of that kernel, from the
 committed rocprofv3 counter summary (profiles/traffic.json), when one exists
-for the workload.
+for the workload and was taken on a build of the same kernel sources (the
+summary records their digest); otherwise null, and `traffic_source` says
+which build the committed counters belong to.
 
     python bench.py --copy-calibration MIB   (one plain copy of MIB MiB: the
                                               reference dispatch for the
@@ -183,16 +185,38 @@ def copy_calibration(mib):
     print(json.dumps({"copy_bytes": n, "copy_ms": round(dt * 1e3, 4)}), flush=True)
 
 
+def kernel_sources_sha256(csrc_dir=os.path.join(PKG_DIR, "csrc")):
+    """Digest of the library's sources (file names and contents, in name
+    order): names the build a counter figure belongs to."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(csrc_dir)):
+        path = os.path.join(csrc_dir, name)
+        if os.path.isfile(path) and name.endswith((".hip", ".h", ".cpp")):
+            h.update(name.encode() + b"\0")
+            with open(path, "rb") as f:
+                h.update(f.read())
+            h.update(b"\0")
+    return h.hexdigest()
+
+
 def traffic_for(workload, kernel_role):
-    """HBM bytes per launch of the role's kernel from the committed counter
-    summary, or None."""
+    """(HBM bytes per launch of the role's kernel from the committed counter
+    summary or None, where that figure comes from).  The figure is given only
+    when the summary was taken on a build of the same sources as this one."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, "no counter summary"
     with open(path) as f:
         t = json.load(f)
     e = t.get(workload, {}).get(kernel_role)
-    return None if e is None else e.get("bytes_per_launch")
+    if e is None:
+        return None, f"no counters for {workload} {kernel_role}"
+    build = t.get("build", {})
+    if build.get("kernel_sources_sha256") != kernel_sources_sha256():
+        return None, (f"counters of build {build.get('commit', '?')} ({e['bytes_per_launch']} B per launch of "
+                      f"{e['kernel']}); this build's kernel sources differ")
+    return e["bytes_per_launch"], f"counters of this build ({build.get('commit', '?')})"
 
 
 def reference_stream(workload):
@@ -328,7 +352,7 @@ def main():
 
     per_kernel = kernel_table(ms, nbytes, kind, cfg.wdtype)
     dom = max(per_kernel, key=lambda e: e["total_ms"])
-    traffic = traffic_for(args.workload, dom["role"])
+    traffic, traffic_source = traffic_for(args.workload, dom["role"])
 
     tok_s = args.steps / dt
     achieved = dom["achieved_gbs"]
@@ -358,7 +382,7 @@ def main():
         "topk_decode": "top_k 40, temperature 0.8, std::mt19937 seed 7; decode steps of one call (the graph "
                        "replays with the device sampler), prompt and first token subtracted",
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_source,
                      "kernel": dom["kernel"], "avg_launch_us": dom["avg_launch_us"],
                      "bytes_per_launch": dom["bytes_per_launch"], "launches": dom["launches"]},
         "per_kernel": per_kernel,

@@ -78,6 +78,18 @@ WORKLOADS = {
                           n_kv_heads=4, n_ffn=5632, eos=32002, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0001),
     "zephyr-q4": dict(arch=ZEPHYR, wdtype=Q4, n_vocab=100352, n_embd=2048, n_layers=24, n_heads=32,
                       n_kv_heads=32, n_ffn=5632, eos=100257, rope_pct=0.25, prompt=128, gen=128, seed=0x5EED0003),
+    # OpenELM's sm and md configurations (openelm/openelm.h:26-42) in Q8
+    "openelm-sm-q8": dict(arch=OPENELM, wdtype=Q8, n_vocab=32000, n_embd=1280, n_layers=16,
+                          n_heads=[12] * 5 + [16] * 7 + [20] * 4, n_kv_heads=[3] * 5 + [4] * 7 + [5] * 4,
+                          n_ffn=[768, 1024, 1280, 1536, 1792, 2048, 2560, 2816, 3072, 3328, 3584, 3840, 4352, 4608,
+                                 4864, 5120],
+                          eos=32002, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0006),
+    "openelm-md-q8": dict(arch=OPENELM, wdtype=Q8, n_vocab=32000, n_embd=1536, n_layers=20,
+                          n_heads=[12] * 3 + [16] * 7 + [20] * 6 + [24] * 4,
+                          n_kv_heads=[3] * 3 + [4] * 7 + [5] * 6 + [6] * 4,
+                          n_ffn=[768, 1024, 1280, 1536, 1792, 2304, 2560, 2816, 3072, 3328, 3584, 3840, 4096, 4352,
+                                 4608, 5120, 5376, 5632, 5888, 6144],
+                          eos=32002, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0007),
 }
 PROMPT_SEED_OFFSET = 0x1000
 

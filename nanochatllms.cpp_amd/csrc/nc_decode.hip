@@ -291,7 +291,7 @@ __global__ __launch_bounds__(NT) void k_dmv(DmvArgs A)
     }
 }
 
-// LM heads (32000 - 122753 rows of 2048 / 2304 values) read a second copy of
+// LM heads (32000 - 122753 rows of 1280 - 2304 values) read a second copy of
 // the weight in the head layout (k_head_layout): rows in groups of 16, and
 // per group and chunk of E blocks (Q4: 4, Q8: 2) the 16 rows x 4 lanes'
 // 16 bytes in (row, lane) order -- lane k's code dwords of the chunk's
@@ -666,6 +666,15 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
             if (epi == EPI_ARGMAX) return head_go<WT, PRO_RES_RMS, EPI_ARGMAX, 2, 72 / E>(A, st, ev0, ev1);
             return head_go<WT, PRO_RES_RMS, EPI_RAW, 2, 72 / E>(A, st, ev0, ev1);
         }
+        // OpenELM's narrower rows (1280, 1536 values)
+        if (A.nb == 40 && pro == PRO_RES_RMS) {
+            if (epi == EPI_ARGMAX) return head_go<WT, PRO_RES_RMS, EPI_ARGMAX, 1, 40 / E>(A, st, ev0, ev1);
+            return head_go<WT, PRO_RES_RMS, EPI_RAW, 1, 40 / E>(A, st, ev0, ev1);
+        }
+        if (A.nb == 48 && pro == PRO_RES_RMS) {
+            if (epi == EPI_ARGMAX) return head_go<WT, PRO_RES_RMS, EPI_ARGMAX, 1, 48 / E>(A, st, ev0, ev1);
+            return head_go<WT, PRO_RES_RMS, EPI_RAW, 1, 48 / E>(A, st, ev0, ev1);
+        }
         return fail(NC_ERR_ARG, "decode matvec: head layout rows of %d blocks, prologue %d", A.nb, pro);
     }
     if (pro == PRO_X) return dmv_r<WT, PRO_X, EPI_RAW, 1>(A, lds0, R, st, ev0, ev1);
@@ -707,14 +716,14 @@ bool decode_matvec_supported(int wdtype, int K, int N, int pro, int epi)
     if (K <= 0 || K % 32 || N <= 0 || !dmv_shape(K / 32, N, norm).rows) return false;
     if (norm && (K % kSsThreads || K > kDmvThreads * 8 * kDmvNormChunks)) return false;
     if (epi == EPI_ARGMAX && !norm) return false;
-    if (epi == EPI_SWIGLU && (N % 64 || (K != 2048 && K != 2304) || !norm)) return false;
+    if (epi == EPI_SWIGLU && (N % 64 || (K != 1280 && K != 1536 && K != 2048 && K != 2304) || !norm)) return false;
     return true;
 }
 
 bool head_layout_supported(int wdtype, int N, int K)
 {
     if (wdtype != NC_Q4 && wdtype != NC_Q8) return false;
-    return (K == 2048 || K == 2304) && N >= kHdGroup * (kDmvThreads / kWave);
+    return (K == 1280 || K == 1536 || K == 2048 || K == 2304) && N >= kHdGroup * (kDmvThreads / kWave);
 }
 
 int head_layout_bytes(int wdtype, int N, int K, size_t* code_bytes, size_t* delta_bytes)

@@ -270,8 +270,8 @@ int glu_dispatch(const DmvArgs& A, int wdtype, int pro, hipStream_t st, hipEvent
 {
     auto go = [&](auto wt) {
         constexpr int WT = decltype(wt)::value;
-        // gate|up rows of 2048 (64 blocks) or 2304 (72 blocks) values;
-        // layer_norm at 2048 only
+        // gate|up rows of 1280, 1536, 2048 or 2304 values (40, 48, 64, 72
+        // blocks); layer_norm at 2048 only
         if constexpr (kSpecGlu) {
             if (A.nb == 64) {
                 switch (pro) {
@@ -281,6 +281,12 @@ int glu_dispatch(const DmvArgs& A, int wdtype, int pro, hipStream_t st, hipEvent
                 default: return glu_spec_go<WT, PRO_RES_LN, 1, 64>(A, st, ev0, ev1);
                 }
             }
+            if (A.nb == 40)
+                return pro == PRO_RMS ? glu_spec_go<WT, PRO_RMS, 1, 40>(A, st, ev0, ev1)
+                                      : glu_spec_go<WT, PRO_RES_RMS, 1, 40>(A, st, ev0, ev1);
+            if (A.nb == 48)
+                return pro == PRO_RMS ? glu_spec_go<WT, PRO_RMS, 1, 48>(A, st, ev0, ev1)
+                                      : glu_spec_go<WT, PRO_RES_RMS, 1, 48>(A, st, ev0, ev1);
             return pro == PRO_RMS ? glu_spec_go<WT, PRO_RMS, 2, 72>(A, st, ev0, ev1)
                                   : glu_spec_go<WT, PRO_RES_RMS, 2, 72>(A, st, ev0, ev1);
         } else {
@@ -293,6 +299,14 @@ int glu_dispatch(const DmvArgs& A, int wdtype, int pro, hipStream_t st, hipEvent
                 case PRO_LN: return glu_go<WT, PRO_LN, 1, 64>(A, lds, st, ev0, ev1);
                 default: return glu_go<WT, PRO_RES_LN, 1, 64>(A, lds, st, ev0, ev1);
                 }
+            }
+            if (A.nb == 40) {
+                if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 40>(A, lds, st, ev0, ev1);
+                return glu_go<WT, PRO_RES_RMS, 1, 40>(A, lds, st, ev0, ev1);
+            }
+            if (A.nb == 48) {
+                if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 48>(A, lds, st, ev0, ev1);
+                return glu_go<WT, PRO_RES_RMS, 1, 48>(A, lds, st, ev0, ev1);
             }
             if (pro == PRO_RMS) return glu_go<WT, PRO_RMS, 1, 72>(A, lds, st, ev0, ev1);
             return glu_go<WT, PRO_RES_RMS, 1, 72>(A, lds, st, ev0, ev1);

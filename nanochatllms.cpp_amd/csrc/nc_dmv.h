@@ -569,7 +569,8 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
 int device_cus();
 
 // The gate|up launch with the SwiGLU epilogue (nc_decode_glu.hip): K = 32 nb
-// of 2048 or 2304, a norm prologue (rms_norm; layer_norm at K = 2048).
+// of 1280, 1536, 2048 or 2304, a norm prologue (rms_norm; layer_norm at
+// K = 2048).
 int glu_dispatch(const DmvArgs& A, int wdtype, int pro, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
 
 }  // namespace nc

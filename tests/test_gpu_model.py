@@ -97,7 +97,8 @@ def test_small_model_prefill_and_stream(gpu, oracle, name):
     m.close()
 
 
-FULL = ["tinyllama-q4", "tinyllama-q8", "openelm-q8", "zephyr-f16", "minicpm-q4", "tinyllama-f16", "zephyr-q4"]
+FULL = ["tinyllama-q4", "tinyllama-q8", "openelm-q8", "zephyr-f16", "minicpm-q4", "tinyllama-f16", "zephyr-q4",
+        "openelm-sm-q8", "openelm-md-q8"]
 
 
 @pytest.mark.parametrize("name", FULL)

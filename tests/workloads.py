@@ -70,6 +70,14 @@ WIDE = {
     "wide-openelm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=32000, n_embd=2048, n_layers=3,
                             n_heads=[16, 16, 20], n_kv_heads=[4, 4, 5], n_ffn=[1024, 4608, 8192], eos=-1,
                             rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0004),
+    # OpenELM sm and md widths (openelm/openelm.h:26-42: 1280 and 1536
+    # values), three of their layers' head and FFN widths
+    "wide-openelm-sm-q8": dict(arch=nc.OPENELM, wdtype=nc.Q8, n_vocab=32000, n_embd=1280, n_layers=3,
+                               n_heads=[12, 16, 20], n_kv_heads=[3, 4, 5], n_ffn=[768, 2816, 5120], eos=-1,
+                               rope_pct=1.0, prompt=16, gen=16, seed=0x7EE0009),
+    "wide-openelm-md-q4": dict(arch=nc.OPENELM, wdtype=nc.Q4, n_vocab=32000, n_embd=1536, n_layers=3,
+                               n_heads=[12, 16, 24], n_kv_heads=[3, 4, 6], n_ffn=[768, 3072, 6144], eos=-1,
+                               rope_pct=1.0, prompt=16, gen=16, seed=0x7EE000A),
 }
 
 # Long contexts: the reference's default inference context is 1024 positions
