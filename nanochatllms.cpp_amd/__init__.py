@@ -78,6 +78,12 @@ WORKLOADS = {
                           n_kv_heads=4, n_ffn=5632, eos=32002, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0001),
     "zephyr-q4": dict(arch=ZEPHYR, wdtype=Q4, n_vocab=100352, n_embd=2048, n_layers=24, n_heads=32,
                       n_kv_heads=32, n_ffn=5632, eos=100257, rope_pct=0.25, prompt=128, gen=128, seed=0x5EED0003),
+    "zephyr-q8": dict(arch=ZEPHYR, wdtype=Q8, n_vocab=100352, n_embd=2048, n_layers=24, n_heads=32,
+                      n_kv_heads=32, n_ffn=5632, eos=100257, rope_pct=0.25, prompt=128, gen=128, seed=0x5EED0003),
+    "minicpm-q8": dict(arch=MINICPM, wdtype=Q8, n_vocab=122753, n_embd=2304, n_layers=40, n_heads=36,
+                       n_kv_heads=36, n_ffn=5760, eos=2, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0004),
+    "minicpm-f16": dict(arch=MINICPM, wdtype=F16, n_vocab=122753, n_embd=2304, n_layers=40, n_heads=36,
+                        n_kv_heads=36, n_ffn=5760, eos=2, rope_pct=1.0, prompt=64, gen=128, seed=0x5EED0004),
     # OpenELM's sm and md configurations (openelm/openelm.h:26-42) in Q8
     "openelm-sm-q8": dict(arch=OPENELM, wdtype=Q8, n_vocab=32000, n_embd=1280, n_layers=16,
                           n_heads=[12] * 5 + [16] * 7 + [20] * 4, n_kv_heads=[3] * 5 + [4] * 7 + [5] * 4,

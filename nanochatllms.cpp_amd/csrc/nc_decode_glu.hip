@@ -1,7 +1,7 @@
 // nc_decode_glu.hip -- the gate|up matvec of the single-row decode step with
 // the SwiGLU epilogue (Q8 activations, Q4/Q8 weights): k_dmv_glu, and
 // k_dmv_glu_spec, which computes the weight terms, fold and SwiGLU beside the
-// exact norm sums from a predicted row (nc_dmv.h: spec_run).  The
+// exact norm sums from a predicted row (nc_dmv.h: spec_exact, spec_weights).  The
 // arithmetic is the reference's block dot product, fold order and
 // requantization points (tinyllama/tinyllama.cpp:88-97).
 #include "nc_dmv.h"
@@ -190,11 +190,10 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
         bar();
         if (s < 32) sq8 = swiglu(s, &sd16);
     };
-    auto commit = [&] {
-        if (s >= 0 && s < 32) store(s, sq8, sd16);
-    };
+    // the exact role's fold and epilogue from the exact terms (every exact
+    // thread folds one lane of one row)
     auto exact_tail = [&] {
-        if (tid < 64 * 4) fold(tid);
+        fold(tid);
         lds_barrier();
         if (tid < 32) {
             uint16_t d16;
@@ -204,14 +203,40 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
     };
     DmvArgs P = A;
     P.nb = NB;
-    spec_run<PRO, NCH, NS>(P, L, ssh, sgh, sy, load_w, terms, spec_tail, commit, exact_tail);
-    // further gate|up blocks of this workgroup (when the grid holds fewer
-    // workgroups than blocks): the exact row is in place
-    for (b += gridDim.x; b < nblk; b += gridDim.x) {
-        load_w();
-        terms(-2);
-        lds_barrier();
-        exact_tail();
+    // Further gate|up blocks of this workgroup (when the grid holds fewer
+    // workgroups than blocks) take the exact row already in place: terms by
+    // the weight role, then the exact role's tail.
+    if (__builtin_amdgcn_readfirstlane(tid) < kSpecExact) {
+        Q8Chunk qx[NCH];
+        spec_exact<PRO, NCH, NS>(P, L, ssh, sgh, sy, qx);
+        lds_barrier();  // B2
+        if (sy.anybad) {
+            spec_exact_fixup<NCH>(P, L, qx);
+            exact_tail();
+        }
+        for (b += gridDim.x; b < nblk; b += gridDim.x) {
+            lds_barrier();
+            exact_tail();
+        }
+    } else {
+        spec_weights<PRO, NCH, NS>(P, L, sy, load_w, terms, spec_tail);
+        lds_barrier();  // B2
+        if (!sy.anybad) {
+            if (s < 32) store(s, sq8, sd16);
+        } else {
+            // the differing blocks' terms from the exact row, then the
+            // exact role's tail
+            lds_barrier();  // B3
+            terms(-1);
+            lds_barrier();  // B4
+            lds_barrier();  // the exact tail's
+        }
+        for (b += gridDim.x; b < nblk; b += gridDim.x) {
+            load_w();
+            terms(-2);
+            lds_barrier();
+            lds_barrier();  // the exact tail's
+        }
     }
 }
 

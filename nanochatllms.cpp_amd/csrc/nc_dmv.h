@@ -236,12 +236,12 @@ constexpr int kGluThreads = 512;  // gate|up workgroup: 64 rows' block terms ove
 constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / threads, NB <= 72
 
 // ================================================ speculative norm rows ==
-// The norm-prologue launches (q|k|v, gate|up) with the weight-block terms
-// computed beside the exact sum of squares instead of after it.  Threads
-// 0-255 build the row and run the exact rms_norm as dmv_prologue does,
-// synchronizing among themselves through an LDS counter; the other threads
-// (256 or 512 more) hold the weights.  While the exact sum runs they
-// normalize the row with an approximate sum of squares (any order),
+// The gate|up norm-prologue launch with the weight-block terms computed
+// beside the exact norm sums instead of after them.  Threads 0-255 build the
+// row and run the exact norm as dmv_prologue does, synchronizing among
+// themselves through an LDS counter; the other 512 threads hold the
+// weights.  While the exact sums run they normalize the row with an
+// approximate sum of squares (and mean, for layer_norm; any order),
 // quantize it and compute every weight block's four terms against that row
 // as the weights arrive.  Once the exact sum is known, threads 0-255
 // quantize the exact row and compare it with the speculative one block by
@@ -327,19 +327,23 @@ struct SpecSync {
     float wsum1[kSpecExact / kWave];  // ... and of the values (layer_norm's predicted mean)
 };
 
-// The whole norm-prologue matvec but its final stores.  load_w(): the weight
-// threads' weight requests (a no-op on threads 0-255).  terms(ph): the
-// weight threads' block terms, ph = 1 (every item, from the speculative
-// row) or -1 (the items of the blocks that differ, from the exact row).
-// spec_tail(bar): the weight threads' fold and epilogue from the
-// speculative terms, held back (bar: their barrier, after every term is
-// stored).  commit(): stores the held results, when every block matched.
-// exact_tail(): otherwise, after the differing terms were recomputed: the
-// fold and epilogue from the exact terms.  NS: weight threads.
-template <int PRO, int NCH, int NS, class LoadW, class Terms, class SpecTail, class Commit, class ExactTail>
-__device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsShared& ssh, SgShared& sgh, SpecSync& sy,
-                                         LoadW&& load_w, Terms&& terms, SpecTail&& spec_tail, Commit&& commit,
-                                         ExactTail&& exact_tail)
+// The two roles of a speculative norm launch.  The workgroup's first
+// kSpecExact threads (the exact role) and the others (the weight role) run
+// separate code: the kernel branches on a wave-uniform role, so the weight
+// registers are not live on the exact role's path and each role's code is
+// allocated registers of its own.  Both roles pass the same workgroup
+// barriers in the same order:
+//   B1  the row, its partial sums and the norm inputs are in LDS;
+//   B2  the exact role has compared the rows, the weight role has held its
+//       results (sy.anybad tells both what follows);
+//   when a block differs: B3 exact row stored, B4 its terms recomputed,
+//   then the kernel's exact tail (its own barriers).
+
+// Exact role, up to B2 (B2 not passed).  Returns the exact row's chunks in
+// qx (stored over the speculative row by the caller when a block differs).
+template <int PRO, int NCH, int NS>
+__device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, SsShared& ssh, SgShared& sgh,
+                                           SpecSync& sy, Q8Chunk (&qx)[NCH])
 {
     constexpr int NT = kSpecExact;
     constexpr bool RES = pro_res(PRO), LN = pro_ln(PRO);
@@ -347,7 +351,6 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int nb = A.nb, K = nb * 32;
     const int nch = K / 8;
-    const bool ex = tid < NT;
     float h[NCH][8], gain[NCH][8], bias[NCH][8], av[NCH][8], ov[NCH][8];
     const bool fixed = !RES ? A.x_pitch == 0 : A.res_cur != nullptr;
     int pos = A.pos;
@@ -356,213 +359,210 @@ __device__ __forceinline__ void spec_run(const DmvArgs& A, const SpecLds& L, SsS
         sy.spec = 0;
         sy.anybad = 0;
     }
-    if (ex) {
-        // the exact side is the critical path: its wavefronts issue first
-        __builtin_amdgcn_s_setprio(3);
-        const uint8_t* arow;
-        if (fixed) {
-            arow = !RES ? A.x : A.res_cur;
-        } else {
-            if (A.dpos) pos = load_pos(A.dpos);
-            arow = !RES ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
-        }
-#pragma unroll
-        for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * NT;
-            const int cc = ch < nch ? ch : 0;
-            load_act_chunk(arow, K, cc, av[j]);
-            if (RES) load_f32_chunk(A.raw_in, cc, ov[j]);
-            const uint4 gw = reinterpret_cast<const uint4*>(A.norm_w)[cc];
-            const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
-#pragma unroll
-            for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
-            if (LN) {
-                const uint4 bw = reinterpret_cast<const uint4*>(A.norm_b)[cc];
-                const uint32_t bws[4] = {bw.x, bw.y, bw.z, bw.w};
-#pragma unroll
-                for (int i = 0; i < 8; i++) bias[j][i] = h2f((uint16_t)(bws[i >> 1] >> (16 * (i & 1))));
-            }
-        }
+    // the critical path: these wavefronts issue first
+    __builtin_amdgcn_s_setprio(3);
+    const uint8_t* arow;
+    if (fixed) {
+        arow = !RES ? A.x : A.res_cur;
+    } else {
+        if (A.dpos) pos = load_pos(A.dpos);
+        arow = !RES ? A.x + (size_t)pos * A.x_pitch : A.res_in + (size_t)pos * A.res_pitch;
     }
-    __builtin_amdgcn_sched_barrier(0);
-    int posv = 0;
-    if (ex && fixed && A.dpos) posv = load_pos(A.dpos);
-    __builtin_amdgcn_sched_barrier(0);
-    load_w();
-    __builtin_amdgcn_sched_barrier(0);
-    if (ex) {
-        if (fixed && A.dpos) pos = posv;
-        float part = 0.0f, part1 = 0.0f;  // this thread's squares and values, for the prediction
 #pragma unroll
-        for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * NT;
-            const bool valid = ch < nch;
-            if (j * NT >= nch) break;  // uniform
-            if (RES) {
-                quad_roundtrip(ov[j]);
-                if (A.bscale != 1.0f) {
+    for (int j = 0; j < NCH; j++) {
+        const int ch = tid + j * NT;
+        const int cc = ch < nch ? ch : 0;
+        load_act_chunk(arow, K, cc, av[j]);
+        if (RES) load_f32_chunk(A.raw_in, cc, ov[j]);
+        const uint4 gw = reinterpret_cast<const uint4*>(A.norm_w)[cc];
+        const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
-                    for (int i = 0; i < 8; i++) ov[j][i] = ov[j][i] * A.bscale;
-                    quad_roundtrip(ov[j]);
-                }
-                float sm[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) sm[i] = av[j][i] + ov[j][i];
-                const Q8Chunk q = quad_quantize(sm);
-                if (valid && blockIdx.x == 0) {
-                    store_act_chunk(A.res_out + (size_t)pos * A.res_pitch, K, ch, q);
-                    if (A.res_cur_out) store_act_chunk(A.res_cur_out, K, ch, q);
-                }
-                const float d = h2f(q.d16);
-#pragma unroll
-                for (int i = 0; i < 8; i++) h[j][i] = (float)q.q[i] * d;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) h[j][i] = av[j][i];
-            }
-            if (valid) {
-                float sqv[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) sqv[i] = h[j][i] * h[j][i];
-                // the first exact sum's terms: the squares (rms_norm) or the values (layer_norm)
-                const float(&t)[8] = LN ? h[j] : sqv;
-                float4* sq4 = reinterpret_cast<float4*>(L.sq) + 2 * ch;
-                sq4[0] = make_float4(t[0], t[1], t[2], t[3]);
-                sq4[1] = make_float4(t[4], t[5], t[6], t[7]);
-                part = part + (((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + ((sqv[4] + sqv[5]) + (sqv[6] + sqv[7])));
-                if (LN)
-                    part1 = part1 + (((h[j][0] + h[j][1]) + (h[j][2] + h[j][3])) +
-                                     ((h[j][4] + h[j][5]) + (h[j][6] + h[j][7])));
-                float4* h4 = reinterpret_cast<float4*>(L.h) + 2 * ch;
-                h4[0] = make_float4(h[j][0], h[j][1], h[j][2], h[j][3]);
-                h4[1] = make_float4(h[j][4], h[j][5], h[j][6], h[j][7]);
-                float4* g4 = reinterpret_cast<float4*>(L.g) + 2 * ch;
-                g4[0] = make_float4(gain[j][0], gain[j][1], gain[j][2], gain[j][3]);
-                g4[1] = make_float4(gain[j][4], gain[j][5], gain[j][6], gain[j][7]);
-                if (LN) {
-                    float4* b4 = reinterpret_cast<float4*>(L.b) + 2 * ch;
-                    b4[0] = make_float4(bias[j][0], bias[j][1], bias[j][2], bias[j][3]);
-                    b4[1] = make_float4(bias[j][4], bias[j][5], bias[j][6], bias[j][7]);
-                }
-            }
-        }
-        part = wave_scan_add(part);
-        if (lane == kWave - 1) sy.wsum[tid / kWave] = part;
+        for (int i = 0; i < 8; i++) gain[j][i] = h2f((uint16_t)(gws[i >> 1] >> (16 * (i & 1))));
         if (LN) {
-            part1 = wave_scan_add(part1);
-            if (lane == kWave - 1) sy.wsum1[tid / kWave] = part1;
+            const uint4 bw = reinterpret_cast<const uint4*>(A.norm_b)[cc];
+            const uint32_t bws[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) bias[j][i] = h2f((uint16_t)(bws[i >> 1] >> (16 * (i & 1))));
         }
     }
-    lds_barrier();
-    Q8Chunk qx[NCH];
-    if (ex) {
-        // the exact sums on threads 0-255, then the exact row (held until
-        // the speculative side is done)
-        SsWaveBarrier<NT / kWave> bar{&sy.exact, 0};
-        float mean = 0.0f;
-        if constexpr (LN) {
-            // layer_norm (gten/ops.cpp:669-698): the mean, the exact sum of
-            // the Q8 row's values (on the fp16 grid), then the squared
-            // deviations over the values in sq
-            mean = block_seq_sum_grid<8, NT>(L.sq, sgh, nullptr, bar) / (float)K;
-            const int ch = tid;
-            float t[8];
+    __builtin_amdgcn_sched_barrier(0);
+    if (fixed && A.dpos) pos = load_pos(A.dpos);
+    float part = 0.0f, part1 = 0.0f;  // this thread's squares and values, for the prediction
 #pragma unroll
-            for (int i = 0; i < 8; i++) t[i] = (h[0][i] - mean) * (h[0][i] - mean);
+    for (int j = 0; j < NCH; j++) {
+        const int ch = tid + j * NT;
+        const bool valid = ch < nch;
+        if (j * NT >= nch) break;  // uniform
+        if (RES) {
+            quad_roundtrip(ov[j]);
+            if (A.bscale != 1.0f) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) ov[j][i] = ov[j][i] * A.bscale;
+                quad_roundtrip(ov[j]);
+            }
+            float sm[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) sm[i] = av[j][i] + ov[j][i];
+            const Q8Chunk q = quad_quantize(sm);
+            if (valid && blockIdx.x == 0) {
+                store_act_chunk(A.res_out + (size_t)pos * A.res_pitch, K, ch, q);
+                if (A.res_cur_out) store_act_chunk(A.res_cur_out, K, ch, q);
+            }
+            const float d = h2f(q.d16);
+#pragma unroll
+            for (int i = 0; i < 8; i++) h[j][i] = (float)q.q[i] * d;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) h[j][i] = av[j][i];
+        }
+        if (valid) {
+            float sqv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) sqv[i] = h[j][i] * h[j][i];
+            // the first exact sum's terms: the squares (rms_norm) or the values (layer_norm)
+            const float(&t)[8] = LN ? h[j] : sqv;
             float4* sq4 = reinterpret_cast<float4*>(L.sq) + 2 * ch;
             sq4[0] = make_float4(t[0], t[1], t[2], t[3]);
             sq4[1] = make_float4(t[4], t[5], t[6], t[7]);
-            bar();
-        }
-        const float ss = block_seq_sum_nonneg_bar(L.sq, K, ssh, bar);
-        const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
-#pragma unroll
-        for (int j = 0; j < NCH; j++) {
-            if (j * NT >= nch) break;  // uniform
-            qx[j] = spec_norm_chunk<LN>(h[j], gain[j], bias[j], mean, denom, A.post_scale);
-        }
-        // once the speculative row is complete (every weight wavefront has
-        // passed its first barrier), compare it block by block with the
-        // exact one (a lane quad holds a block) while the weight threads
-        // finish
-        while (__hip_atomic_load(&sy.spec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NS / kWave) {
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        int any = 0;
-#pragma unroll
-        for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * NT;
-            if (j * NT >= nch) break;  // uniform
-            const bool valid = ch < nch;
-            const int cc = valid ? ch : 0;
-            const Q8Chunk& q = qx[j];
-            const uint2 sc = *reinterpret_cast<const uint2*>(L.row + (size_t)cc * 8);
-            const uint16_t sd = reinterpret_cast<const uint16_t*>(L.row + K)[cc >> 2];
-            uint32_t w[2] = {0, 0};
-#pragma unroll
-            for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q.q[i] << (8 * (i & 3));
-            int diff = valid && (sc.x != w[0] || sc.y != w[1] || sd != q.d16) ? 1 : 0;
-            diff |= dpp_i<kDppQuadXor1>(diff);
-            diff |= dpp_i<kDppQuadXor2>(diff);
-            any |= diff;
-            if (valid && (ch & 3) == 0) L.bad[ch >> 2] = (uint8_t)diff;
-        }
-        if (__builtin_amdgcn_ballot_w64(any != 0) && lane == 0) sy.anybad = 1;
-        __builtin_amdgcn_s_setprio(0);
-    } else {
-        // the speculative row (weight threads 0-255, a quad per block), a
-        // barrier among the weight threads, every block's terms, then the
-        // fold and epilogue
-        const int sc = tid - NT;
-        if (sc < NT) {
-            const float s2 = ((sy.wsum[0] + sy.wsum[1]) + sy.wsum[2]) + sy.wsum[3];
-            float mn = 0.0f, dn;
+            part = part + (((sqv[0] + sqv[1]) + (sqv[2] + sqv[3])) + ((sqv[4] + sqv[5]) + (sqv[6] + sqv[7])));
+            if (LN)
+                part1 = part1 + (((h[j][0] + h[j][1]) + (h[j][2] + h[j][3])) +
+                                 ((h[j][4] + h[j][5]) + (h[j][6] + h[j][7])));
+            float4* h4 = reinterpret_cast<float4*>(L.h) + 2 * ch;
+            h4[0] = make_float4(h[j][0], h[j][1], h[j][2], h[j][3]);
+            h4[1] = make_float4(h[j][4], h[j][5], h[j][6], h[j][7]);
+            float4* g4 = reinterpret_cast<float4*>(L.g) + 2 * ch;
+            g4[0] = make_float4(gain[j][0], gain[j][1], gain[j][2], gain[j][3]);
+            g4[1] = make_float4(gain[j][4], gain[j][5], gain[j][6], gain[j][7]);
             if (LN) {
-                // mean and variance from the sums of the values and squares
-                mn = (((sy.wsum1[0] + sy.wsum1[1]) + sy.wsum1[2]) + sy.wsum1[3]) / (float)K;
-                const float var = fmaxf(s2 / (float)K - mn * mn, 0.0f) * A.spec_skew;
-                dn = sqrtf(var) + 1e-05f;
-            } else {
-                dn = sqrtf(s2 * A.spec_skew / (float)K) + 1e-6f;
-            }
-#pragma unroll
-            for (int j = 0; j < NCH; j++) {
-                const int ch = sc + j * NT;
-                if (j * NT >= nch) break;  // uniform
-                const int cc = ch < nch ? ch : 0;
-                float hv[8], gv[8], bv[8];
-                load_f32_chunk(L.h, cc, hv);
-                load_f32_chunk(L.g, cc, gv);
-                if (LN) load_f32_chunk(L.b, cc, bv);
-                const Q8Chunk q = spec_norm_chunk<LN>(hv, gv, bv, mn, dn, A.post_scale);
-                if (ch < nch) store_act_chunk(L.row, K, ch, q);
+                float4* b4 = reinterpret_cast<float4*>(L.b) + 2 * ch;
+                b4[0] = make_float4(bias[j][0], bias[j][1], bias[j][2], bias[j][3]);
+                b4[1] = make_float4(bias[j][4], bias[j][5], bias[j][6], bias[j][7]);
             }
         }
-        SsWaveBarrier<NS / kWave> sbar{&sy.spec, 0};
-        sbar();
-        terms(1);
-        spec_tail(sbar);
     }
-    lds_barrier();
-    if (!sy.anybad) {
-        commit();
-        return;
+    part = wave_scan_add(part);
+    if (lane == kWave - 1) sy.wsum[tid / kWave] = part;
+    if (LN) {
+        part1 = wave_scan_add(part1);
+        if (lane == kWave - 1) sy.wsum1[tid / kWave] = part1;
     }
-    // some block differs: the exact row over the speculative one, the
-    // differing blocks' terms recomputed, and the fold and epilogue again
-    if (A.spec_fixups && tid == 0) atomicAdd(A.spec_fixups, 1);
-    if (ex) {
+    lds_barrier();  // B1
+    // the exact sums, then the exact row (held until the weight role is done)
+    SsWaveBarrier<NT / kWave> bar{&sy.exact, 0};
+    float mean = 0.0f;
+    if constexpr (LN) {
+        // layer_norm (gten/ops.cpp:669-698): the mean, the exact sum of the
+        // Q8 row's values (on the fp16 grid), then the squared deviations
+        // over the values in sq
+        mean = block_seq_sum_grid<8, NT>(L.sq, sgh, nullptr, bar) / (float)K;
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) t[i] = (h[0][i] - mean) * (h[0][i] - mean);
+        float4* sq4 = reinterpret_cast<float4*>(L.sq) + 2 * tid;
+        sq4[0] = make_float4(t[0], t[1], t[2], t[3]);
+        sq4[1] = make_float4(t[4], t[5], t[6], t[7]);
+        bar();
+    }
+    const float ss = block_seq_sum_nonneg_bar(L.sq, K, ssh, bar);
+    const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        if (j * NT >= nch) break;  // uniform
+        qx[j] = spec_norm_chunk<LN>(h[j], gain[j], bias[j], mean, denom, A.post_scale);
+    }
+    // once the speculative row is complete (every weight wavefront has
+    // passed its first barrier), compare it block by block with the exact
+    // one (a lane quad holds a block) while the weight role finishes
+    while (__hip_atomic_load(&sy.spec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NS / kWave) {
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    int any = 0;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int ch = tid + j * NT;
+        if (j * NT >= nch) break;  // uniform
+        const bool valid = ch < nch;
+        const int cc = valid ? ch : 0;
+        const Q8Chunk& q = qx[j];
+        const uint2 sc = *reinterpret_cast<const uint2*>(L.row + (size_t)cc * 8);
+        const uint16_t sd = reinterpret_cast<const uint16_t*>(L.row + K)[cc >> 2];
+        uint32_t w[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q.q[i] << (8 * (i & 3));
+        int diff = valid && (sc.x != w[0] || sc.y != w[1] || sd != q.d16) ? 1 : 0;
+        diff |= dpp_i<kDppQuadXor1>(diff);
+        diff |= dpp_i<kDppQuadXor2>(diff);
+        any |= diff;
+        if (valid && (ch & 3) == 0) L.bad[ch >> 2] = (uint8_t)diff;
+    }
+    if (__builtin_amdgcn_ballot_w64(any != 0) && lane == 0) sy.anybad = 1;
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// The exact role's stores after B2 when a block differs: the exact row over
+// the speculative one, then B3 and B4 (the weight role recomputes the
+// differing blocks' terms between them).
+template <int NCH>
+__device__ __forceinline__ void spec_exact_fixup(const DmvArgs& A, const SpecLds& L, const Q8Chunk (&qx)[NCH])
+{
+    constexpr int NT = kSpecExact;
+    const int K = A.nb * 32, nch = K / 8;
+    if (A.spec_fixups && threadIdx.x == 0) atomicAdd(A.spec_fixups, 1);
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int ch = threadIdx.x + j * NT;
+        if (j * NT >= nch) break;  // uniform
+        if (ch < nch) store_act_chunk(L.row, K, ch, qx[j]);
+    }
+    lds_barrier();  // B3
+    lds_barrier();  // B4
+}
+
+// Weight role, up to B2 (B2 not passed): the weight requests, B1, the
+// speculative row (its first 256 threads, a quad per block), a barrier among
+// the weight wavefronts, every block's terms from that row (terms(1)), then
+// spec_tail(bar): the fold and epilogue from those terms, held back.  NS:
+// the weight role's threads.
+template <int PRO, int NCH, int NS, class LoadW, class Terms, class SpecTail>
+__device__ __forceinline__ void spec_weights(const DmvArgs& A, const SpecLds& L, SpecSync& sy, LoadW&& load_w,
+                                             Terms&& terms, SpecTail&& spec_tail)
+{
+    constexpr int NT = kSpecExact;
+    constexpr bool LN = pro_ln(PRO);
+    const int nb = A.nb, K = nb * 32;
+    const int nch = K / 8;
+    load_w();
+    lds_barrier();  // B1
+    const int sc = threadIdx.x - NT;
+    if (sc < NT) {
+        const float s2 = ((sy.wsum[0] + sy.wsum[1]) + sy.wsum[2]) + sy.wsum[3];
+        float mn = 0.0f, dn;
+        if (LN) {
+            // mean and variance from the sums of the values and squares
+            mn = (((sy.wsum1[0] + sy.wsum1[1]) + sy.wsum1[2]) + sy.wsum1[3]) / (float)K;
+            const float var = fmaxf(s2 / (float)K - mn * mn, 0.0f) * A.spec_skew;
+            dn = sqrtf(var) + 1e-05f;
+        } else {
+            dn = sqrtf(s2 * A.spec_skew / (float)K) + 1e-6f;
+        }
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
-            const int ch = tid + j * NT;
+            const int ch = sc + j * NT;
             if (j * NT >= nch) break;  // uniform
-            if (ch < nch) store_act_chunk(L.row, K, ch, qx[j]);
+            const int cc = ch < nch ? ch : 0;
+            float hv[8], gv[8], bv[8];
+            load_f32_chunk(L.h, cc, hv);
+            load_f32_chunk(L.g, cc, gv);
+            if (LN) load_f32_chunk(L.b, cc, bv);
+            const Q8Chunk q = spec_norm_chunk<LN>(hv, gv, bv, mn, dn, A.post_scale);
+            if (ch < nch) store_act_chunk(L.row, K, ch, q);
         }
     }
-    lds_barrier();
-    terms(-1);
-    lds_barrier();
-    exact_tail();
+    SsWaveBarrier<NS / kWave> sbar{&sy.spec, 0};
+    sbar();
+    terms(1);
+    spec_tail(sbar);
 }
 
 // Compute units of the current device.

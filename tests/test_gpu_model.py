@@ -98,7 +98,7 @@ def test_small_model_prefill_and_stream(gpu, oracle, name):
 
 
 FULL = ["tinyllama-q4", "tinyllama-q8", "openelm-q8", "zephyr-f16", "minicpm-q4", "tinyllama-f16", "zephyr-q4",
-        "openelm-sm-q8", "openelm-md-q8"]
+        "openelm-sm-q8", "openelm-md-q8", "zephyr-q8", "minicpm-q8", "minicpm-f16"]
 
 
 @pytest.mark.parametrize("name", FULL)
