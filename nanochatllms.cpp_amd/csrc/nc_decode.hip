@@ -291,6 +291,117 @@ __global__ __launch_bounds__(NT) void k_dmv(DmvArgs A)
     }
 }
 
+// The norm-prologue matvec of one group of R rows per workgroup (q|k|v)
+// with the weight terms and the fold computed beside the exact norm sums
+// from a predicted row (nc_dmv.h: spec_exact, spec_weights): kSpecExact
+// threads of the exact role and kDmvThreads of the weight role, which holds
+// the group's weights (IT blocks per thread; a thread's blocks are all the
+// same block column, NB dividing kDmvThreads).  Raw fp32 outputs.
+template <int WT, int IT, int PRO, int NCH, int NB>
+__global__ __launch_bounds__(kSpecExact + kDmvThreads) void k_dmv_spec(DmvArgs A)
+{
+    constexpr int NS = kDmvThreads;
+    constexpr int WD = WT == Q4 ? 4 : 8;
+    constexpr int WV = WD / 4;
+    constexpr int TP = ((NB + 3) & ~3) + 4;
+    static_assert(NS % NB == 0, "a weight thread's blocks share one block column");
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ SsShared ssh;
+    __shared__ SgShared sgh;
+    __shared__ SpecSync sy;
+    const int R = A.rows, nitems = R * NB;
+    float* T = reinterpret_cast<float*>(lds);  // R rows x 4 lanes x TP
+    const SpecLds L = spec_lds(T + R * 4 * TP, NB, pro_ln(PRO));
+    const int tid = threadIdx.x, s = tid - kSpecExact;
+    const int col = s & (NB - 1);  // the thread's block column (NB a power of two here)
+
+    uint4 w[IT][WV];
+    uint16_t dw[IT];
+    int g = blockIdx.x;
+    auto load_w = [&] {
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            // every slot loads (items past the group and rows past N: block
+            // 0), so the waits for these loads are exact counts
+            const int j = s + it * NS;
+            const int r = j / NB;
+            const size_t b = j < nitems && g * R + r < A.N ? (size_t)(g * R + r) * NB + col : 0;
+            const uint4* src = reinterpret_cast<const uint4*>(A.wq + b * WD);
+#pragma unroll
+            for (int v = 0; v < WV; v++) w[it][v] = load_stream(src + v);
+            dw[it] = load_stream(A.wd + b);
+        }
+    };
+    // ph 1: every item from the speculative row; -1: the items of a block
+    // column that differs, from the exact row; -2: every item from the exact
+    // row (a further group of this workgroup)
+    auto terms = [&](int ph) {
+        if (ph == -1 && !L.bad[col]) return;
+        const StagedX x = make_staged(load_x_block(L.row, NB, col));
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int j = s + it * NS;
+            if (j >= nitems) continue;
+            float tv[4];
+            q_block_terms<WT>(x, w[it], dw[it], tv);
+            float* t = T + (j / NB) * 4 * TP + col;
+#pragma unroll
+            for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
+        }
+    };
+    // thread 4r + k folds lane k of row r in block order; lane 4r's result
+    auto fold = [&](int t) {
+        const float acc = seq_sum<16>(T + t * TP, NB);
+        return (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
+    };
+    auto store = [&](int t, float res) {
+        const int row = g * R + (t >> 2);
+        if ((t & 3) == 0 && row < A.N) A.raw[row] = res;
+    };
+    float sres = 0.0f;
+    auto spec_tail = [&](auto& bar) {
+        bar();
+        if (s < 4 * R) sres = fold(s);
+    };
+    auto exact_tail = [&] {
+        if (tid < 4 * R) store(tid, fold(tid));
+    };
+    DmvArgs P = A;
+    P.nb = NB;
+    if (__builtin_amdgcn_readfirstlane(tid) < kSpecExact) {
+        Q8Chunk qx[NCH];
+        spec_exact<PRO, NCH, NS>(P, L, ssh, sgh, sy, qx);
+        lds_barrier();  // B2
+        if (sy.anybad) {
+            spec_exact_fixup<NCH>(P, L, qx);
+            exact_tail();
+            lds_barrier();  // B5: the folds done (the terms may be overwritten)
+        }
+        for (g += gridDim.x; g < A.ngroups; g += gridDim.x) {
+            lds_barrier();  // the group's terms
+            exact_tail();
+            lds_barrier();  // its folds done
+        }
+    } else {
+        spec_weights<PRO, NCH, NS>(P, L, sy, load_w, terms, spec_tail);
+        lds_barrier();  // B2
+        if (!sy.anybad) {
+            if (s < 4 * R) store(s, sres);
+        } else {
+            lds_barrier();  // B3
+            terms(-1);
+            lds_barrier();  // B4
+            lds_barrier();  // B5
+        }
+        for (g += gridDim.x; g < A.ngroups; g += gridDim.x) {
+            load_w();
+            terms(-2);
+            lds_barrier();
+            lds_barrier();
+        }
+    }
+}
+
 // LM heads (32000 - 122753 rows of 1280 - 2304 values) read a second copy of
 // the weight in the head layout (k_head_layout): rows in groups of 16, and
 // per group and chunk of E blocks (Q4: 4, Q8: 2) the 16 rows x 4 lanes'
@@ -582,6 +693,32 @@ int head_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
     return launch_status("k_dmv_head");
 }
 
+// The speculative q|k|v launch (k_dmv_spec): one group of R rows per
+// workgroup, every workgroup resident at once.
+template <int WT, int IT, int PRO, int NCH, int NB>
+int dmv_spec_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
+{
+    constexpr int TP = ((NB + 3) & ~3) + 4;
+    auto kern = k_dmv_spec<WT, IT, PRO, NCH, NB>;
+    const size_t lds = (size_t)A.rows * 4 * TP * 4 + spec_lds_bytes(NB, pro_ln(PRO));
+    A.ngroups = (A.N + A.rows - 1) / A.rows;
+    const dim3 grid(A.ngroups);
+    const dim3 block(kSpecExact + kDmvThreads);
+    if (ev0)
+        hipExtLaunchKernelGGL(kern, grid, block, lds, st, ev0, ev1, 0, A);
+    else
+        hipLaunchKernelGGL(kern, grid, block, lds, st, A);
+    return launch_status("k_dmv_spec");
+}
+
+// Speculative q|k|v (k_dmv_spec) for norm-prologue launches of rows of 2048
+// values spread one group per CU with four blocks per weight thread
+// (TinyLlama's 16-row groups: 1,489 -> 1,506 tok/s in an on-box A/B).  With
+// fewer blocks per thread the weight terms are too short to hide much of
+// the exact sum, and the wider workgroup costs more than it saves (OpenELM's
+// 8-row groups: 1,059 -> 1,046 tok/s), so those keep k_dmv.
+constexpr bool kSpecQkv = true;
+
 // Launch with the items per thread the group needs (1, 2, 4, 8 or 12).
 template <int WT, int PRO, int EPI, int NCH>
 int dmv_r(DmvArgs A, size_t lds0, DmvShape sh, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
@@ -685,6 +822,12 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
             });
         return with_pro<1>(
             pro, [&](auto p) { return dmv_r<WT, decltype(p)::value, EPI_ARGMAX, 1>(A, lds0, R, st, ev0, ev1); });
+    }
+    if (kSpecQkv && R.spread && A.nb == 64 && R.rows * A.nb == kDmvThreads * 4) {
+        DmvArgs As = A;
+        As.rows = R.rows;
+        return with_pro<1>(
+            pro, [&](auto p) { return dmv_spec_go<WT, 4, decltype(p)::value, 1, 64>(As, st, ev0, ev1); });
     }
     if (R.spread && R.rows * A.nb > kDmvThreads * 4 && R.rows * A.nb <= kDmvWideThreads * 6) {
         if (K > (size_t)kDmvWideThreads * 8) {
