@@ -294,17 +294,16 @@ __global__ __launch_bounds__(NT) void k_dmv(DmvArgs A)
 // The norm-prologue matvec of one group of R rows per workgroup (q|k|v)
 // with the weight terms and the fold computed beside the exact norm sums
 // from a predicted row (nc_dmv.h: spec_exact, spec_weights): kSpecExact
-// threads of the exact role and kDmvThreads of the weight role, which holds
-// the group's weights (IT blocks per thread; a thread's blocks are all the
-// same block column, NB dividing kDmvThreads).  Raw fp32 outputs.
-template <int WT, int IT, int PRO, int NCH, int NB>
-__global__ __launch_bounds__(kSpecExact + kDmvThreads) void k_dmv_spec(DmvArgs A)
+// threads of the exact role and NS of the weight role, which holds the
+// group's weights (IT blocks per thread; where NB divides NS a thread's
+// blocks are all the same block column).  Raw fp32 outputs.
+template <int WT, int IT, int PRO, int NCH, int NB, int NS>
+__global__ __launch_bounds__(kSpecExact + NS) void k_dmv_spec(DmvArgs A)
 {
-    constexpr int NS = kDmvThreads;
     constexpr int WD = WT == Q4 ? 4 : 8;
     constexpr int WV = WD / 4;
     constexpr int TP = ((NB + 3) & ~3) + 4;
-    static_assert(NS % NB == 0, "a weight thread's blocks share one block column");
+    constexpr bool kOne = NS % NB == 0;
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ SsShared ssh;
     __shared__ SgShared sgh;
@@ -313,7 +312,7 @@ __global__ __launch_bounds__(kSpecExact + kDmvThreads) void k_dmv_spec(DmvArgs A
     float* T = reinterpret_cast<float*>(lds);  // R rows x 4 lanes x TP
     const SpecLds L = spec_lds(T + R * 4 * TP, NB, pro_ln(PRO));
     const int tid = threadIdx.x, s = tid - kSpecExact;
-    const int col = s & (NB - 1);  // the thread's block column (NB a power of two here)
+    const int col = s % NB;  // the thread's block column (kOne)
 
     uint4 w[IT][WV];
     uint16_t dw[IT];
@@ -324,8 +323,8 @@ __global__ __launch_bounds__(kSpecExact + kDmvThreads) void k_dmv_spec(DmvArgs A
             // every slot loads (items past the group and rows past N: block
             // 0), so the waits for these loads are exact counts
             const int j = s + it * NS;
-            const int r = j / NB;
-            const size_t b = j < nitems && g * R + r < A.N ? (size_t)(g * R + r) * NB + col : 0;
+            const int r = j / NB, i = j - r * NB;
+            const size_t b = j < nitems && g * R + r < A.N ? (size_t)(g * R + r) * NB + i : 0;
             const uint4* src = reinterpret_cast<const uint4*>(A.wq + b * WD);
 #pragma unroll
             for (int v = 0; v < WV; v++) w[it][v] = load_stream(src + v);
@@ -336,15 +335,18 @@ __global__ __launch_bounds__(kSpecExact + kDmvThreads) void k_dmv_spec(DmvArgs A
     // column that differs, from the exact row; -2: every item from the exact
     // row (a further group of this workgroup)
     auto terms = [&](int ph) {
-        if (ph == -1 && !L.bad[col]) return;
-        const StagedX x = make_staged(load_x_block(L.row, NB, col));
+        if (kOne && ph == -1 && !L.bad[col]) return;
+        StagedX x0;
+        if (kOne) x0 = make_staged(load_x_block(L.row, NB, col));
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int j = s + it * NS;
             if (j >= nitems) continue;
+            const int r = j / NB, i = j - r * NB;
+            if (!kOne && ph == -1 && !L.bad[i]) continue;
             float tv[4];
-            q_block_terms<WT>(x, w[it], dw[it], tv);
-            float* t = T + (j / NB) * 4 * TP + col;
+            q_block_terms<WT>(kOne ? x0 : make_staged(load_x_block(L.row, NB, i)), w[it], dw[it], tv);
+            float* t = T + r * 4 * TP + i;
 #pragma unroll
             for (int k = 0; k < 4; k++) t[k * TP] = tv[k];
         }
@@ -363,6 +365,7 @@ __global__ __launch_bounds__(kSpecExact + kDmvThreads) void k_dmv_spec(DmvArgs A
         bar();
         if (s < 4 * R) sres = fold(s);
     };
+    // the exact role folds R <= 64 rows: one lane of one row per thread
     auto exact_tail = [&] {
         if (tid < 4 * R) store(tid, fold(tid));
     };
@@ -695,15 +698,15 @@ int head_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 
 // The speculative q|k|v launch (k_dmv_spec): one group of R rows per
 // workgroup, every workgroup resident at once.
-template <int WT, int IT, int PRO, int NCH, int NB>
+template <int WT, int IT, int PRO, int NCH, int NB, int NS>
 int dmv_spec_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 {
     constexpr int TP = ((NB + 3) & ~3) + 4;
-    auto kern = k_dmv_spec<WT, IT, PRO, NCH, NB>;
+    auto kern = k_dmv_spec<WT, IT, PRO, NCH, NB, NS>;
     const size_t lds = (size_t)A.rows * 4 * TP * 4 + spec_lds_bytes(NB, pro_ln(PRO));
     A.ngroups = (A.N + A.rows - 1) / A.rows;
     const dim3 grid(A.ngroups);
-    const dim3 block(kSpecExact + kDmvThreads);
+    const dim3 block(kSpecExact + NS);
     if (ev0)
         hipExtLaunchKernelGGL(kern, grid, block, lds, st, ev0, ev1, 0, A);
     else
@@ -718,6 +721,11 @@ int dmv_spec_go(DmvArgs A, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1)
 // the exact sum, and the wider workgroup costs more than it saves (OpenELM's
 // 8-row groups: 1,059 -> 1,046 tok/s), so those keep k_dmv.
 constexpr bool kSpecQkv = true;
+// The same for 32-row groups of 2048-value rows (Zephyr's q|k|v) over 512
+// weight threads: Zephyr-Q4 1,072 -> 1,086 tok/s, Zephyr-Q8 970 -> 1,009 in
+// an on-box A/B.  MiniCPM's (rows of 2304 values, five blocks per weight
+// thread) measured no gain (563 -> 562) and keeps k_dmv.
+constexpr bool kSpecQkvWide = true;
 
 // Launch with the items per thread the group needs (1, 2, 4, 8 or 12).
 template <int WT, int PRO, int EPI, int NCH>
@@ -827,7 +835,14 @@ int dmv_dispatch(const DmvArgs& A, int pro, int epi, hipStream_t st, hipEvent_t 
         DmvArgs As = A;
         As.rows = R.rows;
         return with_pro<1>(
-            pro, [&](auto p) { return dmv_spec_go<WT, 4, decltype(p)::value, 1, 64>(As, st, ev0, ev1); });
+            pro, [&](auto p) { return dmv_spec_go<WT, 4, decltype(p)::value, 1, 64, kDmvThreads>(As, st, ev0, ev1); });
+    }
+    if (kSpecQkvWide && R.spread && R.rows == 32 && A.nb == 64) {
+        DmvArgs As = A;
+        As.rows = R.rows;
+        return with_pro<1>(pro, [&](auto p) {
+            return dmv_spec_go<WT, 4, decltype(p)::value, 1, 64, kDmvWideThreads>(As, st, ev0, ev1);
+        });
     }
     if (R.spread && R.rows * A.nb > kDmvThreads * 4 && R.rows * A.nb <= kDmvWideThreads * 6) {
         if (K > (size_t)kDmvWideThreads * 8) {
