@@ -111,6 +111,11 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
     } else {
         // h: the stored row (PRO_RMS, PRO_LN) or the residual sum (RES)
         float h[NCH][8], gain[NCH][8], bias[NCH][8];
+        // rows of 2048 values: the block sum's first phase from the terms in
+        // registers (thread j's chunk is the sum's chunk j)
+        constexpr bool REG8 = NCH == 1;
+        const bool reg8 = REG8 && K == 2048;
+        float tsq[8];
         float av[NCH][8], ov[NCH][8];
         // A row at a fixed address (x_pitch = 0, res_cur) is requested
         // before the position: the position is then loaded after the row
@@ -183,9 +188,12 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
                 for (int i = 0; i < 8; i++) t[i] = LN ? h[j][i] : h[j][i] * h[j][i];
                 reinterpret_cast<float4*>(sq)[2 * ch] = make_float4(t[0], t[1], t[2], t[3]);
                 reinterpret_cast<float4*>(sq)[2 * ch + 1] = make_float4(t[4], t[5], t[6], t[7]);
+                if (REG8 && j == 0)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) tsq[i] = t[i];
             }
         }
-        lds_barrier();
+        if (LN || !reg8) lds_barrier();
         float mean = 0.0f;
         if (LN) {
             // layer_norm (gten/ops.cpp:669-698): the mean as the exact sum of
@@ -202,11 +210,15 @@ __device__ __forceinline__ int dmv_prologue(const DmvArgs& A, uint32_t* xs, floa
                     for (int i = 0; i < 8; i++) t[i] = (h[j][i] - mean) * (h[j][i] - mean);
                     reinterpret_cast<float4*>(sq)[2 * ch] = make_float4(t[0], t[1], t[2], t[3]);
                     reinterpret_cast<float4*>(sq)[2 * ch + 1] = make_float4(t[4], t[5], t[6], t[7]);
+                    if (j == 0)
+#pragma unroll
+                        for (int i = 0; i < 8; i++) tsq[i] = t[i];
                 }
             }
-            lds_barrier();
         }
-        const float ss = block_seq_sum_nonneg(sq, K, ssh);
+        // (reg8: the call's own barrier publishes the terms)
+        if (!reg8 && LN) lds_barrier();
+        const float ss = reg8 ? block_seq_sum_regs8(tsq, sq, ssh) : block_seq_sum_nonneg(sq, K, ssh);
         const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
         // the normalized row as stored (codes, then deltas) over sq's bytes
 #pragma unroll
@@ -352,6 +364,11 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
     const int nb = A.nb, K = nb * 32;
     const int nch = K / 8;
     float h[NCH][8], gain[NCH][8], bias[NCH][8], av[NCH][8], ov[NCH][8];
+    // rows of 2048 values: the block sum's first phase from the terms in
+    // registers (thread j's chunk is the sum's chunk j)
+    const bool reg8 = NCH == 1 && K == 2048;
+    float v16[kSsMaxPer];
+    float I = 0.0f;
     const bool fixed = !RES ? A.x_pitch == 0 : A.res_cur != nullptr;
     int pos = A.pos;
     if (tid == 0) {
@@ -439,8 +456,12 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
                 b4[0] = make_float4(bias[j][0], bias[j][1], bias[j][2], bias[j][3]);
                 b4[1] = make_float4(bias[j][4], bias[j][5], bias[j][6], bias[j][7]);
             }
+            if (!LN && NCH == 1)
+#pragma unroll
+                for (int i = 0; i < kSsMaxPer; i++) v16[i] = i < 8 ? sqv[i] : 0.0f;
         }
     }
+    if (!LN && reg8) I = ss_prefix<8>(v16, 8, ssh);
     part = wave_scan_add(part);
     if (lane == kWave - 1) sy.wsum[tid / kWave] = part;
     if (LN) {
@@ -462,9 +483,14 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
         float4* sq4 = reinterpret_cast<float4*>(L.sq) + 2 * tid;
         sq4[0] = make_float4(t[0], t[1], t[2], t[3]);
         sq4[1] = make_float4(t[4], t[5], t[6], t[7]);
+#pragma unroll
+        for (int i = 0; i < kSsMaxPer; i++) v16[i] = i < 8 ? t[i] : 0.0f;
+        I = ss_prefix<8>(v16, 8, ssh);
         bar();
     }
-    const float ss = block_seq_sum_nonneg_bar(L.sq, K, ssh, bar);
+    // (reg8: the first phase ran before the barrier that published the terms)
+    const float ss = reg8 ? block_seq_sum_after<8, false>(v16, I, L.sq, K, ssh, nullptr, bar)
+                          : block_seq_sum_nonneg_bar(L.sq, K, ssh, bar);
     const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {

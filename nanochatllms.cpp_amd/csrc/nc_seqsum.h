@@ -187,31 +187,14 @@ struct SsWaveBarrier {
     }
 };
 
-// Threads 0..255 only.
-template <int C, class Bar>
-__device__ __forceinline__ float block_seq_sum_core(const float* t, int n, SsShared& sh, bool* fast, Bar& bar)
+// Phase one of the sum, threads 0..255 with their chunk of c terms in v:
+// the chunks' approximate inclusive prefix within the wavefront (returned)
+// and the wavefront totals in sh.wf.  A barrier must follow before
+// block_seq_sum_after.
+template <int C>
+__device__ __forceinline__ float ss_prefix(const float (&v)[kSsMaxPer], int c, SsShared& sh)
 {
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-    const int c = C ? C : n / kSsThreads;
-    const int i0 = tid * c;
-    const int nh = kSsHead * c;  // head terms
-    float v[kSsMaxPer];
-    if (c % 4 == 0) {
-#pragma unroll
-        for (int k = 0; k < kSsMaxPer; k += 4) {
-            if (k < c) {
-                const float4 q = *reinterpret_cast<const float4*>(t + i0 + k);
-                v[k] = q.x;
-                v[k + 1] = q.y;
-                v[k + 2] = q.z;
-                v[k + 3] = q.w;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < kSsMaxPer; k++)
-            if (k < c) v[k] = t[i0 + k];
-    }
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     // chunk sum in order (a prediction only)
     float cs = 0.0f;
 #pragma unroll
@@ -223,9 +206,22 @@ __device__ __forceinline__ float block_seq_sum_core(const float* t, int n, SsSha
     // a wave the exclusive value is the previous lane's I, and across waves
     // I = local + WP with WP_w = ((0 + wf_0) + wf_1) + ... + wf_{w-1}, so the
     // last lane's wf_{w-1} + WP_{w-1} equals the next wave's WP_w.
-    float I = wave_scan_add(cs);
+    const float I = wave_scan_add(cs);
     if (lane == kWave - 1) sh.wf[w] = I;
-    bar();
+    return I;
+}
+
+// The rest of the sum after ss_prefix and a barrier (threads 0..255): the
+// terms t[0..n) also in LDS (the head and the fallback read them there).
+// FINAL: end with a barrier after which sh may be reused (without it, sh
+// must not be written again by this workgroup).
+template <int C, bool FINAL, class Bar>
+__device__ __forceinline__ float block_seq_sum_after(const float (&v)[kSsMaxPer], float I, const float* t, int n,
+                                                     SsShared& sh, bool* fast, Bar& bar)
+{
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+    const int c = C ? C : n / kSsThreads;
+    const int nh = kSsHead * c;  // head terms
     float WP = 0.0f;
     {
         const float4 F = *reinterpret_cast<const float4*>(sh.wf);  // every wave's total at once
@@ -403,8 +399,37 @@ __device__ __forceinline__ float block_seq_sum_core(const float* t, int n, SsSha
     }
     if (fast && tid == 0) *fast = sh.ok != 0;
     const float res = sh.result;
-    bar();  // sh reusable after return
+    if (FINAL) bar();  // sh reusable after return
     return res;
+}
+
+// Threads 0..255 only.
+template <int C, class Bar>
+__device__ __forceinline__ float block_seq_sum_core(const float* t, int n, SsShared& sh, bool* fast, Bar& bar)
+{
+    const int tid = threadIdx.x;
+    const int c = C ? C : n / kSsThreads;
+    const int i0 = tid * c;
+    float v[kSsMaxPer];
+    if (c % 4 == 0) {
+#pragma unroll
+        for (int k = 0; k < kSsMaxPer; k += 4) {
+            if (k < c) {
+                const float4 q = *reinterpret_cast<const float4*>(t + i0 + k);
+                v[k] = q.x;
+                v[k + 1] = q.y;
+                v[k + 2] = q.z;
+                v[k + 3] = q.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kSsMaxPer; k++)
+            if (k < c) v[k] = t[i0 + k];
+    }
+    const float I = ss_prefix<C>(v, c, sh);
+    bar();
+    return block_seq_sum_after<C, true>(v, I, t, n, sh, fast, bar);
 }
 
 
@@ -427,6 +452,34 @@ __device__ __forceinline__ float block_seq_sum_impl(const float* t, int n, SsSha
     }
     SsLdsBarrier bar;
     return block_seq_sum_core<C>(t, n, sh, fast, bar);
+}
+
+// The sum of 2048 terms where thread j < 256 holds terms [8 j, 8 j + 8) in
+// registers (t8) as well as in LDS (t), called by every thread of a
+// workgroup of 256 or more threads after the terms are stored: the sum's
+// first phase runs from the registers before the barrier that publishes
+// them (this call's first), and no barrier follows the result (sh must not
+// be written again; t may be, by any thread, once the call returns).
+__device__ __forceinline__ float block_seq_sum_regs8(const float (&t8)[8], const float* t, SsShared& sh)
+{
+    float v[kSsMaxPer];
+    float I = 0.0f;
+    if (threadIdx.x < kSsThreads) {
+#pragma unroll
+        for (int k = 0; k < kSsMaxPer; k++) v[k] = k < 8 ? t8[k] : 0.0f;
+        I = ss_prefix<8>(v, 8, sh);
+    }
+    lds_barrier();
+    if (threadIdx.x >= kSsThreads) {
+        // the phase barriers of the computing threads, and the fallback's
+        lds_barrier();
+        lds_barrier();
+        lds_barrier();
+        if (!sh.ok) lds_barrier();
+        return sh.result;
+    }
+    SsLdsBarrier bar;
+    return block_seq_sum_after<8, false>(v, I, t, 8 * kSsThreads, sh, nullptr, bar);
 }
 
 // Dispatch on the terms per thread (compile-time chunk lengths for the
