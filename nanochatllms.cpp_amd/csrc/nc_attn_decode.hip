@@ -4,7 +4,8 @@
 // One workgroup per query head h (group g = h / (hq / hkv)) does what
 // k_qkv_post + k_attn do for the decode row, with the same arithmetic:
 //   q_h, k_g, v_g from the fused qkv matvec output: requantized as Linear
-//     outputs; OpenELM's per-head QK RMSNorm (requantized); RoPE of q and k
+//     outputs; Zephyr's biases added (requantized); OpenELM's per-head QK
+//     RMSNorm (requantized); RoPE of q and k
 //     (requantized when stored) -- gten/modules.cpp:242-267, openelm.cpp:33-60;
 //   the group's first head appends k_g and v_g to the caches at the position
 //     (the others take that position from shared memory, so no workgroup
@@ -184,8 +185,11 @@ __device__ __forceinline__ void store_vchunk(const VChunk& v, uint8_t* buf, int 
 //   codes   [l][k4][column 64] dwords, byte j = the code at position c;
 //   deltas  [block 2][l][VP / 8] fp32, entry c / 8;
 //   P       [l][sT] fp32 (the probabilities, entry c / 8).
-template <bool QKNORM, int MK, int VP>
+template <bool QKNORM, bool BIAS, int MK, int VP>
 __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict__ raw, int hq, int hkv,
+                                                         const uint16_t* __restrict__ bq,
+                                                         const uint16_t* __restrict__ bk,
+                                                         const uint16_t* __restrict__ bv,
                                                          const uint16_t* __restrict__ qn_w,
                                                          const uint16_t* __restrict__ kn_w,
                                                          const float2* __restrict__ table, int d_half, int pos_host,
@@ -210,6 +214,9 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     // requested before the position is known
     const int col = w == 0 ? h * 64 : (w == 1 ? hq * 64 + g * 64 : hq * 64 + hkv * 64 + g * 64);
     const float raw_x = w < 3 ? raw[col + lane] : 0.0f;
+    // the Linear's bias of this value (Zephyr's q/k/v projections)
+    uint16_t bias16 = 0;
+    if (BIAS && w < 3) bias16 = (w == 0 ? bq + h * 64 : (w == 1 ? bk : bv) + g * 64)[lane];
     // the lane's RoPE pair (q and k waves) is requested before the K / V
     // rows: the vector memory counter completes in order, so a pair
     // requested after them would be waited for together with all of them
@@ -252,6 +259,8 @@ __global__ __launch_bounds__(kAdThreads) void k_attn_dec(const float* __restrict
     // ---- q_h (wave 0), k_g (wave 1), v_g (wave 2) of the new position
     if (w < 3) {
         float x = q8_roundtrip_lane(raw_x, true);  // the Linear output as stored
+        // + bias, stored (bias_add_inplace, gten/ops.cpp:639-666)
+        if (BIAS) x = q8_roundtrip_lane(x + h2f(bias16), true);
         if (w < 2) {
             if (QKNORM) {
                 // RMSNorm3D over the head (rms_norm_vec_f32, gten/ops.cpp:830-903)
@@ -915,10 +924,13 @@ bool attn_decode_supported(int hq, int hkv, int max_ctx)
     return hkv > 0 && hq % hkv == 0 && max_ctx > 0 && max_ctx <= kAttnMaxCtx;
 }
 
-int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
-                       const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur)
+int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                       const uint16_t* qn_w, const uint16_t* kn_w, const float* table, int d_half, int pos,
+                       const int* dpos, uint8_t* kc, uint8_t* vc, int kv_pitch, uint8_t* out, int max_ctx,
+                       hipStream_t st, const float* rope_cur)
 {
+    if ((bq || bk || bv) && !(bq && bk && bv)) return fail(NC_ERR_ARG, "attention: q, k and v biases go together");
+    if (bq && qn_w) return fail(NC_ERR_ARG, "attention: biases with the q/k norms");
     if (hkv <= 0 || hq % hkv) return fail(NC_ERR_ARG, "attention: %d query heads over %d kv heads", hq, hkv);
     if (max_ctx <= 0 || max_ctx > kAttnMaxCtx)
         return fail(NC_ERR_ARG, "attention: context %d (at most %d positions)", max_ctx, kAttnMaxCtx);
@@ -926,22 +938,24 @@ int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, 
     const size_t lds = attn_decode_lds(max_ctx);
     const float scale = 1.0f / sqrtf(64.0f);
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, qn_w, kn_w, (const float2*)table,
-                           d_half, pos, dpos, kc, vc, kv_pitch, out, scale, (const float2*)rope_cur, max_ctx);
+        hipLaunchKernelGGL(kern, dim3(hq), dim3(kAdThreads), lds, st, raw, hq, hkv, bq, bk, bv, qn_w, kn_w,
+                           (const float2*)table, d_half, pos, dpos, kc, vc, kv_pitch, out, scale,
+                           (const float2*)rope_cur, max_ctx);
     };
     // K rows requested at the start: one per thread for caches of up to
     // kAdThreads positions, two beyond; the V slice resident up to kAdResMax
-    auto by_ctx = [&](auto qk) {
-        constexpr bool QK = decltype(qk)::value;
+    auto by_ctx = [&](auto qk, auto bias) {
+        constexpr bool QK = decltype(qk)::value, B = decltype(bias)::value;
         switch (attn_decode_vp(max_ctx)) {
-        case 256: go(k_attn_dec<QK, 1, 256>); break;
-        case 512: go(k_attn_dec<QK, 1, 512>); break;
-        case kAdResMax: go(k_attn_dec<QK, kAdMaxK, kAdResMax>); break;
-        default: go(k_attn_dec<QK, kAdMaxK, 0>); break;
+        case 256: go(k_attn_dec<QK, B, 1, 256>); break;
+        case 512: go(k_attn_dec<QK, B, 1, 512>); break;
+        case kAdResMax: go(k_attn_dec<QK, B, kAdMaxK, kAdResMax>); break;
+        default: go(k_attn_dec<QK, B, kAdMaxK, 0>); break;
         }
     };
-    if (qn_w) by_ctx(std::true_type{});
-    else by_ctx(std::false_type{});
+    if (qn_w) by_ctx(std::true_type{}, std::false_type{});
+    else if (bq) by_ctx(std::false_type{}, std::true_type{});
+    else by_ctx(std::false_type{}, std::false_type{});
     return launch_status("k_attn_dec");
 }
 

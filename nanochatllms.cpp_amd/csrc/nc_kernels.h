@@ -108,16 +108,18 @@ int attn_launch(int adt, const uint8_t* q, int q_pitch, const uint8_t* kc, int k
 // max_ctx (zephyr/zephyr.h:12); TinyLlama and MiniCPM stop at 2048.
 constexpr int kAttnMaxCtx = NC_MAX_CTX;
 
-// Decode attention with the q/k/v post-processing fused in (Q8 activations,
-// no qkv bias): raw = the qkv matvec's fp32 row [q | k | v]; the new k / v
+// Decode attention with the q/k/v post-processing fused in (Q8 activations;
+// optional q / k / v biases, bias_add_inplace after the Linear outputs, or
+// OpenELM's q / k norms): raw = the qkv matvec's fp32 row [q | k | v]; the new k / v
 // rows are appended to the caches at the position (*dpos when set, else
 // pos); out = the attention output Act row.  rope_cur, when set, is the
 // position's RoPE (cos, sin) row at a fixed address (read instead of the
 // table row, so that load does not wait for the position).
 bool attn_decode_supported(int hq, int hkv, int max_ctx);
-int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* qn_w, const uint16_t* kn_w,
-                       const float* table, int d_half, int pos, const int* dpos, uint8_t* kc, uint8_t* vc,
-                       int kv_pitch, uint8_t* out, int max_ctx, hipStream_t st, const float* rope_cur = nullptr);
+int attn_decode_launch(const float* raw, int hq, int hkv, const uint16_t* bq, const uint16_t* bk, const uint16_t* bv,
+                       const uint16_t* qn_w, const uint16_t* kn_w, const float* table, int d_half, int pos,
+                       const int* dpos, uint8_t* kc, uint8_t* vc, int kv_pitch, uint8_t* out, int max_ctx,
+                       hipStream_t st, const float* rope_cur = nullptr);
 // The same for fp16 rows, with optional q / k / v biases (bias_add_inplace
 // after the Linear outputs) and the RoPE pair read from the table at the
 // (device-held) position.

@@ -946,8 +946,7 @@ public:
         const int pr = pro_res_add();
         for (int l = 0; l < cfg.n_layers; l++) {
             Layer& y = L[l];
-            const int pq = pitch(y.qd), pkv = pitch(y.kvd);
-            const int nqkv = y.qd + 2 * y.kvd;
+            const int pkv = pitch(y.kvd);
             DmvArgs a = base;
             a.norm_w = y.attn_norm;
             a.norm_b = y.attn_norm_b;
@@ -964,18 +963,9 @@ public:
                 a.res_cur_out = cur2;
                 if ((s = dmv(a, &y.qkv, pr, EPI_RAW, NC_PROF_QKV))) return s;
             }
-            if (!y.bq) {
-                if ((s = attn_decode_launch(qkv_raw, y.hq, y.hkv, y.qn, y.kn, rope, d_half, pos, dpos, y.kc, y.vc, pkv,
-                                            attn, cfg.max_ctx, st, dpos ? cur_rope : nullptr)))
-                    return s;
-            } else {
-                if ((s = qkv_post_launch(adt, qkv_raw, nqkv, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half,
-                                         pos, 1, q_act, pq, y.kc, pkv, y.vc, pkv, st, dpos)))
-                    return s;
-                if ((s = attn_launch(adt, q_act, pq, y.kc, pkv, y.vc, pkv, attn, pq, y.hq, y.hkv, pos, pos + 1, st,
-                                     dpos, cfg.max_ctx)))
-                    return s;
-            }
+            if ((s = attn_decode_launch(qkv_raw, y.hq, y.hkv, y.bq, y.bk, y.bv, y.qn, y.kn, rope, d_half, pos, dpos,
+                                        y.kc, y.vc, pkv, attn, cfg.max_ctx, st, dpos ? cur_rope : nullptr)))
+                return s;
             a = base;
             a.x = attn;
             a.raw = o_raw;
