@@ -62,12 +62,14 @@ nc = _load_package()
 METRIC = "decode tok/s (1 GPU) + Q4/Q8 matvec HBM GB/s as % of MI355X peak"
 HBM_PEAK_GBS = 8000.0
 # kernel names (as the profiler lists them) of the fused decode matvecs
-FUSED_KERNEL = {"qkv": "k_dmv (qkv, residual add + rms_norm prologue)",
+FUSED_KERNEL = {"qkv": "k_dmv_spec (q|k|v, residual add + norm prologue, weight terms beside the exact sums; "
+                       "k_dmv where the speculative launch is not used)",
                 "o": "k_dmv (o)",
-                "gate_up": "k_dmv_glu (gate|up, residual add + rms_norm prologue, SwiGLU epilogue)",
+                "gate_up": "k_dmv_glu_spec (gate|up, residual add + norm prologue beside the weight terms, "
+                           "SwiGLU epilogue)",
                 "down": "k_dmv (down)",
                 "lm_head": "k_dmv_head (lm head in the head layout, residual add + final norm prologue, "
-                           "greedy-token epilogue; k_dmv for widths other than 2048 / 2304)"}
+                           "greedy-token epilogue; k_dmv for widths other than 1280 / 1536 / 2048 / 2304)"}
 
 FUSED_F16_KERNEL = {"qkv": "k_dmv_f16_nrm (q|k|v, residual add + norm prologue)",
                     "gate_up": "k_dmv_f16_nrm<GLU> (gate|up, residual add + norm prologue, SwiGLU epilogue)"}
