@@ -156,13 +156,14 @@ int nc_block_seq_sum_grid(const float* x, int n, int count, float* out, int* pas
 /* Host run of the same decomposition (no GPU); plant = 1 drops the rounding
  * error after each rounding step (a planted mistake for tests). */
 float nc_seq_sum_grid_host(const float* x, int n, int plant, int* passes);
-/* Test hook (no counterpart in the reference): the fused decode matvecs with
- * an rms_norm prologue compute their weight terms from a row normalized with
- * a predicted sum of squares, beside the exact sum, and recompute every
- * block whose exact row differs.  Launches made after this call scale the
- * prediction by skew (1: none), so that tests can force the recomputation;
- * when fixups (device int) is not null, each workgroup that recomputed adds
- * one to it.  Results are the same for every skew > 0. */
+/* Test hook (no counterpart in the reference): the speculative fused decode
+ * matvecs (q|k|v and gate|up with a norm prologue) compute their weight
+ * terms from a row normalized with a predicted statistic (rms_norm: the sum
+ * of squares; layer_norm: the variance), beside the exact sums, and
+ * recompute every block whose exact row differs.  Launches made after this
+ * call scale the prediction by skew (1: none), so that tests can force the
+ * recomputation; when fixups (device int) is not null, each workgroup that
+ * recomputed adds one to it.  Results are the same for every skew > 0. */
 int nc_debug_spec(float skew, void* fixups);
 /* Greedy pick of greedy_sample (src/gten/sampler.cpp:33-41): first index of
  * the maximum. */
