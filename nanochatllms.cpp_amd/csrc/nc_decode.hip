@@ -386,7 +386,7 @@ __global__ __launch_bounds__(kSpecExact + NS) void k_dmv_spec(DmvArgs A)
             lds_barrier();  // its folds done
         }
     } else {
-        spec_weights<PRO, NCH, NS>(P, L, sy, load_w, terms, spec_tail);
+        spec_weights<PRO, NCH, NS, WT == Q4>(P, L, sy, load_w, terms, spec_tail);
         lds_barrier();  // B2
         if (!sy.anybad) {
             if (s < 4 * R) store(s, sres);

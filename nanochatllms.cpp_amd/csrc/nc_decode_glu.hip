@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
             exact_tail();
         }
     } else {
-        spec_weights<PRO, NCH, NS>(P, L, sy, load_w, terms, spec_tail);
+        spec_weights<PRO, NCH, NS, WT == Q4>(P, L, sy, load_w, terms, spec_tail);
         lds_barrier();  // B2
         if (!sy.anybad) {
             if (s < 32) store(s, sq8, sd16);

@@ -551,8 +551,11 @@ __device__ __forceinline__ void spec_exact_fixup(const DmvArgs& A, const SpecLds
 // threads, a quad per block), a barrier among
 // the weight wavefronts, every block's terms from that row (terms(1)), then
 // spec_tail(bar): the fold and epilogue from those terms, held back.  NS:
-// the weight role's threads.
-template <int PRO, int NCH, int NS, class LoadW, class Terms, class SpecTail>
+// the weight role's threads.  ROW_FIRST: the wavefronts that compute the
+// speculative row request their weights after it (a wavefront waits at a
+// large transfer's issue; with Q4 weights TinyLlama-Q4 1,513 -> 1,522 tok/s,
+// with Q8 1,374 -> 1,370, so the Q8 launches request them first).
+template <int PRO, int NCH, int NS, bool ROW_FIRST, class LoadW, class Terms, class SpecTail>
 __device__ __forceinline__ void spec_weights(const DmvArgs& A, const SpecLds& L, SpecSync& sy, LoadW&& load_w,
                                              Terms&& terms, SpecTail&& spec_tail)
 {
@@ -561,8 +564,8 @@ __device__ __forceinline__ void spec_weights(const DmvArgs& A, const SpecLds& L,
     const int nb = A.nb, K = nb * 32;
     const int nch = K / 8;
     lds_barrier();  // B1
-    load_w();
     const int sc = threadIdx.x - NT;
+    if (!ROW_FIRST || sc >= NT) load_w();
     if (sc < NT) {
         const float s2 = ((sy.wsum[0] + sy.wsum[1]) + sy.wsum[2]) + sy.wsum[3];
         float mn = 0.0f, dn;
@@ -586,6 +589,7 @@ __device__ __forceinline__ void spec_weights(const DmvArgs& A, const SpecLds& L,
             const Q8Chunk q = spec_norm_chunk<LN>(hv, gv, bv, mn, dn, A.post_scale);
             if (ch < nch) store_act_chunk(L.row, K, ch, q);
         }
+        if (ROW_FIRST) load_w();
     }
     SsWaveBarrier<NS / kWave> sbar{&sy.spec, 0};
     sbar();
