@@ -373,7 +373,7 @@ __global__ __launch_bounds__(kSpecExact + NS) void k_dmv_spec(DmvArgs A)
     P.nb = NB;
     if (__builtin_amdgcn_readfirstlane(tid) < kSpecExact) {
         Q8Chunk qx[NCH];
-        spec_exact<PRO, NCH, NS>(P, L, ssh, sgh, sy, qx);
+        spec_exact<PRO, NCH, NS, spec_issue<WT, PRO>()>(P, L, ssh, sgh, sy, qx);
         lds_barrier();  // B2
         if (sy.anybad) {
             spec_exact_fixup<NCH>(P, L, qx);
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(kSpecExact + NS) void k_dmv_spec(DmvArgs A)
             lds_barrier();  // its folds done
         }
     } else {
-        spec_weights<PRO, NCH, NS, WT == Q4>(P, L, sy, load_w, terms, spec_tail);
+        spec_weights<PRO, NCH, NS, spec_issue<WT, PRO>()>(P, L, sy, load_w, terms, spec_tail);
         lds_barrier();  // B2
         if (!sy.anybad) {
             if (s < 4 * R) store(s, sres);

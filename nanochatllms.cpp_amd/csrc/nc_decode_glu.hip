@@ -208,7 +208,7 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
     // the weight role, then the exact role's tail.
     if (__builtin_amdgcn_readfirstlane(tid) < kSpecExact) {
         Q8Chunk qx[NCH];
-        spec_exact<PRO, NCH, NS>(P, L, ssh, sgh, sy, qx);
+        spec_exact<PRO, NCH, NS, spec_issue<WT, PRO>()>(P, L, ssh, sgh, sy, qx);
         lds_barrier();  // B2
         if (sy.anybad) {
             spec_exact_fixup<NCH>(P, L, qx);
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
             exact_tail();
         }
     } else {
-        spec_weights<PRO, NCH, NS, WT == Q4>(P, L, sy, load_w, terms, spec_tail);
+        spec_weights<PRO, NCH, NS, spec_issue<WT, PRO>()>(P, L, sy, load_w, terms, spec_tail);
         lds_barrier();  // B2
         if (!sy.anybad) {
             if (s < 32) store(s, sq8, sd16);

@@ -353,7 +353,22 @@ struct SpecSync {
 
 // Exact role, up to B2 (B2 not passed).  Returns the exact row's chunks in
 // qx (stored over the speculative row by the caller when a block differs).
-template <int PRO, int NCH, int NS>
+// When the weight role requests its weights (ISSUE): kIssueAfterRows after
+// the exact role's rows have arrived; kIssueAfterSpecRow the same, the
+// wavefronts that compute the speculative row after it; kIssueEarly as soon
+// as the exact role has requested its rows (barrier B0).  Measured on-box:
+// early issue TinyLlama-Q4 1,529 -> 1,558 tok/s but Zephyr-Q4 (layer_norm,
+// whose longer exact path the weights then delay) 1,177 -> 1,166 and
+// TinyLlama-Q8 1,384 -> 1,377; after the speculative row TinyLlama-Q4
+// 1,513 -> 1,522, TinyLlama-Q8 1,374 -> 1,370.
+enum { kIssueAfterRows = 0, kIssueAfterSpecRow = 1, kIssueEarly = 2 };
+template <int WT, int PRO>
+constexpr int spec_issue()
+{
+    return WT != Q4 ? kIssueAfterRows : (pro_ln(PRO) ? kIssueAfterSpecRow : kIssueEarly);
+}
+
+template <int PRO, int NCH, int NS, int ISSUE>
 __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, SsShared& ssh, SgShared& sgh,
                                            SpecSync& sy, Q8Chunk (&qx)[NCH])
 {
@@ -404,6 +419,11 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
     }
     __builtin_amdgcn_sched_barrier(0);
     if (fixed && A.dpos) pos = load_pos(A.dpos);
+    if (ISSUE == kIssueEarly) {
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();  // B0: the rows requested, the weights may follow
+        __builtin_amdgcn_sched_barrier(0);
+    }
     float part = 0.0f, part1 = 0.0f;  // this thread's squares and values, for the prediction
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
@@ -551,11 +571,9 @@ __device__ __forceinline__ void spec_exact_fixup(const DmvArgs& A, const SpecLds
 // threads, a quad per block), a barrier among
 // the weight wavefronts, every block's terms from that row (terms(1)), then
 // spec_tail(bar): the fold and epilogue from those terms, held back.  NS:
-// the weight role's threads.  ROW_FIRST: the wavefronts that compute the
-// speculative row request their weights after it (a wavefront waits at a
-// large transfer's issue; with Q4 weights TinyLlama-Q4 1,513 -> 1,522 tok/s,
-// with Q8 1,374 -> 1,370, so the Q8 launches request them first).
-template <int PRO, int NCH, int NS, bool ROW_FIRST, class LoadW, class Terms, class SpecTail>
+// the weight role's threads; ISSUE: when the weights are requested (a
+// wavefront waits at a large transfer's issue).
+template <int PRO, int NCH, int NS, int ISSUE, class LoadW, class Terms, class SpecTail>
 __device__ __forceinline__ void spec_weights(const DmvArgs& A, const SpecLds& L, SpecSync& sy, LoadW&& load_w,
                                              Terms&& terms, SpecTail&& spec_tail)
 {
@@ -563,9 +581,14 @@ __device__ __forceinline__ void spec_weights(const DmvArgs& A, const SpecLds& L,
     constexpr bool LN = pro_ln(PRO);
     const int nb = A.nb, K = nb * 32;
     const int nch = K / 8;
+    constexpr bool ROW_FIRST = ISSUE == kIssueAfterSpecRow;
+    if (ISSUE == kIssueEarly) {
+        lds_barrier();  // B0
+        load_w();
+    }
     lds_barrier();  // B1
     const int sc = threadIdx.x - NT;
-    if (!ROW_FIRST || sc >= NT) load_w();
+    if (ISSUE == kIssueAfterRows || (ROW_FIRST && sc >= NT)) load_w();
     if (sc < NT) {
         const float s2 = ((sy.wsum[0] + sy.wsum[1]) + sy.wsum[2]) + sy.wsum[3];
         float mn = 0.0f, dn;
