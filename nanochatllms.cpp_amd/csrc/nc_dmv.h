@@ -45,6 +45,40 @@ __device__ __forceinline__ Q8Chunk quad_quantize(const float (&v)[8])
     return r;
 }
 
+// quad_quantize, which also returns the fp32 delta (dl) and whether a code
+// of these 8 values could change when the block is recomputed from a
+// denominator other than this one (unc).  Why that can be decided here:
+// the block y = RN(RN(h / D) g) under another D' = D / rho is y' = y rho
+// (1 + t) with |t| <= 4.0001u (u = 2^-24, one factor 1 +- u per rounding),
+// and amax' lies within the same factors of amax rho, so the scaled value
+// z = RN(y RN(1 / RN(amax / 127))) becomes z' = z (1 + t'), |t'| <= 14.0001u:
+// rho cancels.  A code roundf(z) can then change only when a half-integer
+// lies within 14.0001u |z| of z; unc flags every value with |z| within
+// 16u |z| = 2^-20 |z| of one (both sides exact in fp32 for |z| < 2^23).
+// The delta's fp16 rounding does depend on rho: the exact side checks it.
+__device__ __forceinline__ Q8Chunk quad_quantize_cert(const float (&v)[8], float& dl, bool& unc)
+{
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+    a = quad_max(a);
+    const float delta = a / 127.0f;
+    Q8Chunk r;
+    r.d16 = f2h(delta);
+    const float scale = delta != 0.0f ? 1.0f / delta : 0.0f;
+    bool u = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float z = v[i] * scale;
+        r.q[i] = (int8_t)roundf(z);
+        const float az = fabsf(z);
+        u = u || fabsf((az - floorf(az)) - 0.5f) <= az * 0x1p-20f;
+    }
+    dl = delta;
+    unc = u;
+    return r;
+}
+
 __device__ __forceinline__ void quad_roundtrip(float (&v)[8])
 {
     const Q8Chunk c = quad_quantize(v);
@@ -257,8 +291,10 @@ constexpr int kGluMaxItems = 18;  // 64 rows x NB blocks / threads, NB <= 72
 // quantize it and compute every weight block's four terms against that row
 // as the weights arrive.  Once the exact sum is known, threads 0-255
 // quantize the exact row and compare it with the speculative one block by
-// block.  A block's terms are a function of its 32 codes and its fp16 delta
-// alone, so where those match the speculative terms are the exact ones; the
+// block (rms_norm: only the blocks the speculative side could not certify
+// as unchanged, spec_rms_uncertain).  A block's terms are a function of its
+// 32 codes and its fp16 delta alone, so where those match the speculative
+// terms are the exact ones; the
 // weight threads recompute the terms of every block that differs.  The fold
 // then sees the terms of the exact row, and the result is the reference's
 // bit for bit whatever the approximation was.  (With unit norm gains the
@@ -274,12 +310,14 @@ struct SpecLds {
     float* b;      // K norm biases (layer_norm)
     uint8_t* row;  // the speculative Act row, then the exact one: K codes, nb fp16 deltas
     uint8_t* bad;  // nb flags: the block differs between the two rows
+    float* dl;     // rms_norm: nb fp32 deltas of the speculative row (its first quantization's)
+    uint8_t* uc;   // rms_norm: K / 8 flags: a code of the chunk may differ in the exact row
 };
 
 __host__ __device__ constexpr size_t spec_lds_bytes(int nb, bool ln)
 {
     return (size_t)nb * 32 * 4 * (ln ? 4 : 3) + (((size_t)nb * 34 + 15) & ~(size_t)15) +
-           (((size_t)nb + 15) & ~(size_t)15);
+           (((size_t)nb + 15) & ~(size_t)15) + (size_t)nb * 4 + (((size_t)nb * 4 + 15) & ~(size_t)15);
 }
 
 __device__ __forceinline__ SpecLds spec_lds(float* base, int nb, bool ln)
@@ -293,6 +331,8 @@ __device__ __forceinline__ SpecLds spec_lds(float* base, int nb, bool ln)
     L.b = ln ? base + 3 * K : nullptr;
     L.row = reinterpret_cast<uint8_t*>(base + na * K);
     L.bad = L.row + ((nb * 34 + 15) & ~15);
+    L.dl = reinterpret_cast<float*>(L.bad + ((nb + 15) & ~15));
+    L.uc = reinterpret_cast<uint8_t*>(L.dl + nb);
     return L;
 }
 
@@ -330,6 +370,48 @@ __device__ __forceinline__ Q8Chunk spec_norm_chunk(const float (&h)[8], const fl
     return quad_quantize(y);
 }
 
+// spec_norm_chunk for rms_norm, which also returns the fp32 delta of the
+// first quantization (the post scale's round trip, else the row's own) and
+// its code flag (quad_quantize_cert): with those two the exact side can tell
+// whether the chunk changes under its own denominator.  Once the first
+// quantization's codes and fp16 delta are the same, everything after it is.
+__device__ __forceinline__ Q8Chunk spec_rms_chunk_cert(const float (&h)[8], const float (&g)[8], float denom,
+                                                       float post, float& dl, bool& unc)
+{
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = h[i] / denom * g[i];
+    Q8Chunk q = quad_quantize_cert(y, dl, unc);
+    if (post != 1.0f) {
+        const float d = h2f(q.d16);
+#pragma unroll
+        for (int i = 0; i < 8; i++) y[i] = (float)q.q[i] * d;
+#pragma unroll
+        for (int i = 0; i < 8; i++) y[i] = y[i] * post;
+        q = quad_quantize(y);
+    }
+    return q;
+}
+
+// Whether the exact row's chunk may differ from the speculative one
+// (rms_norm; the caller ORs the flags of a block's lane quad).  dl, uc: the
+// speculative chunk's first delta and code flag; r = RN(Ds / De), the ratio
+// of the two denominators.  The exact delta dl' = RN(amax' / 127) lies in
+// dl rho [1 - 6.0001u, 1 + 6.0001u] and rho = Ds / De in r [1 - u, 1 + 1.0001u],
+// so dl' is inside [lo, hi] below (each product's rounding counted), and the
+// fp16 rounding, monotone, gives dl's fp16 value everywhere in it when it
+// gives it at both ends.  Deltas below 2^-66 (where values may be subnormal)
+// are not certified.
+__device__ __forceinline__ bool spec_rms_uncertain(float dl, bool uc, float r)
+{
+    if (uc || !(dl >= 0x1p-66f)) return true;
+    const float p = dl * r;
+    const float lo = p * 0x1.ffffecp-1f;  // 1 - 10u
+    const float hi = p * 0x1.00000ap0f;   // 1 + 10u
+    const uint16_t d16 = f2h(dl);
+    return f2h(lo) != d16 || f2h(hi) != d16;
+}
+
 // LDS state of the two sides.
 struct SpecSync {
     int exact;    // barrier counter of threads 0-255 (the exact sum)
@@ -337,6 +419,7 @@ struct SpecSync {
     int anybad;   // some block differs: the speculative results are void
     float wsum[kSpecExact / kWave];   // per exact wavefront: its part of the squares (the prediction)
     float wsum1[kSpecExact / kWave];  // ... and of the values (layer_norm's predicted mean)
+    float dn;                         // the speculative row's denominator
 };
 
 // The two roles of a speculative norm launch.  The workgroup's first
@@ -352,7 +435,8 @@ struct SpecSync {
 //   then the kernel's exact tail (its own barriers).
 
 // Exact role, up to B2 (B2 not passed).  Returns the exact row's chunks in
-// qx (stored over the speculative row by the caller when a block differs).
+// qx for the blocks it requantized (stored over the speculative row by the
+// caller where a block differs).
 // When the weight role requests its weights (ISSUE): kIssueAfterRows after
 // the exact role's rows have arrived; kIssueAfterSpecRow the same, the
 // wavefronts that compute the speculative row after it; kIssueEarly as soon
@@ -512,10 +596,12 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
     const float ss = reg8 ? block_seq_sum_after<8, false>(v16, I, L.sq, K, ssh, nullptr, bar)
                           : block_seq_sum_nonneg_bar(L.sq, K, ssh, bar);
     const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
+    if constexpr (LN) {
 #pragma unroll
-    for (int j = 0; j < NCH; j++) {
-        if (j * NT >= nch) break;  // uniform
-        qx[j] = spec_norm_chunk<LN>(h[j], gain[j], bias[j], mean, denom, A.post_scale);
+        for (int j = 0; j < NCH; j++) {
+            if (j * NT >= nch) break;  // uniform
+            qx[j] = spec_norm_chunk<LN>(h[j], gain[j], bias[j], mean, denom, A.post_scale);
+        }
     }
     // once the speculative row is complete (every weight wavefront has
     // passed its first barrier), compare it block by block with the exact
@@ -523,6 +609,13 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
     while (__hip_atomic_load(&sy.spec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NS / kWave) {
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // rms_norm: only the blocks the speculative side could not certify are
+    // requantized here (spec_rms_uncertain); the same denominator certifies
+    // every block.  layer_norm requantizes every block.
+    const float dns = LN ? 0.0f : sy.dn;
+    const bool same = !LN && dns == denom;
+    const float r = dns / denom;
+    const bool okr = r > 0.0f && r < __builtin_inff();
     int any = 0;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
@@ -530,15 +623,28 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
         if (j * NT >= nch) break;  // uniform
         const bool valid = ch < nch;
         const int cc = valid ? ch : 0;
-        const Q8Chunk& q = qx[j];
-        const uint2 sc = *reinterpret_cast<const uint2*>(L.row + (size_t)cc * 8);
-        const uint16_t sd = reinterpret_cast<const uint16_t*>(L.row + K)[cc >> 2];
-        uint32_t w[2] = {0, 0};
+        bool check = true;
+        if constexpr (!LN) {
+            bool unc = false;
+            if (!same) unc = !okr || spec_rms_uncertain(L.dl[cc >> 2], L.uc[cc] != 0, r);
+            int ui = unc ? 1 : 0;
+            ui |= dpp_i<kDppQuadXor1>(ui);
+            ui |= dpp_i<kDppQuadXor2>(ui);
+            check = ui != 0;  // uniform over the block's lane quad
+            if (check) qx[j] = spec_norm_chunk<false>(h[j], gain[j], bias[j], 0.0f, denom, A.post_scale);
+        }
+        int diff = 0;
+        if (check) {
+            const Q8Chunk& q = qx[j];
+            const uint2 sc = *reinterpret_cast<const uint2*>(L.row + (size_t)cc * 8);
+            const uint16_t sd = reinterpret_cast<const uint16_t*>(L.row + K)[cc >> 2];
+            uint32_t w[2] = {0, 0};
 #pragma unroll
-        for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q.q[i] << (8 * (i & 3));
-        int diff = valid && (sc.x != w[0] || sc.y != w[1] || sd != q.d16) ? 1 : 0;
-        diff |= dpp_i<kDppQuadXor1>(diff);
-        diff |= dpp_i<kDppQuadXor2>(diff);
+            for (int i = 0; i < 8; i++) w[i >> 2] |= (uint32_t)(uint8_t)q.q[i] << (8 * (i & 3));
+            diff = valid && (sc.x != w[0] || sc.y != w[1] || sd != q.d16) ? 1 : 0;
+            diff |= dpp_i<kDppQuadXor1>(diff);
+            diff |= dpp_i<kDppQuadXor2>(diff);
+        }
         any |= diff;
         if (valid && (ch & 3) == 0) L.bad[ch >> 2] = (uint8_t)diff;
     }
@@ -559,7 +665,8 @@ __device__ __forceinline__ void spec_exact_fixup(const DmvArgs& A, const SpecLds
     for (int j = 0; j < NCH; j++) {
         const int ch = threadIdx.x + j * NT;
         if (j * NT >= nch) break;  // uniform
-        if (ch < nch) store_act_chunk(L.row, K, ch, qx[j]);
+        // (only a differing block's chunks were requantized)
+        if (ch < nch && L.bad[ch >> 2]) store_act_chunk(L.row, K, ch, qx[j]);
     }
     lds_barrier();  // B3
     lds_barrier();  // B4
@@ -608,10 +715,23 @@ __device__ __forceinline__ void spec_weights(const DmvArgs& A, const SpecLds& L,
             float hv[8], gv[8], bv[8];
             load_f32_chunk(L.h, cc, hv);
             load_f32_chunk(L.g, cc, gv);
-            if (LN) load_f32_chunk(L.b, cc, bv);
-            const Q8Chunk q = spec_norm_chunk<LN>(hv, gv, bv, mn, dn, A.post_scale);
-            if (ch < nch) store_act_chunk(L.row, K, ch, q);
+            if constexpr (LN) {
+                load_f32_chunk(L.b, cc, bv);
+                const Q8Chunk q = spec_norm_chunk<LN>(hv, gv, bv, mn, dn, A.post_scale);
+                if (ch < nch) store_act_chunk(L.row, K, ch, q);
+            } else {
+                // with each chunk's first delta and code flag, for the exact side
+                float dl;
+                bool uc;
+                const Q8Chunk q = spec_rms_chunk_cert(hv, gv, dn, A.post_scale, dl, uc);
+                if (ch < nch) {
+                    store_act_chunk(L.row, K, ch, q);
+                    L.uc[ch] = uc ? 1 : 0;
+                    if ((ch & 3) == 0) L.dl[ch >> 2] = dl;
+                }
+            }
         }
+        if (sc == 0) sy.dn = dn;
         if (ROW_FIRST) load_w();
     }
     SsWaveBarrier<NS / kWave> sbar{&sy.spec, 0};
