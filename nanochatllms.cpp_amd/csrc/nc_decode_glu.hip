@@ -206,9 +206,17 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
     // Further gate|up blocks of this workgroup (when the grid holds fewer
     // workgroups than blocks) take the exact row already in place: terms by
     // the weight role, then the exact role's tail.
+    // Which role is on the critical path: with Q4 weights and rms_norm the
+    // weight role (its terms, fold and SwiGLU take longer than the exact
+    // sum; its wavefronts issue first: TinyLlama Q4 1,593 -> 1,620 tok/s,
+    // MiniCPM Q4 566 -> 569), with layer_norm the exact role (the mean's
+    // sum, then the variance's; weight-first Zephyr Q4 went 1,184 -> 1,150).
+    // Q8 rms_norm launches measured the same either way (TinyLlama Q8 1,399
+    // -> 1,397, OpenELM Q8 1,069 -> 1,070) and keep the exact role first.
+    constexpr bool kWeightFirst = !pro_ln(PRO) && WT == Q4;
     if (__builtin_amdgcn_readfirstlane(tid) < kSpecExact) {
         Q8Chunk qx[NCH];
-        spec_exact<PRO, NCH, NS, spec_issue<WT, PRO>()>(P, L, ssh, sgh, sy, qx);
+        spec_exact<PRO, NCH, NS, spec_issue<WT, PRO>(), kWeightFirst ? 0 : 3>(P, L, ssh, sgh, sy, qx);
         lds_barrier();  // B2
         if (sy.anybad) {
             spec_exact_fixup<NCH>(P, L, qx);
@@ -219,6 +227,7 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
             exact_tail();
         }
     } else {
+        if (kWeightFirst) __builtin_amdgcn_s_setprio(2);
         spec_weights<PRO, NCH, NS, spec_issue<WT, PRO>()>(P, L, sy, load_w, terms, spec_tail);
         lds_barrier();  // B2
         if (!sy.anybad) {

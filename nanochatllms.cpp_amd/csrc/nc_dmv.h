@@ -452,7 +452,7 @@ constexpr int spec_issue()
     return WT != Q4 ? kIssueAfterRows : (pro_ln(PRO) ? kIssueAfterSpecRow : kIssueEarly);
 }
 
-template <int PRO, int NCH, int NS, int ISSUE>
+template <int PRO, int NCH, int NS, int ISSUE, int PRIO = 3>
 __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, SsShared& ssh, SgShared& sgh,
                                            SpecSync& sy, Q8Chunk (&qx)[NCH])
 {
@@ -475,8 +475,8 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
         sy.spec = 0;
         sy.anybad = 0;
     }
-    // the critical path: these wavefronts issue first
-    __builtin_amdgcn_s_setprio(3);
+    // on the critical path (PRIO 3), these wavefronts issue first
+    __builtin_amdgcn_s_setprio(PRIO);
     const uint8_t* arow;
     if (fixed) {
         arow = !RES ? A.x : A.res_cur;
@@ -593,7 +593,7 @@ __device__ __forceinline__ void spec_exact(const DmvArgs& A, const SpecLds& L, S
         bar();
     }
     // (reg8: the first phase ran before the barrier that published the terms)
-    const float ss = reg8 ? block_seq_sum_after<8, false>(v16, I, L.sq, K, ssh, nullptr, bar)
+    const float ss = reg8 ? block_seq_sum_after<8, false, false>(v16, I, L.sq, K, ssh, nullptr, bar)
                           : block_seq_sum_nonneg_bar(L.sq, K, ssh, bar);
     const float denom = LN ? sqrtf(ss / (float)K) + 1e-05f : sqrtf(ss / (float)K) + 1e-6f;
     if constexpr (LN) {

@@ -88,17 +88,24 @@ constexpr int kSsThreads = 256;   // workgroup size the block sum is written for
 constexpr int kSsMaxPer = 16;     // terms per thread: n <= 4096
 constexpr int kSsMaxCross = 63;   // crossings handled before the fallback
 constexpr int kSsMaxRec = 4;      // crossings one thread's chunk may hold before the fallback
+constexpr int kSsWaveRec = 32;    // crossings one wavefront's chunks may hold before the fallback
 constexpr int kSsHead = 8;        // chunks in the head
+
+// Crossing record flags (next to the binade in a record's third word).
+constexpr int kSsRecNz = 0x100;    // the record's map holds a nonzero term
+constexpr int kSsRecBack = 0x200;  // its segment opened in an earlier wavefront
 
 struct SsShared {
     // the wave arrays are read as one 16-byte vector each: keep them first
     float wf[kSsThreads / kWave];
     int wc0[kSsThreads / kWave], wc1[kSsThreads / kWave], wfl[kSsThreads / kWave], wcnt[kSsThreads / kWave];
-    int4 rec[kSsMaxCross + 1];  // crossing records: map (c0, c1), binade (0: no check), term bits
-    int m;
+    // per wavefront, its crossing records in order: the map (c0, c1) of the
+    // segment that ends at the crossing, binade | flags, the crossing term's bits
+    int4 rec[kSsThreads / kWave][kSsWaveRec];
     int ok;
     float result;
     float head;  // the exact sum of the head chunks
+    int tail_e;  // the binade of the segment after the last crossing
 };
 
 // Segmented scan element: a parity map and flags (bit 0: nz, bit 1: the
@@ -108,11 +115,15 @@ struct SsSeg {
 };
 
 // (a then b): b alone when b restarts, else the composition.
+// Written with bit selects (no branches): p0, p1 are all ones where a's
+// count is odd (b then starts on the other parity), rb where b restarts.
 __device__ __forceinline__ SsSeg ss_seg(const SsSeg& a, const SsSeg& b)
 {
-    if (b.f & 2) return SsSeg{b.c0, b.c1, b.f, a.n + b.n};
-    const SsMap m = ss_compose(SsMap{a.c0, a.c1, (a.f & 1) != 0}, SsMap{b.c0, b.c1, (b.f & 1) != 0});
-    return SsSeg{m.c0, m.c1, (m.nz ? 1 : 0) | (a.f & 2), a.n + b.n};
+    const int p0 = -(a.c0 & 1), p1 = -(a.c1 & 1);
+    const int c0 = a.c0 + ((p0 & b.c1) | (~p0 & b.c0));
+    const int c1 = a.c1 + ((p1 & b.c0) | (~p1 & b.c1));
+    const int rb = -((b.f >> 1) & 1);
+    return SsSeg{(rb & b.c0) | (~rb & c0), (rb & b.c1) | (~rb & c1), b.f | (~rb & a.f), a.n + b.n};
 }
 
 template <int CTRL, int ROW_MASK = 0xf, bool BZ = true>
@@ -159,7 +170,9 @@ __device__ __forceinline__ SsSeg wave_scan_seg(SsSeg x)
 // exactly (the start of everything after it).  Every later thread walks its
 // chunk once: binade predicted from an approximate prefix, step maps
 // composed, and up to four crossings recorded (more fall back).  A segmented
-// scan joins the chunks, and wave 0 replays the few records in order.
+// scan joins the chunks of a wavefront, which stores its records at once;
+// after one barrier every computing wavefront composes the four wavefronts'
+// open segments and replays the few records in order.
 //
 // The barrier among the 256 threads is a functor: the workgroup's LDS
 // barrier, or SsWaveBarrier when the first four wavefronts compute the sum
@@ -213,9 +226,12 @@ __device__ __forceinline__ float ss_prefix(const float (&v)[kSsMaxPer], int c, S
 
 // The rest of the sum after ss_prefix and a barrier (threads 0..255): the
 // terms t[0..n) also in LDS (the head and the fallback read them there).
-// FINAL: end with a barrier after which sh may be reused (without it, sh
-// must not be written again by this workgroup).
-template <int C, bool FINAL, class Bar>
+// Every computing thread returns the sum.  BCAST: a barrier after the
+// replay publishes the result and sh.ok, for threads past the first 256 that
+// take the barriers without computing.  FINAL: end with a barrier after which
+// sh may be reused (without it, sh must not be written again by this
+// workgroup).
+template <int C, bool FINAL, bool BCAST, class Bar>
 __device__ __forceinline__ float block_seq_sum_after(const float (&v)[kSsMaxPer], float I, const float* t, int n,
                                                      SsShared& sh, bool* fast, Bar& bar)
 {
@@ -294,14 +310,38 @@ __device__ __forceinline__ float block_seq_sum_after(const float (&v)[kSsMaxPer]
         c1 = __builtin_bit_cast(int, r1) - (b0 | 1);
         nz = nzb ? 1 : 0;
     }
-    // the head's exact sum, by the last thread (after its own chunk)
-    if (tid == kSsThreads - 1) sh.head = seq_sum(t, nh);
-    // ---- segmented scan of (open map, has-crossing) and scan of the counts
+    // the head's exact sum, by the last thread (after its own chunk), and the
+    // binade of the segment after the last crossing (the prefix at the end)
+    if (tid == kSsThreads - 1) {
+        sh.head = seq_sum(t, nh);
+        sh.tail_e = ss_binade(I);
+    }
+    // ---- segmented scan of (open map, has-crossing) and scan of the counts,
+    // within the wavefront
     SsSeg x{c0, c1, nz | (ncross > 0 ? 2 : 0), ncross};
     x = wave_scan_seg(x);
     // a chunk with too many crossings or a representative that left its
     // binade takes the plain loop
     const int over = __builtin_amdgcn_ballot_w64(ncross > kSsMaxRec || bad) != 0;
+    // the open segment entering this chunk (from the wavefront's start), and
+    // the wavefront's crossings before it
+    SsSeg in = ss_dpp<kDppWaveShr1>(x);
+    if (lane == 0) in = SsSeg{0, 0, 0, 0};
+    const int base = in.n;
+    if (ncross > 0) {
+        // the first crossing closes the segment open at the chunk start (its
+        // binade: no crossing before it in this chunk); when that segment
+        // opened before this wavefront, the replay composes the earlier
+        // wavefronts' part in front of it (kSsRecBack)
+        const SsMap m0 = ss_compose(SsMap{in.c0, in.c1, (in.f & 1) != 0}, SsMap{rec[0].x, rec[0].y, rec[0].z != 0});
+        rec[0] = make_int4(m0.c0, m0.c1, ss_binade(A) | (m0.nz ? kSsRecNz : 0) | ((in.f & 2) ? 0 : kSsRecBack),
+                           rec[0].w);
+#pragma unroll
+        for (int q = 1; q < kSsMaxRec; q++) rec[q].z = rec[q].z ? (rec[q].z | kSsRecNz) : 0;
+#pragma unroll
+        for (int q = 0; q < kSsMaxRec; q++)
+            if (q < ncross && base + q < kSsWaveRec) sh.rec[w][base + q] = rec[q];
+    }
     if (lane == kWave - 1) {
         sh.wc0[w] = x.c0;
         sh.wc1[w] = x.c1;
@@ -309,102 +349,94 @@ __device__ __forceinline__ float block_seq_sum_after(const float (&v)[kSsMaxPer]
         sh.wcnt[w] = x.n | (over << 30);
     }
     bar();
-    SsSeg pre{0, 0, 0, 0};
-    int any_over;
-    {
-        // every wave's scan total at once, then the earlier waves' composed in order
-        const int4 W0 = *reinterpret_cast<const int4*>(sh.wc0), W1 = *reinterpret_cast<const int4*>(sh.wc1);
-        const int4 WF = *reinterpret_cast<const int4*>(sh.wfl), WN = *reinterpret_cast<const int4*>(sh.wcnt);
-        const int a0[4] = {W0.x, W0.y, W0.z, W0.w}, a1[4] = {W1.x, W1.y, W1.z, W1.w};
-        const int af[4] = {WF.x, WF.y, WF.z, WF.w}, an[4] = {WN.x, WN.y, WN.z, WN.w};
-#pragma unroll
-        for (int q = 0; q < 3; q++)
-            if (q < w) pre = ss_seg(pre, SsSeg{a0[q], a1[q], af[q], an[q] & 0xFFFF});
-        any_over = (an[0] | an[1] | an[2] | an[3]) >> 30;
-    }
-    x = ss_seg(pre, x);
-    const int cnt = x.n;
-    // the open segment entering this chunk, and the crossings before it
-    SsSeg in = ss_dpp<kDppWaveShr1>(x);
-    if (lane == 0) in = pre;
-    const int base = in.n;
-    // records in crossing order: the first crossing of a chunk closes the
-    // segment open at its start
-    if (ncross > 0) {
-        // the first crossing closes the segment open at the chunk start
-        // (its binade: no crossing before it in this chunk)
-        const SsMap m0 = ss_compose(SsMap{in.c0, in.c1, (in.f & 1) != 0}, SsMap{rec[0].x, rec[0].y, rec[0].z != 0});
-        rec[0] = make_int4(m0.c0, m0.c1, m0.nz ? ss_binade(A) : 0, rec[0].w);
-#pragma unroll
-        for (int q = 0; q < kSsMaxRec; q++)
-            if (q < ncross && base + q < kSsMaxCross) sh.rec[base + q] = rec[q];
-    }
-    if (tid == kSsThreads - 1) {
-        sh.m = any_over ? kSsMaxCross + 1 : cnt;
-        if (cnt < kSsMaxCross) sh.rec[cnt] = make_int4(x.c0, x.c1, (x.f & 1) ? ss_binade(I) : 0, 0);
-    }
-    bar();
-    // ---- replay on wave 0 from thread 0's exact chunk sum: record r in lane
-    // r; per record s = s + u C(parity) (when the segment holds a nonzero
-    // term), then the crossing add; the binade checks ride beside the chain
-    if (w == 0) {
-        const int mm = sh.m;
-        int ok = mm < kSsMaxCross;
+    // ---- replay, on every computing wavefront (no barrier needed after
+    // it): the wavefronts' open segments composed in order, record r in lane
+    // r (the wavefronts' records one after the other, then the segment
+    // after the last crossing); per record s = s + u C(parity) when its
+    // segment holds a nonzero term, then the crossing add; the binade checks
+    // ride beside the chain
+    const int4 W0 = *reinterpret_cast<const int4*>(sh.wc0), W1 = *reinterpret_cast<const int4*>(sh.wc1);
+    const int4 WF = *reinterpret_cast<const int4*>(sh.wfl), WN = *reinterpret_cast<const int4*>(sh.wcnt);
+    const int b1 = WN.x & 0xFFFF, b2 = b1 + (WN.y & 0xFFFF), b3 = b2 + (WN.z & 0xFFFF), mm = b3 + (WN.w & 0xFFFF);
+    const int most = max(max(WN.x & 0xFFFF, WN.y & 0xFFFF), max(WN.z & 0xFFFF, WN.w & 0xFFFF));
+    int ok = mm < kSsMaxCross && most <= kSsWaveRec && ((WN.x | WN.y | WN.z | WN.w) >> 30) == 0;
+    // the open segment entering wavefront q (P1..P3) and after the last (P4)
+    const SsSeg P1 = ss_seg(SsSeg{0, 0, 0, 0}, SsSeg{W0.x, W1.x, WF.x, 0});
+    const SsSeg P2 = ss_seg(P1, SsSeg{W0.y, W1.y, WF.y, 0});
+    const SsSeg P3 = ss_seg(P2, SsSeg{W0.z, W1.z, WF.z, 0});
+    const SsSeg P4 = ss_seg(P3, SsSeg{W0.w, W1.w, WF.w, 0});
+    int sb = __builtin_bit_cast(int, sh.head);
+    if (ok) {
+        int4 R = make_int4(0, 0, 0, 0);  // past the last record: the identity with a +0 term
+        if (lane < mm) {
+            const int wr = (lane >= b1 ? 1 : 0) + (lane >= b2 ? 1 : 0) + (lane >= b3 ? 1 : 0);
+            R = sh.rec[wr][lane - (wr == 0 ? 0 : wr == 1 ? b1 : wr == 2 ? b2 : b3)];
+            if (R.z & kSsRecBack) {
+                const int pc0 = wr == 1 ? P1.c0 : wr == 2 ? P2.c0 : wr == 3 ? P3.c0 : 0;
+                const int pc1 = wr == 1 ? P1.c1 : wr == 2 ? P2.c1 : wr == 3 ? P3.c1 : 0;
+                const int pf = wr == 1 ? P1.f : wr == 2 ? P2.f : wr == 3 ? P3.f : 0;
+                const SsMap m = ss_compose(SsMap{pc0, pc1, (pf & 1) != 0}, SsMap{R.x, R.y, (R.z & kSsRecNz) != 0});
+                R = make_int4(m.c0, m.c1, (R.z & 0xFF) | (m.nz ? kSsRecNz : 0), R.w);
+            }
+        } else if (lane == mm) {
+            R = make_int4(P4.c0, P4.c1, sh.tail_e | ((P4.f & 1) ? kSsRecNz : 0), 0);
+        }
         // within binade E consecutive grid values have consecutive bit
         // patterns (E = 1 spans the subnormals too), so s + u C is bits + C
-        // and the parity of s / u is the last bit; records past the last are
-        // the identity with a +0 term, which leaves s as it is.  Lane r
-        // holds record r; the chain reads them with readlane, in vector
-        // registers (the empty asm marks the state lane-varying, so it does
-        // not bounce through scalar registers).
-        int sb = __builtin_bit_cast(int, sh.head);
-        if (ok) {
-            const int4 R = lane <= mm ? sh.rec[lane] : make_int4(0, 0, 0, 0);
-            int okl = R.z == 0 || R.z < 255;
-            asm volatile("" : "+v"(sb));
-            int sbl = 0, nbl = 0;  // the chain's value entering / leaving record `lane` (for the checks)
-            for (int r0 = 0; r0 <= mm; r0 += 2) {
+        // and the parity of s / u is the last bit: C = C0, or C0 + (C1 - C0)
+        // when the bits are odd.  The chain reads the records with readlane,
+        // in vector registers (the empty asm marks the state lane-varying, so
+        // it does not bounce through scalar registers).
+        const int dc = R.y - R.x;
+        int okl = !(R.z & kSsRecNz) || (R.z & 0xFF) < 255;
+        asm volatile("" : "+v"(sb));
+        int sbl = 0, nbl = 0;  // the chain's value entering / leaving record `lane` (for the checks)
+        for (int r0 = 0; r0 <= mm; r0 += 2) {
 #pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    // past the last record: lane 63, which holds the identity
-                    // (mm < kSsMaxCross = 63); readlane indices stay below 64
-                    const int r = min(r0 + k, kWave - 1);
-                    const int C0 = __builtin_amdgcn_readlane(R.x, r), C1 = __builtin_amdgcn_readlane(R.y, r);
-                    const float tr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(R.w, r));
-                    const int nb = sb + ((sb & 1) ? C1 : C0);
-                    sbl = lane == r ? sb : sbl;
-                    nbl = lane == r ? nb : nbl;
-                    sb = __builtin_bit_cast(int, __builtin_bit_cast(float, nb) + tr);
-                }
+            for (int k = 0; k < 2; k++) {
+                // past the last record: lane 63, which holds the identity
+                // (mm < kSsMaxCross = 63); readlane indices stay below 64
+                const int r = min(r0 + k, kWave - 1);
+                const int C0 = __builtin_amdgcn_readlane(R.x, r), DC = __builtin_amdgcn_readlane(dc, r);
+                const float tr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(R.w, r));
+                const int nb = sb + C0 + (-(sb & 1) & DC);
+                sbl = lane == r ? sb : sbl;
+                nbl = lane == r ? nb : nbl;
+                sb = __builtin_bit_cast(int, __builtin_bit_cast(float, nb) + tr);
             }
-            // record `lane`'s segment must start and end inside its binade
-            if (lane <= mm && R.z != 0)
-                okl = okl && ss_binade(__builtin_bit_cast(float, sbl)) == R.z &&
-                      ss_binade(__builtin_bit_cast(float, nbl)) == R.z;
-            ok = __builtin_amdgcn_ballot_w64(!okl) == 0;
         }
-        if (lane == 0) {
-            sh.result = __builtin_bit_cast(float, sb);
+        // record `lane`'s segment must start and end inside its binade
+        if (lane <= mm && (R.z & kSsRecNz))
+            okl = okl && ss_binade(__builtin_bit_cast(float, sbl)) == (R.z & 0xFF) &&
+                  ss_binade(__builtin_bit_cast(float, nbl)) == (R.z & 0xFF);
+        ok = __builtin_amdgcn_ballot_w64(!okl) == 0;
+    }
+    float res = __builtin_bit_cast(float, sb);
+    if (BCAST) {
+        // for threads past the computing ones (they take the barriers too)
+        if (tid == 0) {
+            sh.result = res;
             sh.ok = ok;
         }
+        bar();
     }
-    bar();
-    if (!sh.ok) {
-        // fallback: the plain loop on one wavefront
+    if (!ok) {
+        // fallback (the same on every computing wavefront): the plain loop
+        // on one wavefront
         if (tid < kWave) {
             const float s = seq_sum(t, n);
             if (tid == 0) sh.result = s;
         }
         bar();
+        res = sh.result;
     }
-    if (fast && tid == 0) *fast = sh.ok != 0;
-    const float res = sh.result;
+    if (fast && tid == 0) *fast = ok != 0;
     if (FINAL) bar();  // sh reusable after return
     return res;
 }
 
-// Threads 0..255 only.
-template <int C, class Bar>
+// Threads 0..255 only (BCAST: see block_seq_sum_after).
+template <int C, bool BCAST = false, class Bar>
 __device__ __forceinline__ float block_seq_sum_core(const float* t, int n, SsShared& sh, bool* fast, Bar& bar)
 {
     const int tid = threadIdx.x;
@@ -429,7 +461,7 @@ __device__ __forceinline__ float block_seq_sum_core(const float* t, int n, SsSha
     }
     const float I = ss_prefix<C>(v, c, sh);
     bar();
-    return block_seq_sum_after<C, true>(v, I, t, n, sh, fast, bar);
+    return block_seq_sum_after<C, true, BCAST>(v, I, t, n, sh, fast, bar);
 }
 
 
@@ -439,9 +471,8 @@ template <int C>
 __device__ __forceinline__ float block_seq_sum_impl(const float* t, int n, SsShared& sh, bool* fast)
 {
     if (threadIdx.x >= kSsThreads) {
-        // the four phase barriers, the fallback's barrier when it is
+        // the three phase barriers, the fallback's barrier when it is
         // taken, and the final one
-        lds_barrier();
         lds_barrier();
         lds_barrier();
         lds_barrier();
@@ -451,7 +482,7 @@ __device__ __forceinline__ float block_seq_sum_impl(const float* t, int n, SsSha
         return res;
     }
     SsLdsBarrier bar;
-    return block_seq_sum_core<C>(t, n, sh, fast, bar);
+    return block_seq_sum_core<C, true>(t, n, sh, fast, bar);
 }
 
 // The sum of 2048 terms where thread j < 256 holds terms [8 j, 8 j + 8) in
@@ -474,12 +505,11 @@ __device__ __forceinline__ float block_seq_sum_regs8(const float (&t8)[8], const
         // the phase barriers of the computing threads, and the fallback's
         lds_barrier();
         lds_barrier();
-        lds_barrier();
         if (!sh.ok) lds_barrier();
         return sh.result;
     }
     SsLdsBarrier bar;
-    return block_seq_sum_after<8, false>(v, I, t, 8 * kSsThreads, sh, nullptr, bar);
+    return block_seq_sum_after<8, false, true>(v, I, t, 8 * kSsThreads, sh, nullptr, bar);
 }
 
 // Dispatch on the terms per thread (compile-time chunk lengths for the
