@@ -88,11 +88,13 @@ __global__ __launch_bounds__(kGluThreads) void k_dmv_glu(DmvArgs A)
     };
     for (;;) {
         pass();
-        if (tid < 32) {
-            const float gq = q8_roundtrip_lane(s_out[tid], true);
-            const float gs = q8_roundtrip_lane(gq / (1.0f + expf_ref(-gq)), true);
-            const float uq = q8_roundtrip_lane(s_out[32 + tid], true);
-            act_store<Q8>(A.m_out, 32 * b + tid, f, gs * uq, true);
+        if (tid < 64) {
+            // lanes 0-31: the gate chain; lanes 32-63: the up value's round
+            // trip beside it (each half-wavefront its own 32-value block)
+            const float v = q8_roundtrip_lane(s_out[tid], true);
+            const float uq = __shfl(v, (tid & 31) + 32);
+            const float gs = q8_roundtrip_lane(v / (1.0f + expf_ref(-v)), true);
+            act_store<Q8>(A.m_out, 32 * b + (tid & 31), f, gs * uq, tid < 32);
         }
         b += gridDim.x;
         if (b >= nblk) break;
@@ -166,12 +168,15 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
         const float res = (acc + dpp_f<kDppQuadXor1>(acc)) + (dpp_f<kDppQuadXor2>(acc) + dpp_f<0x1B>(acc));
         if ((t & 3) == 0) s_out[t >> 2] = res;
     };
-    // SwiGLU of element 32 b + l from s_out (lanes 0..31 of a wavefront):
-    // m = Act(Act(silu(Act(g))) * Act(u)), its code and fp16 delta
+    // SwiGLU of element 32 b + (l & 31) from s_out, on a whole wavefront
+    // (l: its lane): m = Act(Act(silu(Act(g))) * Act(u)), its code and fp16
+    // delta on lanes 0-31.  Lanes 32-63 round-trip the up value beside the
+    // gate chain (each half-wavefront its own 32-value block); their other
+    // results are not used.
     auto swiglu = [&](int l, uint16_t* d16) {
-        const float gq = q8_roundtrip_lane(s_out[l], true);
-        const float gs = q8_roundtrip_lane(gq / (1.0f + expf_ref(-gq)), true);
-        const float uq = q8_roundtrip_lane(s_out[32 + l], true);
+        const float v = q8_roundtrip_lane(s_out[l], true);
+        const float uq = __shfl(v, (l & 31) + 32);
+        const float gs = q8_roundtrip_lane(v / (1.0f + expf_ref(-v)), true);
         return q8_quant_lane(gs * uq, true, d16);
     };
     auto store = [&](int l, int8_t q, uint16_t d16) {
@@ -188,17 +193,17 @@ __global__ __launch_bounds__(kSpecExact + kGluThreads) void k_dmv_glu_spec(DmvAr
         bar();
         if (s < 64 * 4) fold(s);
         bar();
-        if (s < 32) sq8 = swiglu(s, &sd16);
+        if (s < 64) sq8 = swiglu(s, &sd16);
     };
     // the exact role's fold and epilogue from the exact terms (every exact
     // thread folds one lane of one row)
     auto exact_tail = [&] {
         fold(tid);
         lds_barrier();
-        if (tid < 32) {
+        if (tid < 64) {
             uint16_t d16;
             const int8_t q = swiglu(tid, &d16);
-            store(tid, q, d16);
+            if (tid < 32) store(tid, q, d16);
         }
     };
     DmvArgs P = A;
