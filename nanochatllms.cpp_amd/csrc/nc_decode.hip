@@ -114,8 +114,9 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
     int& s_tok = *s_tok_p;
 
     // Two-level reduction over the workgroups: keys in slots, the last
-    // of each 32 workgroups reduces its slots, the last of those the
-    // rest.  Keys and level-1 results are written with agent-scope atomic
+    // of each 32 workgroups reduces its slots and stores the group's result,
+    // then reads every group's (level 2 has no counter: one round trip
+    // fewer after the last group).  Keys and level-1 results are written with agent-scope atomic
     // stores (through the XCD's L2) and read with agent-scope atomic loads,
     // so they are coherent across the XCDs' L2s without a cache flush.  A
     // writer waits for its store to complete (wait_stores_done) before it
@@ -123,9 +124,9 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
     // write-back of a release fence), so a reader that sees the count sees
     // every key counted; the last arriver takes an agent-scope acquire fence
     // before it reads them.
-    // Scratch layout (64-bit words): [0] top counter, [64, 192) level-1
-    // results, [192, 320) level-1 counters, [320, 320 + grid) workgroup keys.
-    unsigned long long* top = A.amax;
+    // Scratch layout (64-bit words): [0] unused, [64, 192) level-1 results
+    // (zero between launches), [192, 320) level-1 counters, [320, 320 +
+    // grid) workgroup keys.
     unsigned long long* sub = A.amax + 64;
     unsigned long long* cnt = A.amax + 192;
     unsigned long long* slot = A.amax + 320;
@@ -162,31 +163,44 @@ __device__ __forceinline__ void argmax_epilogue(const DmvArgs& A, unsigned long 
                 const unsigned long long other = __shfl_xor(k, o);
                 k = other > k ? other : k;
             }
-            unsigned long long done2 = 0;
+            // level 2 without a counter: this group's result stored (and
+            // waited for), then every group's read at once; a level-1
+            // finisher that sees them all (the last one does, and any other
+            // that sees them agrees) takes the token and clears them for
+            // the next launch (zero: not yet written; a result is nonzero)
             if (tid == 0) {
                 __hip_atomic_store(cnt + grp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(sub + grp, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 wait_stores_done();
-                done2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            done2 = __shfl(done2, 0);
-            if (done2 == (unsigned long long)ngrp - 1) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-                unsigned long long b2 = 0;
-                for (int q = tid; q < ngrp; q += kWave) {
+            __builtin_amdgcn_wave_barrier();
+            unsigned long long b2 = 0;
+            bool all = true;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int q = tid + h * kWave;
+                if (q < ngrp) {
                     const unsigned long long o = __hip_atomic_load(sub + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    all = all && o != 0;
                     b2 = o > b2 ? o : b2;
                 }
+            }
+            if (__builtin_amdgcn_ballot_w64(!all) == 0) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
                 for (int o = 32; o >= 1; o >>= 1) {
                     const unsigned long long other = __shfl_xor(b2, o);
                     b2 = other > b2 ? other : b2;
                 }
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int q = tid + h * kWave;
+                    if (q < ngrp) __hip_atomic_store(sub + q, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
                 if (tid == 0) {
                     const int tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull));
                     A.tokens[pos + 1] = tok;
                     if (A.dpos) A.pos_out[0] = pos + 1;
-                    __hip_atomic_store(top, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     s_tok = tok;
                 }
             }
