@@ -88,8 +88,10 @@ constexpr int kSsThreads = 256;   // workgroup size the block sum is written for
 constexpr int kSsMaxPer = 16;     // terms per thread: n <= 4096
 constexpr int kSsMaxCross = 63;   // crossings handled before the fallback
 constexpr int kSsMaxRec = 4;      // crossings one thread's chunk may hold before the fallback
-constexpr int kSsWaveRec = 32;    // crossings one wavefront's chunks may hold before the fallback
+constexpr int kSsWaveRec = 16;    // crossings one wavefront's chunks may hold before the fallback (16 x 4 = 64 lanes)
 constexpr int kSsHead = 8;        // chunks in the head
+
+static_assert(kSsWaveRec * (kSsThreads / kWave) == kWave, "one lane per record slot in the replay");
 
 // Crossing record flags (next to the binade in a record's third word).
 constexpr int kSsRecNz = 0x100;    // the record's map holds a nonzero term
@@ -350,16 +352,21 @@ __device__ __forceinline__ float block_seq_sum_after(const float (&v)[kSsMaxPer]
     }
     bar();
     // ---- replay, on every computing wavefront (no barrier needed after
-    // it): the wavefronts' open segments composed in order, record r in lane
-    // r (the wavefronts' records one after the other, then the segment
-    // after the last crossing); per record s = s + u C(parity) when its
+    // it).  Lane l reads record l & 15 of wavefront l >> 4 together with the
+    // wavefronts' totals (one LDS round trip; lanes past a wavefront's count
+    // hold stale words and take no part).  The open segment entering each
+    // wavefront is composed from the totals and put in front of that
+    // wavefront's first record where its segment opened earlier; the chain
+    // then takes the records lane by lane in order, and the segment after
+    // the last crossing last.  Per record s = s + u C(parity) when its
     // segment holds a nonzero term, then the crossing add; the binade checks
-    // ride beside the chain
+    // ride beside the chain.
     const int4 W0 = *reinterpret_cast<const int4*>(sh.wc0), W1 = *reinterpret_cast<const int4*>(sh.wc1);
     const int4 WF = *reinterpret_cast<const int4*>(sh.wfl), WN = *reinterpret_cast<const int4*>(sh.wcnt);
-    const int b1 = WN.x & 0xFFFF, b2 = b1 + (WN.y & 0xFFFF), b3 = b2 + (WN.z & 0xFFFF), mm = b3 + (WN.w & 0xFFFF);
-    const int most = max(max(WN.x & 0xFFFF, WN.y & 0xFFFF), max(WN.z & 0xFFFF, WN.w & 0xFFFF));
-    int ok = mm < kSsMaxCross && most <= kSsWaveRec && ((WN.x | WN.y | WN.z | WN.w) >> 30) == 0;
+    int4 R = sh.rec[lane >> 4][lane & (kSsWaveRec - 1)];
+    const int n0 = WN.x & 0xFFFF, n1 = WN.y & 0xFFFF, n2 = WN.z & 0xFFFF, n3 = WN.w & 0xFFFF;
+    const int most = max(max(n0, n1), max(n2, n3));
+    int ok = n0 + n1 + n2 + n3 < kSsMaxCross && most <= kSsWaveRec && ((WN.x | WN.y | WN.z | WN.w) >> 30) == 0;
     // the open segment entering wavefront q (P1..P3) and after the last (P4)
     const SsSeg P1 = ss_seg(SsSeg{0, 0, 0, 0}, SsSeg{W0.x, W1.x, WF.x, 0});
     const SsSeg P2 = ss_seg(P1, SsSeg{W0.y, W1.y, WF.y, 0});
@@ -367,19 +374,14 @@ __device__ __forceinline__ float block_seq_sum_after(const float (&v)[kSsMaxPer]
     const SsSeg P4 = ss_seg(P3, SsSeg{W0.w, W1.w, WF.w, 0});
     int sb = __builtin_bit_cast(int, sh.head);
     if (ok) {
-        int4 R = make_int4(0, 0, 0, 0);  // past the last record: the identity with a +0 term
-        if (lane < mm) {
-            const int wr = (lane >= b1 ? 1 : 0) + (lane >= b2 ? 1 : 0) + (lane >= b3 ? 1 : 0);
-            R = sh.rec[wr][lane - (wr == 0 ? 0 : wr == 1 ? b1 : wr == 2 ? b2 : b3)];
-            if (R.z & kSsRecBack) {
-                const int pc0 = wr == 1 ? P1.c0 : wr == 2 ? P2.c0 : wr == 3 ? P3.c0 : 0;
-                const int pc1 = wr == 1 ? P1.c1 : wr == 2 ? P2.c1 : wr == 3 ? P3.c1 : 0;
-                const int pf = wr == 1 ? P1.f : wr == 2 ? P2.f : wr == 3 ? P3.f : 0;
-                const SsMap m = ss_compose(SsMap{pc0, pc1, (pf & 1) != 0}, SsMap{R.x, R.y, (R.z & kSsRecNz) != 0});
-                R = make_int4(m.c0, m.c1, (R.z & 0xFF) | (m.nz ? kSsRecNz : 0), R.w);
-            }
-        } else if (lane == mm) {
-            R = make_int4(P4.c0, P4.c1, sh.tail_e | ((P4.f & 1) ? kSsRecNz : 0), 0);
+        const int wr = lane >> 4, k = lane & (kSsWaveRec - 1);
+        const bool valid = k < (wr == 0 ? n0 : wr == 1 ? n1 : wr == 2 ? n2 : n3);
+        if (valid && (R.z & kSsRecBack)) {
+            const int pc0 = wr == 1 ? P1.c0 : wr == 2 ? P2.c0 : wr == 3 ? P3.c0 : 0;
+            const int pc1 = wr == 1 ? P1.c1 : wr == 2 ? P2.c1 : wr == 3 ? P3.c1 : 0;
+            const int pf = wr == 1 ? P1.f : wr == 2 ? P2.f : wr == 3 ? P3.f : 0;
+            const SsMap m = ss_compose(SsMap{pc0, pc1, (pf & 1) != 0}, SsMap{R.x, R.y, (R.z & kSsRecNz) != 0});
+            R = make_int4(m.c0, m.c1, (R.z & 0xFF) | (m.nz ? kSsRecNz : 0), R.w);
         }
         // within binade E consecutive grid values have consecutive bit
         // patterns (E = 1 spans the subnormals too), so s + u C is bits + C
@@ -388,28 +390,29 @@ __device__ __forceinline__ float block_seq_sum_after(const float (&v)[kSsMaxPer]
         // in vector registers (the empty asm marks the state lane-varying, so
         // it does not bounce through scalar registers).
         const int dc = R.y - R.x;
-        int okl = !(R.z & kSsRecNz) || (R.z & 0xFF) < 255;
         asm volatile("" : "+v"(sb));
-        int sbl = 0, nbl = 0;  // the chain's value entering / leaving record `lane` (for the checks)
-        for (int r0 = 0; r0 <= mm; r0 += 2) {
-#pragma unroll
-            for (int k = 0; k < 2; k++) {
-                // past the last record: lane 63, which holds the identity
-                // (mm < kSsMaxCross = 63); readlane indices stay below 64
-                const int r = min(r0 + k, kWave - 1);
-                const int C0 = __builtin_amdgcn_readlane(R.x, r), DC = __builtin_amdgcn_readlane(dc, r);
-                const float tr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(R.w, r));
-                const int nb = sb + C0 + (-(sb & 1) & DC);
-                sbl = lane == r ? sb : sbl;
-                nbl = lane == r ? nb : nbl;
-                sb = __builtin_bit_cast(int, __builtin_bit_cast(float, nb) + tr);
-            }
+        int sbl = 0, nbl = 0;  // the chain's value entering / leaving this lane's record (for the checks)
+        uint64_t mask = __builtin_amdgcn_ballot_w64(valid);
+        while (mask) {
+            const int src = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            const int C0 = __builtin_amdgcn_readlane(R.x, src), DC = __builtin_amdgcn_readlane(dc, src);
+            const float tr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(R.w, src));
+            const int nb = sb + C0 + (-(sb & 1) & DC);
+            sbl = lane == src ? sb : sbl;
+            nbl = lane == src ? nb : nbl;
+            sb = __builtin_bit_cast(int, __builtin_bit_cast(float, nb) + tr);
         }
-        // record `lane`'s segment must start and end inside its binade
-        if (lane <= mm && (R.z & kSsRecNz))
-            okl = okl && ss_binade(__builtin_bit_cast(float, sbl)) == (R.z & 0xFF) &&
-                  ss_binade(__builtin_bit_cast(float, nbl)) == (R.z & 0xFF);
-        ok = __builtin_amdgcn_ballot_w64(!okl) == 0;
+        // the segment after the last crossing
+        const int nt = sb + P4.c0 + (-(sb & 1) & (P4.c1 - P4.c0));
+        const bool tail_ok = !(P4.f & 1) || (sh.tail_e < 255 && ss_binade(__builtin_bit_cast(float, sb)) == sh.tail_e &&
+                                             ss_binade(__builtin_bit_cast(float, nt)) == sh.tail_e);
+        sb = nt;
+        // every record's segment must start and end inside its binade
+        int okl = !valid || !(R.z & kSsRecNz) ||
+                  ((R.z & 0xFF) < 255 && ss_binade(__builtin_bit_cast(float, sbl)) == (R.z & 0xFF) &&
+                   ss_binade(__builtin_bit_cast(float, nbl)) == (R.z & 0xFF));
+        ok = tail_ok && __builtin_amdgcn_ballot_w64(!okl) == 0;
     }
     float res = __builtin_bit_cast(float, sb);
     if (BCAST) {
