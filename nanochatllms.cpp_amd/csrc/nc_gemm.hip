@@ -235,12 +235,14 @@ __device__ __forceinline__ void s8x4_to_h(uint32_t v, uint32_t& lo, uint32_t& hi
 // block j, so no fold waits on the MFMA just issued.  CL: the weights are
 // read from their chunk-major copy (k_chunk_layout), where a wavefront's
 // codes of four blocks are one contiguous 1 KB (Q4) and a thread's are one
-// 16-byte load, instead of four 4-byte loads from 16 rows each.
-template <int WT, int MR, int NW, int CH, int PF, bool CL>
-__global__ __launch_bounds__(64 * NW) void k_gemm_qh(const uint8_t* __restrict__ x, int x_pitch, int n_rows,
-                                                       const uint32_t* __restrict__ wq,
-                                                       const uint16_t* __restrict__ wd, float* __restrict__ out,
-                                                       int out_pitch, int N, int nb)
+// 16-byte load, instead of four 4-byte loads from 16 rows each.  WPE: the
+// wavefronts per SIMD the registers are allotted for (the fold is
+// vector-unit work and needs wavefronts beside each other to cover its
+// latencies).
+template <int WT, int MR, int NW, int CH, int PF, bool CL, int WPE = 1>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void k_gemm_qh(
+        const uint8_t* __restrict__ x, int x_pitch, int n_rows, const uint32_t* __restrict__ wq,
+        const uint16_t* __restrict__ wd, float* __restrict__ out, int out_pitch, int N, int nb)
 {
     constexpr int WV = WT == Q4 ? 1 : 2;  // code dwords of one lane of a weight block
     constexpr int WD = WT == Q4 ? 4 : 8;  // code dwords per weight block
@@ -392,15 +394,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_qh(const uint8_t* __restrict__
             const int ch = cb + p;
             if (ch >= nch) break;  // uniform
             const int buf = ch & 1;
-            // the chunk's activation operands and row deltas, read at once
-            // (one LDS wait per chunk)
-            uint4 Ar[CH][MR];
+            // the chunk's row deltas, and the activation operands two
+            // blocks ahead in a ring of two (block j + 2 is read into block
+            // j's slot once block j's products are issued), which keeps the
+            // registers within three wavefronts per SIMD
+            uint4 Ar[2][MR];
             float dxr[CH][MR];
 #pragma unroll
             for (int j = 0; j < CH; j++)
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
-                    Ar[j][m] = xa[buf][j][m][lane];
+                    if (j < 2) Ar[j][m] = xa[buf][j][m][lane];
                     dxr[j][m] = xd[buf][j][4 * m + lg];
                 }
             f4_t L[2][MR];
@@ -422,7 +426,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_qh(const uint8_t* __restrict__
 #pragma unroll
                     for (int m = 0; m < MR; m++)
                         L[cur ^ 1][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(h8_t, Ar[j + 1][m]), Bh, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                            __builtin_bit_cast(h8_t, Ar[cur ^ 1][m]), Bh, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                }
+                if (j + 2 < CH) {
+#pragma unroll
+                    for (int m = 0; m < MR; m++) Ar[cur][m] = xa[buf][j + 2][m][lane];
                 }
                 // block j's folds in block order: row 4m + lg, lane sums k
 #pragma unroll
@@ -547,7 +555,7 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
         auto by_type_c = [&](auto wt) {
             constexpr int WT = decltype(wt)::value;
             // chunks of 8 blocks need nb % 8 == 0 (the copy itself is in 4-block chunks)
-            if (wide || tall || n_rows > kGemmShortRows || nb % 8) goc(k_gemm_qh<WT, 4, 4, 4, 2, true>, 4, 4);
+            if (wide || tall || n_rows > kGemmShortRows || nb % 8) goc(k_gemm_qh<WT, 4, 4, 4, 2, true, WT == Q4 ? 3 : 1>, 4, 4);
             else goc(k_gemm_qh<WT, 2, 4, 8, 2, true>, 2, 4);
         };
         if (w->dtype == NC_Q4) by_type_c(std::integral_constant<int, Q4>{});
