@@ -554,8 +554,12 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
         auto goc = [&](auto kern, int mr, int nw) { go(kern, mr, 1, nw, wc); };
         auto by_type_c = [&](auto wt) {
             constexpr int WT = decltype(wt)::value;
-            // chunks of 8 blocks need nb % 8 == 0 (the copy itself is in 4-block chunks)
-            if (wide || tall || n_rows > kGemmShortRows || nb % 8) goc(k_gemm_qh<WT, 4, 4, 4, 2, true, WT == Q4 ? 3 : 1>, 4, 4);
+            // chunks of 8 blocks need nb % 8 == 0 (the copy itself is in
+            // 4-block chunks).  Long Q4 prompts: 8 rows per workgroup, one
+            // chunk in flight, five wavefronts per SIMD (84 VGPRs).
+            if (wide && WT == Q4) goc(k_gemm_qh<WT, 2, 4, 4, 1, true, 5>, 2, 4);
+            else if (wide || tall || n_rows > kGemmShortRows || nb % 8)
+                goc(k_gemm_qh<WT, 4, 4, 4, 2, true, WT == Q4 ? 3 : 1>, 4, 4);
             else goc(k_gemm_qh<WT, 2, 4, 8, 2, true>, 2, 4);
         };
         if (w->dtype == NC_Q4) by_type_c(std::integral_constant<int, Q4>{});
