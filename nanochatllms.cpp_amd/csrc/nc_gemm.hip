@@ -210,11 +210,18 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 
 // Four bytes b0..b3 of `u` (each below 256) as fp16 1024 + b, two per dword:
 // [b0, b1] and [b2, b3] (v_perm_b32 with the exponent byte 0x64 from a
-// constant), then plus `bias` (fp16, both halves): exact integers.
+// constant).
+__device__ __forceinline__ void bytes_to_h1024(uint32_t u, uint32_t& lo, uint32_t& hi)
+{
+    lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+}
+
+// The same, then plus `bias` (fp16, both halves): exact integers.
 __device__ __forceinline__ void bytes_to_h(uint32_t u, uint32_t bias2, uint32_t& lo, uint32_t& hi)
 {
-    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    uint32_t a, b;
+    bytes_to_h1024(u, a, b);
     const h2_t bb = __builtin_bit_cast(h2_t, bias2);
     lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, a) + bb);
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, b) + bb);
@@ -253,6 +260,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     // rows' deltas [buffer][block][row]
     __shared__ __align__(16) uint4 xa[2][CH][MR][64];
     __shared__ float xd[2][CH][kRows];
+    // CI (the long-prompt Q4 shape: chunk-major copy, at most 8 rows, one
+    // chunk in flight): the products' accumulator start per (block, row,
+    // lane k), -1031 x (sum of the lane's eight activation codes), and raw
+    // weight codes 1024 + n (four conversions fewer per block; the other
+    // shapes have no registers for the starts)
+    constexpr bool CI = WT == Q4 && CL && MR <= 2 && PF == 1;
+    __shared__ __align__(16) float xc[CI ? 2 : 1][CH][kRows][4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int lc = lane & 15, lg = lane >> 4;
     const int r0 = blockIdx.y * kRows;
@@ -307,6 +321,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
             s8x4_to_h(bq, hv.z, hv.w);
             xa[buf][j][r >> 2][(r & 3) * 4 + k + 16 * k] = hv;
             if (k == 0) xd[buf][j][r] = h2f(q[i].d16);
+            if constexpr (CI)
+                xc[buf][j][r][k] = -1031.0f * (float)(__builtin_amdgcn_sdot4((int)a, 0x01010101, 0, false) +
+                                                       __builtin_amdgcn_sdot4((int)bq, 0x01010101, 0, false));
         }
     };
 
@@ -363,9 +380,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     // one block's B operand (fp16 codes) and delta
     auto b_operand = [&](const WChunk& w, int j, h8_t& Bh, float& dw) {
         uint4 B;
-        if (WT == Q4) {
+        if (CI) {
             // high nibbles pair with the lane's codes {2k,2k+1,2k+8,2k+9},
-            // low nibbles with those + 16
+            // low nibbles with those + 16; raw 1024 + n (the accumulator
+            // start takes off 1031 x the activation codes' sum, so the
+            // result is sum (n - 7) x: every value on the way an integer
+            // below 2^22)
+            const uint32_t P = w.c[j][0];
+            bytes_to_h1024((P >> 4) & 0x0F0F0F0Fu, B.x, B.y);
+            bytes_to_h1024(P & 0x0F0F0F0Fu, B.z, B.w);
+        } else if (WT == Q4) {
+            // the same nibbles as code - 7
             const uint32_t P = w.c[j][0];
             bytes_to_h((P >> 4) & 0x0F0F0F0Fu, kHm1031, B.x, B.y);
             bytes_to_h(P & 0x0F0F0F0Fu, kHm1031, B.z, B.w);
@@ -399,12 +424,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
             // j's slot once block j's products are issued), which keeps the
             // registers within three wavefronts per SIMD
             uint4 Ar[2][MR];
+            f4_t Cr[2][MR];  // CI: accumulator starts, in the same ring
             float dxr[CH][MR];
+            auto c_init = [&](int j, int m) {
+                if constexpr (CI) return *reinterpret_cast<const f4_t*>(&xc[buf][j][4 * m + lg][0]);
+                else return f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            };
 #pragma unroll
             for (int j = 0; j < CH; j++)
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
-                    if (j < 2) Ar[j][m] = xa[buf][j][m][lane];
+                    if (j < 2) {
+                        Ar[j][m] = xa[buf][j][m][lane];
+                        Cr[j][m] = c_init(j, m);
+                    }
                     dxr[j][m] = xd[buf][j][4 * m + lg];
                 }
             f4_t L[2][MR];
@@ -414,8 +447,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
                 b_operand(wr[p], 0, Bh, dw[0]);
 #pragma unroll
                 for (int m = 0; m < MR; m++)
-                    L[0][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, Ar[0][m]), Bh,
-                                                                      f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    L[0][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, Ar[0][m]), Bh, Cr[0][m],
+                                                                      0, 0, 0);
             }
 #pragma unroll
             for (int j = 0; j < CH; j++) {
@@ -426,11 +459,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
                     for (int m = 0; m < MR; m++)
                         L[cur ^ 1][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(h8_t, Ar[cur ^ 1][m]), Bh, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                            __builtin_bit_cast(h8_t, Ar[cur ^ 1][m]), Bh, Cr[cur ^ 1][m], 0, 0, 0);
                 }
                 if (j + 2 < CH) {
 #pragma unroll
-                    for (int m = 0; m < MR; m++) Ar[cur][m] = xa[buf][j + 2][m][lane];
+                    for (int m = 0; m < MR; m++) {
+                        Ar[cur][m] = xa[buf][j + 2][m][lane];
+                        Cr[cur][m] = c_init(j + 2, m);
+                    }
                 }
                 // block j's folds in block order: row 4m + lg, lane sums k
 #pragma unroll
