@@ -552,11 +552,11 @@ int attn_go(const uint8_t* q, int q_pitch, const uint8_t* kc, int k_pitch, const
                                out_pitch, hq, hkv, start, n_ctx, rows, scale);
             return launch_status("k_attn_rows");
         };
-        // four rows per workgroup when eight would leave fewer than 512
+        // four rows per workgroup when eight would leave fewer than 1024
         // workgroups (64-row prompts: TinyLlama-Q4 prefill +4%, its fp16
-        // rows +3% in on-box A/Bs; at MiniCPM's 2,304 workgroups eight stay
-        // 1% ahead, and sixteen were 10% behind)
-        const bool few = hq * ((rows + 7) / 8) < 512;
+        // rows +3%; Zephyr-Q4's 128 rows +4%, in on-box A/Bs; at MiniCPM's
+        // 2,304 workgroups eight stay 1% ahead, and sixteen were 10% behind)
+        const bool few = hq * ((rows + 7) / 8) < 1024;
         if (m <= 1024 && !few) return go_rows(k_attn_rows<ADT, 8>, attn_rows_lds<ADT, 8>(m), 8);
         if (m <= 2048) return go_rows(k_attn_rows<ADT, 4>, attn_rows_lds<ADT, 4>(m), 4);
         return go_rows(k_attn_rows<ADT, 2>, attn_rows_lds<ADT, 2>(m), 2);
