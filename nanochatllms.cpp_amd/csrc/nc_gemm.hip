@@ -592,8 +592,11 @@ int gemm_q_raw(const uint8_t* x, int x_pitch, int n_rows, const nc_tensor* w, fl
             constexpr int WT = decltype(wt)::value;
             // chunks of 8 blocks need nb % 8 == 0 (the copy itself is in
             // 4-block chunks).  Long Q4 prompts: 8 rows per workgroup, one
-            // chunk in flight, five wavefronts per SIMD (84 VGPRs).
+            // chunk in flight, five wavefronts per SIMD (84 VGPRs); medium
+            // ones (81-255 rows): 8 rows, two chunks in flight, four
+            // wavefronts (120 VGPRs).
             if (wide && WT == Q4) goc(k_gemm_qh<WT, 2, 4, 4, 1, true, 5>, 2, 4);
+            else if (n_rows > kGemmShortRows && WT == Q4) goc(k_gemm_qh<WT, 2, 4, 4, 2, true, 4>, 2, 4);
             else if (wide || tall || n_rows > kGemmShortRows || nb % 8)
                 goc(k_gemm_qh<WT, 4, 4, 4, 2, true, WT == Q4 ? 3 : 1>, 4, 4);
             else goc(k_gemm_qh<WT, 2, 4, 8, 2, true>, 2, 4);
