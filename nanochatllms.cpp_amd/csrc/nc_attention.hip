@@ -437,8 +437,33 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_rows(const uint8_t* __res
     if (nch > 1) load_vc<ADT>(vch, vc, v_pitch, kvd, g, 1, m);
     lds_barrier();
 
-    // ---- softmax of row i on wave i % 4: max, expf, sequential sum over
-    // [0, row], divide, requantize in 32-position blocks
+    // ---- softmax of row i: max, expf, sequential sum over [0, row],
+    // divide, requantize in 32-position blocks.  Eight rows: rows w and w + 4
+    // on the two halves of wavefront w (32 positions per half and step), so
+    // their sequential sums run side by side; otherwise row i on wave i % 4.
+    if constexpr (R == 8) {
+        const int hl = lane & 31, i = w + 4 * (lane >> 5);
+        const int n = i < nr ? start + qr0 + i + 1 : 0;  // this half's positions
+        float* Si = S + min(i, R - 1) * mpad;
+        float mx = -INFINITY;
+        for (int c = hl; c < n; c += 32) mx = fmaxf(mx, Si[c]);
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        for (int c = hl; c < n; c += 32) Si[c] = expf_ref(Si[c] - mx);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        const float sum = seq_sum(Si, n);
+        // the trip count is uniform within a half, so each 32-position
+        // block's absmax sees all 32 lanes of its half
+        for (int c0 = 0; c0 < n; c0 += 32) {
+            const int c = c0 + hl;
+            const bool valid = c < n;
+            const float p = valid ? Si[c] / sum : 0.0f;
+            const float pr = act_roundtrip<ADT>(p, valid);
+            if (valid) Si[c] = pr;
+        }
+    } else
     for (int i = w; i < nr; i += kAttnThreads / kWave) {
         const int n = start + qr0 + i + 1;  // positions of this row
         float* Si = S + i * mpad;
