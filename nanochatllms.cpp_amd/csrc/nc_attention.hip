@@ -496,6 +496,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_rows(const uint8_t* __res
 #pragma unroll
     for (int i = 0; i < R; i++) a[i][0] = a[i][1] = 0.0f;
     const int lim_max = min(m, n8);
+    // below the first row's limit every row takes both positions: the
+    // probabilities are read without per-row branches (which would wait for
+    // each read in turn)
+    const int lim_all = min(start + qr0 + 1, n8);
     for (int ch = 0; ch < nch; ch++) {
         const uint8_t* B = Vb + (ch & 1) * (kAvc * VB);
         const int c0 = ch * kAvc;
@@ -503,6 +507,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_rows(const uint8_t* __res
         for (int c8 = c0; c8 < cend; c8 += 8) {
             const int c = c8 + 2 * lp;  // buffer rows past cend exist; the row limits mask them
             const float v0 = v_one<ADT>(B + (c - c0) * VB, j), v1 = v_one<ADT>(B + (c + 1 - c0) * VB, j);
+            if (c + 1 < lim_all) {
+                float2 sp[R];
+#pragma unroll
+                for (int i = 0; i < R; i++) sp[i] = *reinterpret_cast<const float2*>(S + i * mpad + c);
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    a[i][0] = sp[i].x * v0 + a[i][0];
+                    a[i][1] = sp[i].y * v1 + a[i][1];
+                }
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const int lim = min(start + qr0 + i + 1, n8);
